@@ -1,0 +1,202 @@
+"""Benchmark of the north-star path on one MI355X.
+
+Workload: DeepSeek-style FP8 MoE expert layer,
+T=4096 tokens, E=256 experts, top-8 routing (Zipf(1.1) skew, softmax,
+renormalised), hidden 7168, expert intermediate 2048, fused gate/up
+7168->4096, SiLU-mul, down 2048->7168; e4m3 weights with fp32 128x128 block
+scales, e4m3 activations with fp32 per-token per-128 scales.  One step is
+one pass of the whole expert layer through the gfx950 packs: device route
+plan -> activation quant -> grouped gate/up GEMM (+SwiGLU*w epilogue) ->
+quant -> grouped down GEMM -> ordered combine.  Inputs are resident in HBM
+before timing starts.
+
+Prints one JSON line.  ``value`` is the layer's TFLOP/s (2*R*(2I*H + H*I)
+FLOP per step, R = T*top_k).  ``roofline`` covers the dominant kernel (the
+grouped gate/up GEMM), timed with HIP events on its launch stream.
+``cpu_baseline`` times the C restatement of the reference's CPU oracle
+(oracle/pih_oracle.c, po_expert_fp8: the per-expert chain) on a bounded
+sample of the same routed rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "TFLOP/s + %MFMA peak, FP8 MoE grouped GEMM; decode GEMV HBM GB/s"
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5033.2  # 256 CU x 2.4 GHz x 8192 dense FP8 FLOP/clk/CU
+
+T, E, TOPK, H, I = 4096, 256, 8, 7168, 2048
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_inputs(torch):
+    from pih_amd import synth
+
+    ids, wts = synth.zipf_router(synth.config_seed(4, 0), T, E, TOPK)
+    x = synth.bf16_normal(synth.config_seed(4, 1), (T, H))
+    dev = torch.device("cuda")
+    # Expert weights: e4m3 codes of N(0, 0.02) values quantised per 128x128
+    # block with fp32 scale amax/448.  Generated on the device (11.3 GB) with
+    # a seeded torch generator: same distribution as synth.fp8_block_weight.
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x50494804)
+
+    def block_weight(rows, cols):
+        w = torch.empty(E, rows, cols, dtype=torch.uint8, device=dev)
+        s = torch.empty(E, rows // 128, cols // 128, dtype=torch.float32, device=dev)
+        for e in range(E):
+            v = torch.randn(rows, cols, device=dev, generator=gen) * 0.02
+            blk = v.view(rows // 128, 128, cols // 128, 128)
+            amax = blk.abs().amax(dim=(1, 3)).clamp_min(1e-12)
+            sc = amax / 448.0
+            q = (blk / sc[:, None, :, None]).clamp(-448.0, 448.0)
+            w[e] = q.view(rows, cols).to(torch.float8_e4m3fn).view(torch.uint8)
+            s[e] = sc
+        return w, s
+
+    w13, s13 = block_weight(2 * I, H)
+    w2, s2 = block_weight(H, I)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return ids, wts, x, t(ids.view(np.int32)), t(wts), t(x.view(np.int16)).view(torch.bfloat16), w13, s13, w2, s2
+
+
+def cpu_baseline(ids, wts, x_bits, budget_s: float = 12.0):
+    """Time po_expert_fp8 (the reference's per-expert CPU chain, restated) on
+    a bounded sample: routed rows of the hottest expert, grown until the
+    sample takes about ``budget_s``.  Returns the CPU TFLOP/s."""
+    import oracle
+    from pih_amd import synth
+
+    threads = int(os.environ.get("PIH_CPU_THREADS", min(16, os.cpu_count() or 1)))
+    oracle.set_threads(threads)
+    offsets, row_token, row_weight, _ = oracle.route_plan(ids, wts, E)
+    counts = np.diff(offsets.astype(np.int64))
+    e = int(np.argmax(counts))
+    b = int(offsets[e])
+    w13, s13 = synth.fp8_block_weight(synth.config_seed(4, 20 + e), 2 * I, H)
+    w2, s2 = synth.fp8_block_weight(synth.config_seed(4, 600 + e), H, I)
+    flop_per_row = 2.0 * (2 * I * H + H * I)
+    rows, elapsed = threads, 0.0
+    while True:
+        xs = np.ascontiguousarray(x_bits[row_token[b:b + rows]])
+        t0 = time.perf_counter()
+        oracle.expert_fp8(xs, row_weight[b:b + rows], H, I, w13, s13, w2, s2)
+        elapsed = time.perf_counter() - t0
+        if elapsed * 2 > budget_s or rows * 2 > int(counts[e]):
+            break
+        rows *= 2
+    return {"value": flop_per_row * rows / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"po_expert_fp8 on {rows} routed rows of expert {e} (gate/up+SiLU-mul+down, fp32 scales), "
+                      f"{elapsed:.2f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU (the north-star path is a single-GPU kernel "
+              "pack); --gpus must be 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from pih_amd import abi
+    from pih_amd.device import engine_stream, flag_value
+    from pih_amd.linear import MoeFp8Layer
+
+    log("generating inputs")
+    ids, wts, x_bits, ids_d, wts_d, x_d, w13, s13, w2, s2 = build_inputs(torch)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    touched = int((counts > 0).sum())
+    R = T * TOPK
+    flop = 2.0 * R * (2 * I * H + H * I)
+    flop_gu = 2.0 * R * 2 * I * H
+    # algorithmic bytes of the gate/up kernel: weights + scales of touched
+    # experts, fp8 activations + scales of all tokens, bf16 mid out
+    bytes_gu = touched * (2 * I * H + (2 * I // 128) * (H // 128) * 4) + T * H + T * (H // 128) * 4 + R * I * 2
+    bytes_layer = (touched * (3 * I * H + ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128)) * 4)
+                   + T * H * 2 + T * H * 2)
+
+    with engine_stream() as s:
+        layer = MoeFp8Layer(w13, s13, w2, s2, T, TOPK, scale_format=abi.SCALE_F32)
+        log("warmup")
+        for _ in range(args.warmup):
+            layer.forward(x_d, ids_d, wts_d)
+        s.synchronize()
+        if flag_value(layer.flag):
+            log(f"device error flag {flag_value(layer.flag):#x}")
+            return 1
+        n_marks = len(MoeFp8Layer.STAGES) + 1
+        marks = [[torch.cuda.Event(enable_timing=True) for _ in range(n_marks)] for _ in range(args.steps)]
+        log(f"timing {args.steps} steps")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            layer.forward(x_d, ids_d, wts_d, marks=marks[i])
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        stage_ms = {name: float(np.mean([m[j].elapsed_time(m[j + 1]) for m in marks]))
+                    for j, name in enumerate(MoeFp8Layer.STAGES)}
+        if flag_value(layer.flag):
+            log(f"device error flag {flag_value(layer.flag):#x}")
+            return 1
+    ms = wall * 1000.0 / args.steps
+    tflops = flop / (ms * 1e-3) / 1e12
+    gu_ms = stage_ms["gate_up"]
+    gu_gbs = bytes_gu / (gu_ms * 1e-3) / 1e9
+    log("stage ms: " + ", ".join(f"{k}={v:.3f}" for k, v in stage_ms.items()))
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline(ids, wts, x_bits)
+
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 acc, fp32 block scales)",
+        "data": "synthetic (seeded router/activations; random-init e4m3 expert weights)",
+        "config": {"workload": "cfg4 FP8 MoE expert layer", "tokens": T, "experts": E, "top_k": TOPK,
+                   "hidden": H, "intermediate": I, "routed_rows": R, "touched_experts": touched,
+                   "parallelism": "single GPU"},
+        "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+        "layer_hbm_gbs": round(bytes_layer / (ms * 1e-3) / 1e9, 1),
+        "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
+        "roofline": {"kernel": "fp8_block_gemm_kernel (MoE gate/up, SwiGLU epilogue)", "bound": "hbm",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": int(bytes_gu), "flop": flop_gu, "ms": round(gu_ms, 4),
+                     "mfma_tflops": round(flop_gu / (gu_ms * 1e-3) / 1e12, 1),
+                     "mfma_frac": round(flop_gu / (gu_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,235 @@
+/* AMD linear-layer Kernel Pack contract (contract id
+ * "pih.amd-linear-kernels.v1"), function-table ABI version 1.
+ *
+ * The entries here have no one-to-one counterpart in the reference's
+ * pih_deepseek_kernels_api_v1 table; each names the reference code whose
+ * work it takes over:
+ *   launch_route_plan      host DeepSeekExpertSubwavePlan::materialize
+ *                          (plugins/model-deepseek-v4-flash/
+ *                          deepseek_expert_subwave_plan.cpp:32-101), moved
+ *                          onto the device (histogram, prefix scan, stable
+ *                          permutation) so no D2H copy or host sort sits
+ *                          between router and experts;
+ *   launch_fp8_quant       fp8_activation_quant (deepseek_kernels_v1.h
+ *                          entry 3) with fp32 or UE8M0 scales, any K%128,
+ *                          optional row gather;
+ *   launch_fp8_gemm        fp8_gemm (entry 4) with fp32 or UE8M0 scales;
+ *   launch_moe_fp8_gemm    the per-expert loop of DeepSeekExpertCudaBackend
+ *                          (plugins/model-deepseek-v4-flash/cuda/
+ *                          deepseek_expert_cuda_backend.cpp:23-103) as ONE
+ *                          grouped launch over every expert's contiguous row
+ *                          segment, FP8 weights with 128x128 block scales,
+ *                          optional fused gate/up SwiGLU*route-weight
+ *                          epilogue;
+ *   launch_moe_mxfp4_gemm  the same over MXFP4 (e2m1 + UE8M0/32) weights
+ *                          (fp4_gemm, entry 10, generalised);
+ *   launch_moe_combine     ordered_expert_accumulate + expert_finalize
+ *                          (entries 12 and 29) for all experts at once, in
+ *                          the same fp32 add order;
+ *   launch_bf16_gemm       GemmPlan::execute (src/backend/cuda/
+ *                          gemm_plan.cpp:169-198): C = A.W^T, bf16 in, fp32
+ *                          accumulate, bf16 or fp32 out;
+ *   launch_w4a16_gemm      pih_qwen_w4a16_gemm_compat_v1 (kernels/cuda/
+ *                          qwen_bf16_primitives.cu:98-149) in the
+ *                          reference's symmetric format and the asymmetric
+ *                          u32-packed format;
+ *   launch_silu_mul, launch_swiglu, launch_mxfp4_decode
+ *                          pih_qwen_silu_mul_bf16_v1, expert/shared SwiGLU
+ *                          (entries 11 and 28), deepseek_mxfp4_decode.
+ *
+ * Conventions are those of the reference's pack tables: one request pointer
+ * in, pih_status_v1 by value out; a NULL request, wrong struct_size or wrong
+ * abi_version gives PIH_STATUS_INVALID_ARGUMENT_V1; tensors are caller-owned
+ * device addresses; stream is a caller-owned hipStream_t and 0 is rejected;
+ * error_flag is a caller-owned device u32 the kernels OR error bits into;
+ * scratch memory is caller-provided (sizes from query_workspace); entries
+ * only enqueue work and never allocate or synchronise the host. */
+#ifndef PIH_CONTRACTS_AMD_LINEAR_KERNELS_V1_H_
+#define PIH_CONTRACTS_AMD_LINEAR_KERNELS_V1_H_
+
+#include <stdint.h>
+
+#include "pih/plugin_sdk/kernel_pack.h"
+#include "pih/plugin_sdk/status.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PIH_AMD_LINEAR_KERNELS_ABI_VERSION_V1 1U
+
+#define PIH_AMD_SCALE_F32_V1 1U   /* fp32 scale values */
+#define PIH_AMD_SCALE_UE8M0_V1 2U /* one byte b, value 2^(b-127) */
+
+#define PIH_AMD_OUTPUT_BF16_V1 1U
+#define PIH_AMD_OUTPUT_F32_V1 2U
+/* Fused gate/up epilogue: the weight holds [2I, K] (gate rows 0..I-1, then
+ * up rows I..2I-1); the output is bf16 [rows, I] with
+ * mid = bf16(silu(min(g,L)) * clamp(u,-L,L) * route_weight[row]) where
+ * g, u are the bf16-rounded GEMM results and L = swiglu_limit (<= 0: no
+ * clamp). */
+#define PIH_AMD_OUTPUT_SWIGLU_BF16_V1 3U
+
+#define PIH_AMD_ACTIVATION_E4M3_V1 1U
+#define PIH_AMD_ACTIVATION_BF16_V1 2U
+
+#define PIH_AMD_W4A16_SYMMETRIC_V1 1U  /* xing-w4a16-sym-g128-v1 */
+#define PIH_AMD_W4A16_ASYMMETRIC_V1 2U /* u32 x8, bf16 scale, int4 zero */
+
+#define PIH_AMD_WORKSPACE_ROUTE_PLAN_V1 1U
+#define PIH_AMD_WORKSPACE_BF16_GEMM_V1 2U
+#define PIH_AMD_WORKSPACE_W4A16_V1 3U
+
+/* Scratch size query (host only; touches no device). */
+typedef struct pih_amd_workspace_query_v1 {
+  uint32_t struct_size, abi_version;
+  uint32_t kind;          /* PIH_AMD_WORKSPACE_* */
+  uint32_t m, n, k;       /* route plan: tokens, top_k, experts */
+  uintptr_t bytes_u64;    /* host address the size is written to */
+} pih_amd_workspace_query_v1;
+
+/* Device route plan. topk_ids u32 [T, top_k], topk_weights f32 [T, top_k]
+ * -> expert_offsets u32 [E+1] (exclusive prefix of per-expert counts),
+ * row_token u32 [T*top_k] and row_weight f32 [T*top_k] in (expert, token)
+ * order, token_rows u32 [T, top_k] (the row of route (t, j); 0xFFFFFFFF for
+ * a rejected route).  Error bits: 1 expert id >= E, 2 expert repeated in a
+ * token, 4 weight non-finite or negative.  top_k <= 32, E <= 1024. */
+typedef struct pih_amd_route_plan_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t topk_ids_u32, topk_weights_f32;
+  uintptr_t expert_offsets_u32, row_token_u32, row_weight_f32, token_rows_u32;
+  uintptr_t workspace;
+  uint64_t workspace_bytes;
+  uintptr_t error_flag_u32, stream;
+  uint32_t token_count, top_k, expert_count;
+} pih_amd_route_plan_launch_v1;
+
+/* bf16 [input_rows, K] -> e4m3 [row_count, K] + scale [row_count, K/128].
+ * row_index_u32 == 0: output row r reads input row r (input_rows ignored);
+ * otherwise input row row_index[r]. */
+typedef struct pih_amd_fp8_quant_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t input_bf16, row_index_u32, output_e4m3, scale;
+  uintptr_t error_flag_u32, stream;
+  uint32_t row_count, logical_k, input_rows, scale_format;
+} pih_amd_fp8_quant_launch_v1;
+
+/* Dense block-scaled FP8 GEMM: out[m,n] = sum_kb (A.W over the block) *
+ * sa[m,kb] * sw[n/128,kb].  Error bits: 1 e4m3 NaN code, 2 UE8M0 0xFF,
+ * 4 non-finite result (element not written). */
+typedef struct pih_amd_fp8_gemm_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t activation_e4m3, activation_scale, weight_e4m3, weight_scale;
+  uintptr_t output, error_flag_u32, stream;
+  uint32_t m, n, k, scale_format, output_type;
+} pih_amd_fp8_gemm_launch_v1;
+
+/* Grouped FP8 GEMM over MoE expert segments.  Logical row r (0 <= r <
+ * expert_offsets[E]) belongs to the expert e with offsets[e] <= r <
+ * offsets[e+1] and reads activation row row_token[r] (row_token == 0:
+ * row r) of activation [activation_rows, K]; weight e4m3 [E, N, K] and
+ * weight_scale [E, N/128, K/128]; output row r.  row_capacity bounds
+ * offsets[E] (the output has row_capacity rows).  row_weight_f32 is read by
+ * the SwiGLU epilogue only (0 = weight 1). */
+typedef struct pih_amd_moe_fp8_gemm_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t activation_e4m3, activation_scale, row_token_u32;
+  uintptr_t weight_e4m3, weight_scale, expert_offsets_u32, row_weight_f32;
+  uintptr_t output, error_flag_u32, stream;
+  uint32_t row_capacity, expert_count, n, k, activation_rows;
+  uint32_t scale_format, output_type;
+  float swiglu_limit;
+} pih_amd_moe_fp8_gemm_launch_v1;
+
+/* Grouped MXFP4-weight GEMM over MoE expert segments: weight e2m1 packed
+ * two per byte, low nibble = even k, [E, N, K/2], UE8M0 scale [E, N, K/32].
+ * Activations e4m3 with UE8M0 scale [rows, K/128], or bf16. */
+typedef struct pih_amd_moe_mxfp4_gemm_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t activation, activation_scale_ue8m0, row_token_u32;
+  uintptr_t packed_weight, weight_scale_ue8m0, expert_offsets_u32, row_weight_f32;
+  uintptr_t output, error_flag_u32, stream;
+  uint32_t row_capacity, expert_count, n, k, activation_rows;
+  uint32_t activation_type, output_type;
+  float swiglu_limit;
+} pih_amd_moe_mxfp4_gemm_launch_v1;
+
+/* out[t, :] = bf16(sum over t's rows in ascending row order of
+ * expert_output[row, :] + shared[t, :]) (shared_bf16 == 0: no shared). */
+typedef struct pih_amd_moe_combine_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t expert_output_bf16, token_rows_u32, shared_bf16, output_bf16;
+  uintptr_t error_flag_u32, stream;
+  uint32_t token_count, top_k, hidden_size, row_count;
+} pih_amd_moe_combine_launch_v1;
+
+/* C[m,n] = A[m,k] . W[n,k]^T (row-major, bf16 in, fp32 accumulate). */
+typedef struct pih_amd_bf16_gemm_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t a_bf16, w_bf16, output, workspace;
+  uint64_t workspace_bytes;
+  uintptr_t stream;
+  uint32_t m, n, k, output_type;
+} pih_amd_bf16_gemm_launch_v1;
+
+/* W4A16: y[m,n] = bf16(sum_k x[m,k] * w[n,k]).
+ * SYMMETRIC: qweight u8 [N, K/2] (low nibble = even k, signed int4 in
+ *   [-7, 7], nibble 8 reserved), scales fp16 [N, K/128], w = q * s.
+ * ASYMMETRIC: qweight u32 [N, K/8] (nibble j of a word = k%8 == j), scales
+ *   bf16 [N, K/128], zeros u32 [N, ceil(K/1024)] (nibble j = group%8 == j),
+ *   w = (q - z) * s.
+ * The error flag takes the first failure's code (compare-and-swap from 0),
+ * with the reference's QwenCudaInvariant numbers
+ * (include/pih/model/qwen3_cuda_invariant.h:20-23): 12 reserved nibble,
+ * 13 scale not finite and positive, 14 non-finite output. */
+typedef struct pih_amd_w4a16_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t input_bf16, qweight, scales, zeros, output_bf16, workspace;
+  uint64_t workspace_bytes;
+  uintptr_t error_flag_u32, stream;
+  uint32_t m, n, k, format;
+} pih_amd_w4a16_launch_v1;
+
+typedef struct pih_amd_silu_mul_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t gate_bf16, up_bf16, output_bf16, stream;
+  uint64_t count;
+} pih_amd_silu_mul_launch_v1;
+
+typedef struct pih_amd_swiglu_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t gate_bf16, up_bf16, route_weights_f32, output_bf16;
+  uintptr_t error_flag_u32, stream;
+  uint32_t rows, cols;
+  float limit;
+} pih_amd_swiglu_launch_v1;
+
+typedef struct pih_amd_mxfp4_decode_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t packed, scales_ue8m0, output_bf16, error_flag_u32, stream;
+  uint32_t rows, k;
+} pih_amd_mxfp4_decode_launch_v1;
+
+typedef struct pih_amd_linear_kernels_api_v1 {
+  uint32_t struct_size;
+  uint32_t contract_version;
+  const pih_kernel_pack_identity_v1* identity;
+  pih_status_v1 (*query_workspace)(const pih_amd_workspace_query_v1*);
+  pih_status_v1 (*launch_route_plan)(const pih_amd_route_plan_launch_v1*);
+  pih_status_v1 (*launch_fp8_quant)(const pih_amd_fp8_quant_launch_v1*);
+  pih_status_v1 (*launch_fp8_gemm)(const pih_amd_fp8_gemm_launch_v1*);
+  pih_status_v1 (*launch_moe_fp8_gemm)(const pih_amd_moe_fp8_gemm_launch_v1*);
+  pih_status_v1 (*launch_moe_mxfp4_gemm)(const pih_amd_moe_mxfp4_gemm_launch_v1*);
+  pih_status_v1 (*launch_moe_combine)(const pih_amd_moe_combine_launch_v1*);
+  pih_status_v1 (*launch_bf16_gemm)(const pih_amd_bf16_gemm_launch_v1*);
+  pih_status_v1 (*launch_w4a16_gemm)(const pih_amd_w4a16_launch_v1*);
+  pih_status_v1 (*launch_silu_mul)(const pih_amd_silu_mul_launch_v1*);
+  pih_status_v1 (*launch_swiglu)(const pih_amd_swiglu_launch_v1*);
+  pih_status_v1 (*launch_mxfp4_decode)(const pih_amd_mxfp4_decode_launch_v1*);
+} pih_amd_linear_kernels_api_v1;
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PIH_CONTRACTS_AMD_LINEAR_KERNELS_V1_H_ */

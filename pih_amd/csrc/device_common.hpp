@@ -1,0 +1,127 @@
+// Device-side helpers shared by every gfx950 kernel of the packs: bf16 and
+// e4m3fn codecs written from the format definitions, wave reductions, and
+// the CDNA4 MFMA operand types.
+//
+// Formats (the reference defines them in include/pih/core/bfloat16.h:13-27
+// and plugins/model-deepseek-v4-flash/deepseek_fp8_activation_codec.cpp:11-51):
+//   bf16   upper half of an IEEE binary32, round-to-nearest-even, NaN kept
+//          quiet with its sign.
+//   e4m3fn 1.4.3, bias 7, no infinities, S.1111.111 is the only NaN, largest
+//          finite magnitude 448, subnormals are multiples of 2^-9.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pih_amd {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+// Error bits OR-ed into the caller's u32 flag.
+constexpr uint32_t kErrCode = 1u;     // invalid code / non-finite input
+constexpr uint32_t kErrScale = 2u;    // scale byte 0xFF or exponent out of range
+constexpr uint32_t kErrNonFinite = 4u;  // non-finite result (not written)
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
+  const uint32_t raw = __float_as_uint(v);
+  if ((raw & 0x7fffffffu) > 0x7f800000u) return (raw >> 16) | 0x0040u;
+  return (raw + 0x7fffu + ((raw >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_round(float v) {
+  return bf16_bits_to_f32(f32_to_bf16_bits(v));
+}
+
+// Nearest finite e4m3fn code with ties to the even code; |v| <= 448 and
+// finite is the caller's contract (every quantizer clamps first).
+__device__ __forceinline__ uint32_t e4m3_encode(float v) {
+  const uint32_t raw = __float_as_uint(v);
+  const uint32_t sign = (raw >> 24) & 0x80u;
+  const uint32_t mag_bits = raw & 0x7fffffffu;
+  if (mag_bits == 0) return sign;
+  const int exp = (int)(mag_bits >> 23) - 127;
+  uint32_t code;
+  if (exp < -6) {
+    // Subnormal grid 2^-9; the scaling by 512 is exact, rintf rounds half to
+    // even.  A result of 8 is the smallest normal code, which is correct.
+    code = (uint32_t)__builtin_rintf(__uint_as_float(mag_bits) * 512.0f);
+  } else {
+    const uint32_t mant = mag_bits & 0x7fffffu;
+    uint32_t q = mant >> 20;
+    const uint32_t rem = mant & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) ++q;
+    int e = exp;
+    if (q == 8u) {
+      q = 0;
+      ++e;
+    }
+    code = ((uint32_t)(e + 7) << 3) | q;
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ float e4m3_decode(uint32_t bits) {
+  const uint32_t e = (bits >> 3) & 0x0fu, m = bits & 7u;
+  const float mag = e == 0 ? (float)m * 0x1p-9f
+                           : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (bits & 0x80u) ? -mag : mag;
+}
+
+// Non-zero when any byte of w is an e4m3fn NaN code (x111 1111).
+__device__ __forceinline__ uint32_t e4m3_nan_bytes(uint32_t w) {
+  return ((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
+}
+
+// e2m1 magnitudes {0, .5, 1, 1.5, 2, 3, 4, 6}, bit 3 is the sign.
+__device__ __forceinline__ float e2m1_decode(uint32_t nib) {
+  const uint32_t m = nib & 7u;
+  // exact: value = m/2 for m < 4, else (m-2) for m in {4,5} -> 2,3 and 4,6.
+  const float mag = m < 4u ? (float)m * 0.5f : (m == 4u ? 2.0f : m == 5u ? 3.0f : m == 6u ? 4.0f : 6.0f);
+  return (nib & 8u) ? -mag : mag;
+}
+
+// 2^e as a float for e in [-126, 127].
+__device__ __forceinline__ float exp2i(int e) {
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// 2^(b-127) for a UE8M0 byte b in [0, 254] (b = 0 is 2^-127, a subnormal).
+__device__ __forceinline__ float ue8m0_value(uint32_t b) {
+  return b == 0 ? 0x1p-127f : __uint_as_float(b << 23);
+}
+
+template <int kWidth>
+__device__ __forceinline__ float reduce_max_xor(float v) {
+#pragma unroll
+  for (int off = kWidth / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWidth));
+  return v;
+}
+
+template <int kWidth>
+__device__ __forceinline__ float reduce_sum_xor(float v) {
+#pragma unroll
+  for (int off = kWidth / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWidth);
+  return v;
+}
+
+// gfx950 has 8 XCDs; workgroups are dealt to them round-robin.  Renumber the
+// grid so that each XCD walks one contiguous range of the logical tile order
+// (neighbouring tiles share operand tiles in that XCD's L2).
+__device__ __forceinline__ uint32_t xcd_chunked_tile(uint32_t bid, uint32_t grid) {
+  constexpr uint32_t kXcd = 8;
+  if (grid % kXcd) return bid;
+  return (bid % kXcd) * (grid / kXcd) + bid / kXcd;
+}
+
+}  // namespace pih_amd

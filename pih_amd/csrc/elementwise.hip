@@ -1,0 +1,128 @@
+// Elementwise kernels of the linear path for gfx950:
+//   SwiGLU   out = bf16(silu(min(g,L)) * clamp(u,-L,L) * w[row]) — the
+//            reference's expert/shared SwiGLU (plugins/kernels/deepseek-v4-
+//            sm89/native/deepseek_expert_swiglu.cu:11-74) with L = 10; L <= 0
+//            gives the plain SiLU-mul used by the BASELINE MoE chain.
+//   SiLU-mul out = bf16((g / (1 + exp(-g))) * u), the Qwen MLP activation
+//            (plugins/model-qwen3/qwen3_cpu_oracle.cpp:114-126).
+//   MXFP4 decode  e2m1 nibble (low nibble = even k) * 2^(scale-127) -> bf16,
+//            one UE8M0 scale per 32 values (reference
+//            kernels/cuda/deepseek_mxfp4_decode.cu:13-73 and
+//            plugins/model-deepseek-v4-flash/deepseek_mxfp4_codec.cpp:9-46).
+//            Every e2m1 value times a power of two in [2^-127, 2^127] is a
+//            bf16 number, so the decode is exact.
+// All arithmetic is fp32 with no contraction (the build passes
+// -ffp-contract=off), in the reference's operation order.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace pih_amd {
+namespace {
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* gate, const uint16_t* up,
+                                                     const float* weights, uint16_t* out,
+                                                     uint32_t* err, uint32_t rows, uint32_t cols,
+                                                     float limit) {
+  const uint64_t total = (uint64_t)rows * cols;
+  uint32_t bad = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t row = (uint32_t)(i / cols);
+    float g = bf16_bits_to_f32(gate[i]);
+    float u = bf16_bits_to_f32(up[i]);
+    const float w = weights ? weights[row] : 1.0f;
+    if (!__builtin_isfinite(g) || !__builtin_isfinite(u) || !__builtin_isfinite(w) || w < 0.0f) {
+      bad |= 1u;
+      continue;
+    }
+    if (limit > 0.0f) {
+      g = fminf(g, limit);
+      u = fminf(fmaxf(u, -limit), limit);
+    }
+    float v = (g / (1.0f + expf(-g))) * u;
+    if (weights) v = v * w;
+    if (!__builtin_isfinite(v)) {
+      bad |= 2u;
+      continue;
+    }
+    out[i] = (uint16_t)f32_to_bf16_bits(v);
+  }
+  if (bad) atomicOr(err, bad);
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate, const uint16_t* up,
+                                                       uint16_t* out, uint64_t count) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const float g = bf16_bits_to_f32(gate[i]);
+    const float u = bf16_bits_to_f32(up[i]);
+    out[i] = (uint16_t)f32_to_bf16_bits((g / (1.0f + expf(-g))) * u);
+  }
+}
+
+__global__ __launch_bounds__(256) void mxfp4_decode_kernel(const uint8_t* packed,
+                                                           const uint8_t* scales, uint16_t* out,
+                                                           uint32_t* err, uint32_t rows,
+                                                           uint32_t k) {
+  const uint64_t pairs = (uint64_t)rows * (k / 2u);
+  uint32_t bad = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pairs;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t row = (uint32_t)(i / (k / 2u)), kp = (uint32_t)(i % (k / 2u));
+    const uint32_t kk = 2u * kp;
+    const uint8_t s = scales[(uint64_t)row * (k / 32u) + kk / 32u];
+    if (s == 0xffu) {
+      bad |= 2u;
+      continue;
+    }
+    const uint8_t b = packed[i];
+    const float sc = ue8m0_value(s);
+    const float lo = e2m1_decode(b & 0xfu) * sc;
+    const float hi = e2m1_decode(b >> 4) * sc;
+    const uint32_t o = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    reinterpret_cast<uint32_t*>(out)[i] = o;
+  }
+  if (bad) atomicOr(err, bad);
+}
+
+uint32_t grid_for(uint64_t items) {
+  uint64_t b = (items + 255) / 256;
+  if (b == 0) b = 1;
+  return (uint32_t)(b > 16384 ? 16384 : b);
+}
+
+}  // namespace
+
+St LaunchSwiGlu(const SwiGluArgs& a) {
+  if (!a.gate || !a.up || !a.out || !a.error_flag || !a.stream) return Invalid("swiglu_null_argument");
+  if (a.rows == 0 || a.cols == 0) return Invalid("swiglu_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for((uint64_t)a.rows * a.cols)), dim3(256), 0,
+                     a.stream, a.gate, a.up, a.weights, a.out, a.error_flag, a.rows, a.cols,
+                     a.limit);
+  return AfterLaunch("swiglu_launch_failed");
+}
+
+St LaunchSiluMul(const SiluMulArgs& a) {
+  if (!a.gate || !a.up || !a.out || !a.stream) return Invalid("silu_mul_null_argument");
+  if (a.count == 0) return Invalid("silu_mul_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(a.count)), dim3(256), 0, a.stream, a.gate, a.up,
+                     a.out, a.count);
+  return AfterLaunch("silu_mul_launch_failed");
+}
+
+St LaunchMxfp4Decode(const Mxfp4DecodeArgs& a) {
+  if (!a.packed || !a.scales || !a.out || !a.error_flag || !a.stream)
+    return Invalid("mxfp4_decode_null_argument");
+  if (a.rows == 0 || a.k == 0 || a.k % 32u) return Invalid("mxfp4_decode_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(mxfp4_decode_kernel, dim3(grid_for((uint64_t)a.rows * a.k / 2u)), dim3(256), 0,
+                     a.stream, a.packed, a.scales, a.out, a.error_flag, a.rows, a.k);
+  return AfterLaunch("mxfp4_decode_launch_failed");
+}
+
+}  // namespace pih_amd

@@ -1,0 +1,221 @@
+// Internal launcher interface of the gfx950 packs.  Every launcher validates
+// its arguments on the host, enqueues on the caller's stream and returns St;
+// none allocates memory or synchronises the host.  The pack tables
+// (deepseek_pack.cpp, linear_pack.cpp) translate the C-ABI request structs
+// into these calls.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "host_common.hpp"
+
+namespace pih_amd {
+
+enum ScaleFmt : uint32_t { kScaleF32 = 1, kScaleUe8m0 = 2 };
+enum OutKind : uint32_t { kOutBf16 = 1, kOutF32 = 2, kOutSwiGlu = 3 };
+enum ActKind : uint32_t { kActE4m3 = 1, kActBf16 = 2 };
+
+// ------------------------------------------------------------- FP8 quant
+// Per (row, 128 columns): amax -> scale -> e4m3 codes.  kScaleUe8m0 follows
+// the reference codec (deepseek_fp8_activation_codec.cpp:53-107): scale byte
+// e+127 with e the least integer such that max(amax,1e-4) <= 448*2^e.
+// kScaleF32 writes s = max(amax,1e-4)/448.  rows == nullptr reads input row
+// r for output row r; otherwise input row rows[r] (bounded by input_rows).
+struct Fp8QuantArgs {
+  const uint16_t* input = nullptr;
+  const uint32_t* rows = nullptr;
+  uint8_t* codes = nullptr;
+  void* scales = nullptr;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t row_count = 0, k = 0, input_rows = 0;
+  ScaleFmt fmt = kScaleUe8m0;
+};
+St LaunchFp8Quant(const Fp8QuantArgs& a);
+
+// ------------------------------------------------- block-scaled FP8 GEMM
+// out = A . W^T over one or more problems, with one scale per (A row, 128 k)
+// and one per (128 W rows, 128 k), fp32 or UE8M0.  Problems are either
+// strided (dense GEMM, grouped projections) or MoE segments given by
+// device-resident expert offsets.
+struct BlockGemmArgs {
+  const uint8_t* a = nullptr;      // e4m3 [a_rows_total, k]
+  const void* a_scale = nullptr;   // [a_rows_total, k/128]
+  const uint32_t* a_gather = nullptr;  // MoE: logical row -> A row
+  const uint8_t* w = nullptr;      // e4m3 [problems][n][k]
+  const void* w_scale = nullptr;   // [problems][n/128][k/128]
+  void* out = nullptr;
+  const float* row_weight = nullptr;   // SwiGLU epilogue, per logical row
+  const uint32_t* offsets = nullptr;   // MoE: [problems+1] on device
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t m = 0;        // strided: rows per problem; MoE: total rows bound
+  uint32_t n = 0, k = 0; // per-problem weight rows and depth
+  uint32_t problems = 1;
+  uint32_t a_rows_total = 0;
+  // strided addressing: A row = i*a_row_stride + p*a_prob_row,
+  // out element = out[i*out_row_stride + p*out_prob_col + col]
+  uint32_t a_row_stride = 1, a_prob_row = 0;
+  uint64_t out_row_stride = 0;
+  uint32_t out_prob_col = 0;
+  bool moe = false;
+  bool check_codes = false;
+  ScaleFmt scale_fmt = kScaleUe8m0;
+  OutKind out_kind = kOutBf16;
+  float swiglu_limit = 0.0f;  // <= 0: plain SiLU-mul
+  // error bits for: invalid code / A row, UE8M0 0xFF, non-finite result
+  uint32_t err_code_bit = 1u, err_scale_bit = 2u, err_nonfinite_bit = 4u;
+};
+St LaunchFp8BlockGemm(const BlockGemmArgs& a);
+
+// ----------------------------------------------------- MXFP4 weight GEMM
+// out = A . W^T with W e2m1 packed two per byte (low nibble = even k) and a
+// UE8M0 scale per (W row, 32 k).  A is e4m3 with a UE8M0 scale per
+// (row, 128 k) (reference deepseek_fp4_gemm_oracle.cpp:11-91) or bf16.
+struct Fp4GemmArgs {
+  const void* a = nullptr;
+  const uint8_t* a_scale = nullptr;   // e4m3 activations only
+  const uint32_t* a_gather = nullptr;
+  const uint8_t* w = nullptr;         // [problems][n][k/2]
+  const uint8_t* w_scale = nullptr;   // [problems][n][k/32]
+  void* out = nullptr;
+  const float* row_weight = nullptr;
+  const uint32_t* offsets = nullptr;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t m = 0, n = 0, k = 0, problems = 1, a_rows_total = 0;
+  bool moe = false;
+  ActKind act = kActE4m3;
+  OutKind out_kind = kOutBf16;
+  float swiglu_limit = 0.0f;
+};
+St LaunchFp4Gemm(const Fp4GemmArgs& a);
+
+// ------------------------------------------------------------- BF16 GEMM
+// C[m,n] = A[m,k] . W[n,k]^T, fp32 accumulate, bf16 or fp32 out.
+struct Bf16GemmArgs {
+  const uint16_t* a = nullptr;
+  const uint16_t* w = nullptr;
+  void* out = nullptr;
+  void* workspace = nullptr;
+  uint64_t workspace_bytes = 0;
+  hipStream_t stream = nullptr;
+  uint32_t m = 0, n = 0, k = 0;
+  OutKind out_kind = kOutBf16;
+};
+St LaunchBf16Gemm(const Bf16GemmArgs& a);
+uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
+
+// ------------------------------------------------------------- W4A16 GEMV
+struct W4a16Args {
+  const uint16_t* x = nullptr;       // bf16 [m, k]
+  const void* qweight = nullptr;     // asym: u32 [n, k/8]; sym: u8 [n, k/2]
+  const uint16_t* scales = nullptr;  // asym: bf16 [n, k/128]; sym: fp16
+  const uint32_t* zeros = nullptr;   // asym: u32 [n, ceil(k/1024)]
+  uint16_t* out = nullptr;           // bf16 [m, n]
+  void* workspace = nullptr;
+  uint64_t workspace_bytes = 0;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t m = 0, n = 0, k = 0;
+  bool symmetric = false;
+};
+St LaunchW4a16(const W4a16Args& a);
+uint64_t W4a16WorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
+
+// --------------------------------------------------------------- MoE glue
+struct RoutePlanArgs {
+  const uint32_t* topk_ids = nullptr;     // [tokens, topk]
+  const float* topk_weights = nullptr;    // [tokens, topk]
+  uint32_t* expert_offsets = nullptr;     // [experts + 1]
+  uint32_t* row_token = nullptr;          // [tokens * topk]
+  float* row_weight = nullptr;            // [tokens * topk]
+  uint32_t* token_rows = nullptr;         // [tokens * topk]
+  void* workspace = nullptr;
+  uint64_t workspace_bytes = 0;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t tokens = 0, topk = 0, experts = 0;
+};
+St LaunchRoutePlan(const RoutePlanArgs& a);
+uint64_t RoutePlanWorkspaceBytes(uint32_t tokens, uint32_t topk, uint32_t experts);
+
+struct GatherArgs {
+  const uint16_t* source = nullptr;   // bf16 [tokens, hidden]
+  const uint32_t* token_index = nullptr;  // [routes]
+  uint16_t* dest = nullptr;           // bf16 [routes, hidden]
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t routes = 0, tokens = 0, hidden = 0;
+};
+St LaunchRouteGather(const GatherArgs& a);
+
+// Ordered accumulate: acc[token[r], :] += out[r, :] for r in order.
+struct AccumulateArgs {
+  const uint16_t* expert_out = nullptr;  // bf16 [routes, hidden]
+  const uint32_t* token_index = nullptr;
+  float* acc = nullptr;                  // [tokens, hidden]
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t routes = 0, tokens = 0, hidden = 0;
+};
+St LaunchOrderedAccumulate(const AccumulateArgs& a);
+
+// Combine: out[t,:] = bf16(sum over t's rows in ascending row order + shared)
+struct CombineArgs {
+  const uint16_t* expert_out = nullptr;  // bf16 [rows, hidden]
+  const uint32_t* token_rows = nullptr;  // [tokens, topk]
+  const uint16_t* shared = nullptr;      // bf16 [tokens, hidden] or null
+  uint16_t* out = nullptr;               // bf16 [tokens, hidden]
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t tokens = 0, topk = 0, hidden = 0, rows = 0;
+};
+St LaunchMoeCombine(const CombineArgs& a);
+
+struct FinalizeArgs {
+  const float* acc = nullptr;
+  const uint16_t* shared = nullptr;
+  uint16_t* out = nullptr;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint64_t count = 0;
+};
+St LaunchFinalize(const FinalizeArgs& a);
+
+// ------------------------------------------------------------ elementwise
+// out = bf16(silu(min(g,L)) * clamp(u,-L,L) * w[row]) with L <= 0 meaning no
+// clamp and weights == nullptr meaning 1.
+struct SwiGluArgs {
+  const uint16_t* gate = nullptr;
+  const uint16_t* up = nullptr;
+  const float* weights = nullptr;
+  uint16_t* out = nullptr;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t rows = 0, cols = 0;
+  float limit = 0.0f;
+};
+St LaunchSwiGlu(const SwiGluArgs& a);
+
+struct SiluMulArgs {
+  const uint16_t* gate = nullptr;
+  const uint16_t* up = nullptr;
+  uint16_t* out = nullptr;
+  hipStream_t stream = nullptr;
+  uint64_t count = 0;
+};
+St LaunchSiluMul(const SiluMulArgs& a);
+
+struct Mxfp4DecodeArgs {
+  const uint8_t* packed = nullptr;
+  const uint8_t* scales = nullptr;
+  uint16_t* out = nullptr;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t rows = 0, k = 0;
+};
+St LaunchMxfp4Decode(const Mxfp4DecodeArgs& a);
+
+}  // namespace pih_amd

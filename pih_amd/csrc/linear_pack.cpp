@@ -1,0 +1,293 @@
+// gfx950 AMD linear-layer Kernel Pack: identity, the
+// pih_amd_linear_kernels_api_v1 table and the two exported C symbols
+// (the Kernel Pack ABI of include/pih/plugin_sdk/kernel_pack.h, as loaded by
+// the reference's KernelPackLoader, src/microkernel/kernel_pack_loader.cpp:
+// 90-133).  Each entry checks the request header, maps the request onto an
+// internal launcher and returns its status; nothing here allocates or
+// touches a device outside the enqueue.
+#include <hip/hip_runtime.h>
+#include <string.h>
+
+#include "host_common.hpp"
+#include "kernels.hpp"
+#include "pih/contracts/amd_linear_kernels_v1.h"
+
+namespace pih_amd {
+namespace {
+
+constexpr uint32_t kAbi = PIH_AMD_LINEAR_KERNELS_ABI_VERSION_V1;
+
+const pih_kernel_pack_identity_v1 kIdentity = {
+    sizeof(pih_kernel_pack_identity_v1), PIH_KERNEL_PACK_ABI_VERSION_V1,
+    "pih.kernels.amd-linear.gfx950", "1.0.0", "pih.amd-linear-kernels.v1", "gfx950"};
+
+bool ScaleFmtOk(uint32_t f) { return f == PIH_AMD_SCALE_F32_V1 || f == PIH_AMD_SCALE_UE8M0_V1; }
+bool OutOk(uint32_t o) {
+  return o == PIH_AMD_OUTPUT_BF16_V1 || o == PIH_AMD_OUTPUT_F32_V1 || o == PIH_AMD_OUTPUT_SWIGLU_BF16_V1;
+}
+
+St QueryWorkspace(const pih_amd_workspace_query_v1* r) {
+  if (!HeaderOk(r, kAbi) || !r->bytes_u64) return Invalid("workspace_query_invalid");
+  uint64_t bytes;
+  switch (r->kind) {
+    case PIH_AMD_WORKSPACE_ROUTE_PLAN_V1:
+      if (r->m == 0 || r->n == 0 || r->k == 0) return Invalid("workspace_query_shape_invalid");
+      bytes = RoutePlanWorkspaceBytes(r->m, r->n, r->k);
+      break;
+    case PIH_AMD_WORKSPACE_BF16_GEMM_V1:
+      bytes = Bf16GemmWorkspaceBytes(r->m, r->n, r->k);
+      break;
+    case PIH_AMD_WORKSPACE_W4A16_V1:
+      bytes = W4a16WorkspaceBytes(r->m, r->n, r->k);
+      break;
+    default:
+      return Invalid("workspace_query_kind_invalid");
+  }
+  *Ptr<uint64_t>(r->bytes_u64) = bytes;
+  return Ok();
+}
+
+St RoutePlan(const pih_amd_route_plan_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("route_plan_request_invalid");
+  RoutePlanArgs a;
+  a.topk_ids = Ptr<const uint32_t>(r->topk_ids_u32);
+  a.topk_weights = Ptr<const float>(r->topk_weights_f32);
+  a.expert_offsets = Ptr<uint32_t>(r->expert_offsets_u32);
+  a.row_token = Ptr<uint32_t>(r->row_token_u32);
+  a.row_weight = Ptr<float>(r->row_weight_f32);
+  a.token_rows = Ptr<uint32_t>(r->token_rows_u32);
+  a.workspace = Ptr<void>(r->workspace);
+  a.workspace_bytes = r->workspace_bytes;
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.tokens = r->token_count;
+  a.topk = r->top_k;
+  a.experts = r->expert_count;
+  return LaunchRoutePlan(a);
+}
+
+St Fp8Quant(const pih_amd_fp8_quant_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format)) return Invalid("fp8_quant_request_invalid");
+  Fp8QuantArgs a;
+  a.input = Ptr<const uint16_t>(r->input_bf16);
+  a.rows = Ptr<const uint32_t>(r->row_index_u32);
+  a.codes = Ptr<uint8_t>(r->output_e4m3);
+  a.scales = Ptr<void>(r->scale);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.row_count = r->row_count;
+  a.k = r->logical_k;
+  a.input_rows = r->input_rows;
+  a.fmt = (ScaleFmt)r->scale_format;
+  return LaunchFp8Quant(a);
+}
+
+St Fp8Gemm(const pih_amd_fp8_gemm_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format) ||
+      (r->output_type != PIH_AMD_OUTPUT_BF16_V1 && r->output_type != PIH_AMD_OUTPUT_F32_V1))
+    return Invalid("fp8_gemm_request_invalid");
+  BlockGemmArgs a;
+  a.a = Ptr<const uint8_t>(r->activation_e4m3);
+  a.a_scale = Ptr<const void>(r->activation_scale);
+  a.w = Ptr<const uint8_t>(r->weight_e4m3);
+  a.w_scale = Ptr<const void>(r->weight_scale);
+  a.out = Ptr<void>(r->output);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.m = r->m;
+  a.n = r->n;
+  a.k = r->k;
+  a.a_rows_total = r->m;
+  a.scale_fmt = (ScaleFmt)r->scale_format;
+  a.out_kind = (OutKind)r->output_type;
+  a.check_codes = true;
+  return LaunchFp8BlockGemm(a);
+}
+
+St MoeFp8Gemm(const pih_amd_moe_fp8_gemm_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format) || !OutOk(r->output_type))
+    return Invalid("moe_fp8_gemm_request_invalid");
+  if (r->expert_count == 0 || r->row_capacity == 0 || r->activation_rows == 0)
+    return Invalid("moe_fp8_gemm_shape_invalid");
+  BlockGemmArgs a;
+  a.a = Ptr<const uint8_t>(r->activation_e4m3);
+  a.a_scale = Ptr<const void>(r->activation_scale);
+  a.a_gather = Ptr<const uint32_t>(r->row_token_u32);
+  a.w = Ptr<const uint8_t>(r->weight_e4m3);
+  a.w_scale = Ptr<const void>(r->weight_scale);
+  a.offsets = Ptr<const uint32_t>(r->expert_offsets_u32);
+  a.row_weight = Ptr<const float>(r->row_weight_f32);
+  a.out = Ptr<void>(r->output);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.m = r->row_capacity;
+  a.n = r->n;
+  a.k = r->k;
+  a.problems = r->expert_count;
+  a.a_rows_total = r->activation_rows;
+  a.moe = true;
+  a.scale_fmt = (ScaleFmt)r->scale_format;
+  a.out_kind = (OutKind)r->output_type;
+  a.swiglu_limit = r->swiglu_limit;
+  return LaunchFp8BlockGemm(a);
+}
+
+St MoeMxfp4Gemm(const pih_amd_moe_mxfp4_gemm_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) || !OutOk(r->output_type) ||
+      (r->activation_type != PIH_AMD_ACTIVATION_E4M3_V1 &&
+       r->activation_type != PIH_AMD_ACTIVATION_BF16_V1))
+    return Invalid("moe_mxfp4_gemm_request_invalid");
+  if (r->expert_count == 0 || r->row_capacity == 0 || r->activation_rows == 0)
+    return Invalid("moe_mxfp4_gemm_shape_invalid");
+  Fp4GemmArgs a;
+  a.a = Ptr<const void>(r->activation);
+  a.a_scale = Ptr<const uint8_t>(r->activation_scale_ue8m0);
+  a.a_gather = Ptr<const uint32_t>(r->row_token_u32);
+  a.w = Ptr<const uint8_t>(r->packed_weight);
+  a.w_scale = Ptr<const uint8_t>(r->weight_scale_ue8m0);
+  a.offsets = Ptr<const uint32_t>(r->expert_offsets_u32);
+  a.row_weight = Ptr<const float>(r->row_weight_f32);
+  a.out = Ptr<void>(r->output);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.m = r->row_capacity;
+  a.n = r->n;
+  a.k = r->k;
+  a.problems = r->expert_count;
+  a.a_rows_total = r->activation_rows;
+  a.moe = true;
+  a.act = (ActKind)r->activation_type;
+  a.out_kind = (OutKind)r->output_type;
+  a.swiglu_limit = r->swiglu_limit;
+  return LaunchFp4Gemm(a);
+}
+
+St MoeCombine(const pih_amd_moe_combine_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("moe_combine_request_invalid");
+  CombineArgs a;
+  a.expert_out = Ptr<const uint16_t>(r->expert_output_bf16);
+  a.token_rows = Ptr<const uint32_t>(r->token_rows_u32);
+  a.shared = Ptr<const uint16_t>(r->shared_bf16);
+  a.out = Ptr<uint16_t>(r->output_bf16);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.tokens = r->token_count;
+  a.topk = r->top_k;
+  a.hidden = r->hidden_size;
+  a.rows = r->row_count;
+  return LaunchMoeCombine(a);
+}
+
+St Bf16Gemm(const pih_amd_bf16_gemm_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) ||
+      (r->output_type != PIH_AMD_OUTPUT_BF16_V1 && r->output_type != PIH_AMD_OUTPUT_F32_V1))
+    return Invalid("bf16_gemm_request_invalid");
+  Bf16GemmArgs a;
+  a.a = Ptr<const uint16_t>(r->a_bf16);
+  a.w = Ptr<const uint16_t>(r->w_bf16);
+  a.out = Ptr<void>(r->output);
+  a.workspace = Ptr<void>(r->workspace);
+  a.workspace_bytes = r->workspace_bytes;
+  a.stream = AsStream(r->stream);
+  a.m = r->m;
+  a.n = r->n;
+  a.k = r->k;
+  a.out_kind = (OutKind)r->output_type;
+  return LaunchBf16Gemm(a);
+}
+
+St W4a16(const pih_amd_w4a16_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) ||
+      (r->format != PIH_AMD_W4A16_SYMMETRIC_V1 && r->format != PIH_AMD_W4A16_ASYMMETRIC_V1))
+    return Invalid("w4a16_request_invalid");
+  W4a16Args a;
+  a.x = Ptr<const uint16_t>(r->input_bf16);
+  a.qweight = Ptr<const void>(r->qweight);
+  a.scales = Ptr<const uint16_t>(r->scales);
+  a.zeros = Ptr<const uint32_t>(r->zeros);
+  a.out = Ptr<uint16_t>(r->output_bf16);
+  a.workspace = Ptr<void>(r->workspace);
+  a.workspace_bytes = r->workspace_bytes;
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.m = r->m;
+  a.n = r->n;
+  a.k = r->k;
+  a.symmetric = r->format == PIH_AMD_W4A16_SYMMETRIC_V1;
+  return LaunchW4a16(a);
+}
+
+St SiluMul(const pih_amd_silu_mul_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("silu_mul_request_invalid");
+  SiluMulArgs a;
+  a.gate = Ptr<const uint16_t>(r->gate_bf16);
+  a.up = Ptr<const uint16_t>(r->up_bf16);
+  a.out = Ptr<uint16_t>(r->output_bf16);
+  a.stream = AsStream(r->stream);
+  a.count = r->count;
+  return LaunchSiluMul(a);
+}
+
+St SwiGlu(const pih_amd_swiglu_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("swiglu_request_invalid");
+  SwiGluArgs a;
+  a.gate = Ptr<const uint16_t>(r->gate_bf16);
+  a.up = Ptr<const uint16_t>(r->up_bf16);
+  a.weights = Ptr<const float>(r->route_weights_f32);
+  a.out = Ptr<uint16_t>(r->output_bf16);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.rows = r->rows;
+  a.cols = r->cols;
+  a.limit = r->limit;
+  return LaunchSwiGlu(a);
+}
+
+St Mxfp4Decode(const pih_amd_mxfp4_decode_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("mxfp4_decode_request_invalid");
+  Mxfp4DecodeArgs a;
+  a.packed = Ptr<const uint8_t>(r->packed);
+  a.scales = Ptr<const uint8_t>(r->scales_ue8m0);
+  a.out = Ptr<uint16_t>(r->output_bf16);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.rows = r->rows;
+  a.k = r->k;
+  return LaunchMxfp4Decode(a);
+}
+
+PIH_AMD_CONTAINED(CQueryWorkspace, QueryWorkspace, pih_amd_workspace_query_v1)
+PIH_AMD_CONTAINED(CRoutePlan, RoutePlan, pih_amd_route_plan_launch_v1)
+PIH_AMD_CONTAINED(CFp8Quant, Fp8Quant, pih_amd_fp8_quant_launch_v1)
+PIH_AMD_CONTAINED(CFp8Gemm, Fp8Gemm, pih_amd_fp8_gemm_launch_v1)
+PIH_AMD_CONTAINED(CMoeFp8Gemm, MoeFp8Gemm, pih_amd_moe_fp8_gemm_launch_v1)
+PIH_AMD_CONTAINED(CMoeMxfp4Gemm, MoeMxfp4Gemm, pih_amd_moe_mxfp4_gemm_launch_v1)
+PIH_AMD_CONTAINED(CMoeCombine, MoeCombine, pih_amd_moe_combine_launch_v1)
+PIH_AMD_CONTAINED(CBf16Gemm, Bf16Gemm, pih_amd_bf16_gemm_launch_v1)
+PIH_AMD_CONTAINED(CW4a16, W4a16, pih_amd_w4a16_launch_v1)
+PIH_AMD_CONTAINED(CSiluMul, SiluMul, pih_amd_silu_mul_launch_v1)
+PIH_AMD_CONTAINED(CSwiGlu, SwiGlu, pih_amd_swiglu_launch_v1)
+PIH_AMD_CONTAINED(CMxfp4Decode, Mxfp4Decode, pih_amd_mxfp4_decode_launch_v1)
+
+const pih_amd_linear_kernels_api_v1 kContract = {
+    sizeof(pih_amd_linear_kernels_api_v1), kAbi, &kIdentity, &CQueryWorkspace, &CRoutePlan,
+    &CFp8Quant, &CFp8Gemm, &CMoeFp8Gemm, &CMoeMxfp4Gemm, &CMoeCombine, &CBf16Gemm, &CW4a16,
+    &CSiluMul, &CSwiGlu, &CMxfp4Decode};
+
+pih_status_v1 BindOrigin(const char* path) noexcept {
+  return ToAbi(path && path[0] == '/' ? Ok() : Invalid("bind_origin_path_not_absolute"));
+}
+
+const pih_kernel_pack_api_v1 kApi = {sizeof(pih_kernel_pack_api_v1), PIH_KERNEL_PACK_ABI_VERSION_V1,
+                                     &kIdentity, &kContract, &BindOrigin};
+
+}  // namespace
+}  // namespace pih_amd
+
+extern "C" PIH_PLUGIN_EXPORT const pih_kernel_pack_identity_v1* pih_kernel_pack_identity_v1_get(void) {
+  return &pih_amd::kIdentity;
+}
+
+extern "C" PIH_PLUGIN_EXPORT const pih_kernel_pack_api_v1* pih_kernel_pack_api_v1_get(void) {
+  return &pih_amd::kApi;
+}

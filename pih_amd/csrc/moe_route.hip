@@ -1,0 +1,342 @@
+// MoE routing glue for gfx950: the device-side route plan (expert histogram,
+// exclusive prefix scan into expert offsets, stable permutation), the route
+// gather, the ordered expert accumulate, the ordered combine and finalize.
+//
+// Route plan semantics follow the reference's host plan
+// (plugins/model-deepseek-v4-flash/deepseek_expert_subwave_plan.cpp:32-101):
+// routes sorted by (expert, token, ordinal), expert_offsets[e] the exclusive
+// prefix of per-expert route counts (experts+1 entries).  Here the sort is
+// never materialised: a token picks an expert at most once, so a route's
+// place inside its expert segment is the number of earlier tokens that chose
+// the same expert.  Tokens are processed in chunks of 64 (one wave); each
+// chunk builds a 64-bit token mask per expert with LDS atomics (order
+// independent, hence deterministic), one block turns the per-chunk
+// popcounts into chunk bases and expert offsets, and a final pass computes
+// every route's row as offset + chunk base + popcount(mask & lanes_below).
+//
+// Error bits: 1 expert id out of range, 2 expert repeated within a token,
+// 4 route weight non-finite or negative.  An invalid route gets no row
+// (token_rows = 0xffffffff) and is left out of the offsets.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace pih_amd {
+namespace {
+
+constexpr uint32_t kChunk = 64;
+constexpr uint32_t kMaxExperts = 1024;
+constexpr uint32_t kMaxTopk = 32;
+constexpr uint32_t kNoRow = 0xffffffffu;
+
+// Validates route (t, j) and returns its expert or kNoRow.
+__device__ __forceinline__ uint32_t route_expert(const uint32_t* ids, const float* weights,
+                                                 uint32_t t, uint32_t j, uint32_t topk,
+                                                 uint32_t experts, uint32_t& bad) {
+  const uint32_t* row = ids + (uint64_t)t * topk;
+  const uint32_t e = row[j];
+  if (e >= experts) {
+    bad |= 1u;
+    return kNoRow;
+  }
+  for (uint32_t p = 0; p < j; ++p)
+    if (row[p] == e) {
+      bad |= 2u;
+      return kNoRow;
+    }
+  const float w = weights[(uint64_t)t * topk + j];
+  if (!__builtin_isfinite(w) || w < 0.0f) {
+    bad |= 4u;
+    return kNoRow;
+  }
+  return e;
+}
+
+__global__ __launch_bounds__(kChunk) void route_mask_kernel(const uint32_t* ids, const float* weights,
+                                                            unsigned long long* masks,
+                                                            uint32_t* err, uint32_t tokens,
+                                                            uint32_t topk, uint32_t experts) {
+  __shared__ unsigned long long s_mask[kMaxExperts];
+  const uint32_t lane = threadIdx.x, chunk = blockIdx.x;
+  for (uint32_t e = lane; e < experts; e += kChunk) s_mask[e] = 0ull;
+  __syncthreads();
+  const uint32_t t = chunk * kChunk + lane;
+  uint32_t bad = 0;
+  if (t < tokens) {
+    for (uint32_t j = 0; j < topk; ++j) {
+      const uint32_t e = route_expert(ids, weights, t, j, topk, experts, bad);
+      if (e != kNoRow) atomicOr(&s_mask[e], 1ull << lane);
+    }
+  }
+  __syncthreads();
+  for (uint32_t e = lane; e < experts; e += kChunk) masks[(uint64_t)chunk * experts + e] = s_mask[e];
+  if (bad) atomicOr(err, bad);
+}
+
+// One block: per expert, chunk bases by a serial walk over chunks, then a
+// block-wide exclusive scan of the per-expert totals.
+__global__ __launch_bounds__(kMaxExperts) void route_scan_kernel(const unsigned long long* masks,
+                                                                 uint32_t* bases,
+                                                                 uint32_t* offsets,
+                                                                 uint32_t chunks,
+                                                                 uint32_t experts) {
+  __shared__ uint32_t s_scan[kMaxExperts];
+  const uint32_t e = threadIdx.x;
+  uint32_t total = 0;
+  if (e < experts) {
+    for (uint32_t c = 0; c < chunks; ++c) {
+      bases[(uint64_t)c * experts + e] = total;
+      total += (uint32_t)__popcll(masks[(uint64_t)c * experts + e]);
+    }
+  }
+  s_scan[e] = total;
+  __syncthreads();
+  for (uint32_t off = 1; off < blockDim.x; off <<= 1) {
+    const uint32_t v = e >= off ? s_scan[e - off] : 0u;
+    __syncthreads();
+    s_scan[e] += v;
+    __syncthreads();
+  }
+  if (e < experts) offsets[e] = s_scan[e] - total;
+  if (e == experts - 1) offsets[experts] = s_scan[e];
+}
+
+__global__ __launch_bounds__(kChunk) void route_scatter_kernel(
+    const uint32_t* ids, const float* weights, const unsigned long long* masks,
+    const uint32_t* bases, const uint32_t* offsets, uint32_t* row_token, float* row_weight,
+    uint32_t* token_rows, uint32_t tokens, uint32_t topk, uint32_t experts) {
+  const uint32_t lane = threadIdx.x, chunk = blockIdx.x;
+  const uint32_t t = chunk * kChunk + lane;
+  if (t >= tokens) return;
+  const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  uint32_t bad = 0;
+  for (uint32_t j = 0; j < topk; ++j) {
+    const uint32_t e = route_expert(ids, weights, t, j, topk, experts, bad);
+    uint32_t row = kNoRow;
+    if (e != kNoRow) {
+      const unsigned long long m = masks[(uint64_t)chunk * experts + e];
+      row = offsets[e] + bases[(uint64_t)chunk * experts + e] + (uint32_t)__popcll(m & below);
+      row_token[row] = t;
+      row_weight[row] = weights[(uint64_t)t * topk + j];
+    }
+    token_rows[(uint64_t)t * topk + j] = row;
+  }
+}
+
+// dst[r, :] = src[idx[r], :], 16 bytes per lane.
+__global__ __launch_bounds__(256) void gather_kernel(const uint16_t* src, const uint32_t* idx,
+                                                     uint16_t* dst, uint32_t* err, uint32_t routes,
+                                                     uint32_t tokens, uint32_t hidden) {
+  const uint32_t vec = hidden / 8u;
+  const uint64_t total = (uint64_t)routes * vec;
+  uint32_t bad = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t r = (uint32_t)(i / vec), c = (uint32_t)(i % vec);
+    const uint32_t t = idx[r];
+    if (t >= tokens) {
+      bad |= 1u;
+      continue;
+    }
+    reinterpret_cast<uint4*>(dst)[(uint64_t)r * vec + c] =
+        reinterpret_cast<const uint4*>(src)[(uint64_t)t * vec + c];
+  }
+  if (bad) atomicOr(err, bad);
+}
+
+// acc[idx[r], c] += out[r, c]; token indices strictly increasing within one
+// call (reference deepseek_expert_accumulate.cu:13-39), so every (r, c) owns
+// a distinct accumulator element and the sums are order-exact.
+__global__ __launch_bounds__(256) void accumulate_kernel(const uint16_t* out, const uint32_t* idx,
+                                                         float* acc, uint32_t* err,
+                                                         uint32_t routes, uint32_t tokens,
+                                                         uint32_t hidden) {
+  const uint64_t total = (uint64_t)routes * hidden;
+  uint32_t bad = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t r = (uint32_t)(i / hidden), c = (uint32_t)(i % hidden);
+    const uint32_t t = idx[r];
+    if (t >= tokens || (r != 0 && t <= idx[r - 1])) {
+      bad |= 1u;
+      continue;
+    }
+    const float v = bf16_bits_to_f32(out[i]);
+    float* dst = acc + (uint64_t)t * hidden + c;
+    const float next = *dst + v;
+    if (!__builtin_isfinite(v) || !__builtin_isfinite(next)) {
+      bad |= 2u;
+      continue;
+    }
+    *dst = next;
+  }
+  if (bad) atomicOr(err, bad);
+}
+
+// out[t, :] = bf16(sum of t's expert rows in ascending row order (= ascending
+// expert id) + shared).  The fp32 adds run in the order the reference's
+// accumulator oracle applies them (src/model/
+// deepseek_expert_accumulator_oracle.cpp:20-85), so results are bit-exact.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* expert_out,
+                                                      const uint32_t* token_rows,
+                                                      const uint16_t* shared, uint16_t* out,
+                                                      uint32_t* err, uint32_t tokens,
+                                                      uint32_t topk, uint32_t hidden,
+                                                      uint32_t rows) {
+  const uint32_t t = blockIdx.x;
+  if (t >= tokens) return;
+  uint32_t r[kMaxTopk];
+  uint32_t n = 0;
+  for (uint32_t j = 0; j < topk; ++j) {
+    const uint32_t v = token_rows[(uint64_t)t * topk + j];
+    if (v < rows) {
+      uint32_t p = n++;
+      while (p > 0 && r[p - 1] > v) {
+        r[p] = r[p - 1];
+        --p;
+      }
+      r[p] = v;
+    }
+  }
+  uint32_t bad = 0;
+  const uint32_t vec = hidden / 8u;
+  for (uint32_t c = threadIdx.x; c < vec; c += blockDim.x) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (uint32_t j = 0; j < n; ++j) {
+      const uint4 x = reinterpret_cast<const uint4*>(expert_out)[(uint64_t)r[j] * vec + c];
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bf16_bits_to_f32(w[i] & 0xffffu);
+        acc[2 * i + 1] += bf16_bits_to_f32(w[i] >> 16);
+      }
+    }
+    if (shared) {
+      const uint4 x = reinterpret_cast<const uint4*>(shared)[(uint64_t)t * vec + c];
+      const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += bf16_bits_to_f32(w[i] & 0xffffu);
+        acc[2 * i + 1] += bf16_bits_to_f32(w[i] >> 16);
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!__builtin_isfinite(acc[2 * i]) || !__builtin_isfinite(acc[2 * i + 1])) bad |= 4u;
+      o[i] = f32_to_bf16_bits(acc[2 * i]) | (f32_to_bf16_bits(acc[2 * i + 1]) << 16);
+    }
+    reinterpret_cast<uint4*>(out)[(uint64_t)t * vec + c] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (bad) atomicOr(err, bad);
+}
+
+__global__ __launch_bounds__(256) void finalize_kernel(const float* acc, const uint16_t* shared,
+                                                       uint16_t* out, uint32_t* err,
+                                                       uint64_t count) {
+  uint32_t bad = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const float v = acc[i] + (shared ? bf16_bits_to_f32(shared[i]) : 0.0f);
+    if (!__builtin_isfinite(v)) {
+      bad |= 4u;
+      continue;
+    }
+    out[i] = (uint16_t)f32_to_bf16_bits(v);
+  }
+  if (bad) atomicOr(err, bad);
+}
+
+uint32_t grid_for(uint64_t items, uint32_t threads = 256, uint32_t cap = 16384) {
+  uint64_t b = (items + threads - 1) / threads;
+  if (b == 0) b = 1;
+  return (uint32_t)(b > cap ? cap : b);
+}
+
+}  // namespace
+
+uint64_t RoutePlanWorkspaceBytes(uint32_t tokens, uint32_t topk, uint32_t experts) {
+  (void)topk;
+  const uint64_t chunks = (tokens + kChunk - 1) / kChunk;
+  const uint64_t mask_bytes = chunks * experts * 8ull;
+  const uint64_t base_bytes = chunks * experts * 4ull;
+  return ((mask_bytes + 255) / 256) * 256 + base_bytes;
+}
+
+St LaunchRoutePlan(const RoutePlanArgs& a) {
+  if (!a.topk_ids || !a.topk_weights || !a.expert_offsets || !a.row_token || !a.row_weight ||
+      !a.token_rows || !a.workspace || !a.error_flag || !a.stream)
+    return Invalid("route_plan_null_argument");
+  if (a.tokens == 0 || a.topk == 0 || a.topk > kMaxTopk || a.experts == 0 ||
+      a.experts > kMaxExperts || (uint64_t)a.tokens * a.topk > 0x7fffffffull)
+    return Invalid("route_plan_shape_invalid");
+  if (a.workspace_bytes < RoutePlanWorkspaceBytes(a.tokens, a.topk, a.experts))
+    return Invalid("route_plan_workspace_too_small");
+  const uint32_t chunks = (a.tokens + kChunk - 1) / kChunk;
+  const uint64_t mask_bytes = (uint64_t)chunks * a.experts * 8ull;
+  auto* masks = static_cast<unsigned long long*>(a.workspace);
+  auto* bases = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.workspace) +
+                                            ((mask_bytes + 255) / 256) * 256);
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(route_mask_kernel, dim3(chunks), dim3(kChunk), 0, a.stream, a.topk_ids,
+                     a.topk_weights, masks, a.error_flag, a.tokens, a.topk, a.experts);
+  const uint32_t scan_threads = ((a.experts + 63) / 64) * 64;
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(scan_threads), 0, a.stream, masks, bases,
+                     a.expert_offsets, chunks, a.experts);
+  hipLaunchKernelGGL(route_scatter_kernel, dim3(chunks), dim3(kChunk), 0, a.stream, a.topk_ids,
+                     a.topk_weights, masks, bases, a.expert_offsets, a.row_token, a.row_weight,
+                     a.token_rows, a.tokens, a.topk, a.experts);
+  return AfterLaunch("route_plan_launch_failed");
+}
+
+St LaunchRouteGather(const GatherArgs& a) {
+  if (!a.source || !a.token_index || !a.dest || !a.error_flag || !a.stream)
+    return Invalid("route_gather_null_argument");
+  if (a.routes == 0 || a.tokens == 0 || a.hidden == 0 || a.hidden % 8u)
+    return Invalid("route_gather_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(gather_kernel, dim3(grid_for((uint64_t)a.routes * a.hidden / 8u)), dim3(256),
+                     0, a.stream, a.source, a.token_index, a.dest, a.error_flag, a.routes,
+                     a.tokens, a.hidden);
+  return AfterLaunch("route_gather_launch_failed");
+}
+
+St LaunchOrderedAccumulate(const AccumulateArgs& a) {
+  if (!a.expert_out || !a.token_index || !a.acc || !a.error_flag || !a.stream)
+    return Invalid("expert_accumulate_null_argument");
+  if (a.routes == 0 || a.tokens == 0 || a.hidden == 0 || a.routes > a.tokens)
+    return Invalid("expert_accumulate_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(accumulate_kernel, dim3(grid_for((uint64_t)a.routes * a.hidden)), dim3(256), 0,
+                     a.stream, a.expert_out, a.token_index, a.acc, a.error_flag, a.routes,
+                     a.tokens, a.hidden);
+  return AfterLaunch("expert_accumulate_launch_failed");
+}
+
+St LaunchMoeCombine(const CombineArgs& a) {
+  if (!a.expert_out || !a.token_rows || !a.out || !a.error_flag || !a.stream)
+    return Invalid("moe_combine_null_argument");
+  if (a.tokens == 0 || a.topk == 0 || a.topk > kMaxTopk || a.hidden == 0 || a.hidden % 8u ||
+      a.rows == 0)
+    return Invalid("moe_combine_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(combine_kernel, dim3(a.tokens), dim3(256), 0, a.stream, a.expert_out,
+                     a.token_rows, a.shared, a.out, a.error_flag, a.tokens, a.topk, a.hidden,
+                     a.rows);
+  return AfterLaunch("moe_combine_launch_failed");
+}
+
+St LaunchFinalize(const FinalizeArgs& a) {
+  if (!a.acc || !a.out || !a.error_flag || !a.stream) return Invalid("expert_finalize_null_argument");
+  if (a.count == 0) return Invalid("expert_finalize_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  hipLaunchKernelGGL(finalize_kernel, dim3(grid_for(a.count)), dim3(256), 0, a.stream, a.acc,
+                     a.shared, a.out, a.error_flag, a.count);
+  return AfterLaunch("expert_finalize_launch_failed");
+}
+
+}  // namespace pih_amd

@@ -1,0 +1,242 @@
+"""Python-side callers of the gfx950 pack tables (torch tensors in, torch
+tensors out).  Every function goes through the C ABI of the built packs
+(``pih_amd.abi``); there is no fallback: a missing pack or a non-OK status
+raises.
+
+Layouts (row-major):
+  e4m3 codes   uint8 [rows, K], scales fp32 or uint8 (UE8M0) [rows, K/128]
+  FP8 weights  uint8 [E, N, K], scales [E, N/128, K/128]
+  MXFP4        uint8 [E, N, K/2] (low nibble = even k), UE8M0 [E, N, K/32]
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import abi
+from .device import error_flag, ptr, stream_handle
+
+
+class KernelError(RuntimeError):
+    pass
+
+
+def _check(status: abi.Status, what: str) -> None:
+    if status.code != abi.OK:
+        raise KernelError(f"{what}: {status!r}")
+
+
+def _ln():
+    return abi.linear_pack()
+
+
+def _ds():
+    return abi.deepseek_pack()
+
+
+# ------------------------------------------------------------ route plan
+def route_plan_workspace(tokens: int, topk: int, experts: int) -> int:
+    out = (abi.C.c_uint64 * 1)()
+    q = abi.request(abi.LN["workspace_query"], kind=abi.WORKSPACE_ROUTE_PLAN, m=tokens, n=topk, k=experts,
+                    bytes_u64=abi.C.addressof(out))
+    _check(_ln().call("query_workspace", q), "query_workspace")
+    return int(out[0])
+
+
+def route_plan(topk_ids: torch.Tensor, topk_weights: torch.Tensor, experts: int,
+               flag: Optional[torch.Tensor] = None):
+    """Returns (expert_offsets [E+1], row_token [R], row_weight [R],
+    token_rows [T, k], flag)."""
+    tokens, topk = topk_ids.shape
+    dev = topk_ids.device
+    ws = torch.empty(route_plan_workspace(tokens, topk, experts), dtype=torch.uint8, device=dev)
+    offsets = torch.empty(experts + 1, dtype=torch.int32, device=dev)
+    row_token = torch.empty(tokens * topk, dtype=torch.int32, device=dev)
+    row_weight = torch.empty(tokens * topk, dtype=torch.float32, device=dev)
+    token_rows = torch.empty(tokens, topk, dtype=torch.int32, device=dev)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["route_plan"], topk_ids_u32=ptr(topk_ids), topk_weights_f32=ptr(topk_weights),
+                    expert_offsets_u32=ptr(offsets), row_token_u32=ptr(row_token),
+                    row_weight_f32=ptr(row_weight), token_rows_u32=ptr(token_rows), workspace=ptr(ws),
+                    workspace_bytes=ws.numel(), error_flag_u32=ptr(flag), stream=stream_handle(),
+                    token_count=tokens, top_k=topk, expert_count=experts)
+    _check(_ln().call("launch_route_plan", r), "route_plan")
+    return offsets, row_token, row_weight, token_rows, flag
+
+
+# ------------------------------------------------------------- FP8 quant
+def fp8_quant(x: torch.Tensor, scale_format: int, rows: Optional[torch.Tensor] = None,
+              flag: Optional[torch.Tensor] = None):
+    """bf16 [R, K] (or gathered via rows) -> (codes uint8, scales, flag)."""
+    n_out = x.shape[0] if rows is None else rows.numel()
+    k = x.shape[1]
+    codes = torch.empty(n_out, k, dtype=torch.uint8, device=x.device)
+    sdt = torch.float32 if scale_format == abi.SCALE_F32 else torch.uint8
+    scales = torch.empty(n_out, k // 128, dtype=sdt, device=x.device)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["fp8_quant"], input_bf16=ptr(x), row_index_u32=ptr(rows), output_e4m3=ptr(codes),
+                    scale=ptr(scales), error_flag_u32=ptr(flag), stream=stream_handle(), row_count=n_out,
+                    logical_k=k, input_rows=x.shape[0], scale_format=scale_format)
+    _check(_ln().call("launch_fp8_quant", r), "fp8_quant")
+    return codes, scales, flag
+
+
+def fp8_gemm(a, a_scale, w, w_scale, scale_format: int, output_type: int = abi.OUTPUT_BF16,
+             flag: Optional[torch.Tensor] = None):
+    m, k = a.shape
+    n = w.shape[0]
+    out = torch.empty(m, n, dtype=torch.bfloat16 if output_type == abi.OUTPUT_BF16 else torch.float32,
+                      device=a.device)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["fp8_gemm"], activation_e4m3=ptr(a), activation_scale=ptr(a_scale),
+                    weight_e4m3=ptr(w), weight_scale=ptr(w_scale), output=ptr(out), error_flag_u32=ptr(flag),
+                    stream=stream_handle(), m=m, n=n, k=k, scale_format=scale_format, output_type=output_type)
+    _check(_ln().call("launch_fp8_gemm", r), "fp8_gemm")
+    return out, flag
+
+
+def moe_fp8_gemm(a, a_scale, row_token, w, w_scale, offsets, rows: int, scale_format: int,
+                 output_type: int, row_weight=None, swiglu_limit: float = 0.0,
+                 flag: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+    experts, n, k = w.shape
+    ncols = n // 2 if output_type == abi.OUTPUT_SWIGLU_BF16 else n
+    if out is None:
+        out = torch.empty(rows, ncols, dtype=torch.float32 if output_type == abi.OUTPUT_F32 else torch.bfloat16,
+                          device=a.device)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["moe_fp8_gemm"], activation_e4m3=ptr(a), activation_scale=ptr(a_scale),
+                    row_token_u32=ptr(row_token), weight_e4m3=ptr(w), weight_scale=ptr(w_scale),
+                    expert_offsets_u32=ptr(offsets), row_weight_f32=ptr(row_weight), output=ptr(out),
+                    error_flag_u32=ptr(flag), stream=stream_handle(), row_capacity=rows, expert_count=experts,
+                    n=n, k=k, activation_rows=a.shape[0], scale_format=scale_format, output_type=output_type,
+                    swiglu_limit=swiglu_limit)
+    _check(_ln().call("launch_moe_fp8_gemm", r), "moe_fp8_gemm")
+    return out, flag
+
+
+def moe_mxfp4_gemm(a, a_scale, row_token, w_packed, w_scale, offsets, rows: int, activation_type: int,
+                   output_type: int, row_weight=None, swiglu_limit: float = 0.0,
+                   flag: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+    experts, n, k2 = w_packed.shape
+    k = 2 * k2
+    ncols = n // 2 if output_type == abi.OUTPUT_SWIGLU_BF16 else n
+    if out is None:
+        out = torch.empty(rows, ncols, dtype=torch.float32 if output_type == abi.OUTPUT_F32 else torch.bfloat16,
+                          device=w_packed.device)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["moe_mxfp4_gemm"], activation=ptr(a), activation_scale_ue8m0=ptr(a_scale),
+                    row_token_u32=ptr(row_token), packed_weight=ptr(w_packed), weight_scale_ue8m0=ptr(w_scale),
+                    expert_offsets_u32=ptr(offsets), row_weight_f32=ptr(row_weight), output=ptr(out),
+                    error_flag_u32=ptr(flag), stream=stream_handle(), row_capacity=rows, expert_count=experts,
+                    n=n, k=k, activation_rows=a.shape[0], activation_type=activation_type,
+                    output_type=output_type, swiglu_limit=swiglu_limit)
+    _check(_ln().call("launch_moe_mxfp4_gemm", r), "moe_mxfp4_gemm")
+    return out, flag
+
+
+def moe_combine(expert_out, token_rows, shared=None, flag: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None):
+    rows, hidden = expert_out.shape
+    tokens, topk = token_rows.shape
+    if out is None:
+        out = torch.empty(tokens, hidden, dtype=torch.bfloat16, device=expert_out.device)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["moe_combine"], expert_output_bf16=ptr(expert_out), token_rows_u32=ptr(token_rows),
+                    shared_bf16=ptr(shared), output_bf16=ptr(out), error_flag_u32=ptr(flag),
+                    stream=stream_handle(), token_count=tokens, top_k=topk, hidden_size=hidden, row_count=rows)
+    _check(_ln().call("launch_moe_combine", r), "moe_combine")
+    return out, flag
+
+
+class MoeFp8Layer:
+    """The BASELINE FP8 MoE expert layer on device, one launch per stage:
+    route plan -> FP8 quant of the token rows -> grouped gate/up GEMM with
+    the fused SwiGLU * route-weight epilogue -> FP8 quant of the
+    intermediate -> grouped down GEMM -> ordered combine.
+
+    Buffers are allocated once at construction for ``tokens`` x ``topk``
+    routes, so ``forward`` allocates nothing and can be timed or replayed.
+    The stage order and rounding points are those of the reference's
+    routed-expert chain (src/model/deepseek_routed_expert_oracle.cpp:50-95)
+    with fp32 scales and a fused [2I, H] gate/up weight."""
+
+    def __init__(self, w13, w13_scale, w2, w2_scale, tokens: int, topk: int, swiglu_limit: float = 0.0,
+                 scale_format: int = abi.SCALE_F32):
+        self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
+        self.experts, n13, self.hidden = w13.shape
+        self.inter = n13 // 2
+        self.tokens, self.topk = tokens, topk
+        self.rows = tokens * topk
+        self.limit = swiglu_limit
+        self.fmt = scale_format
+        dev = w13.device
+        sdt = torch.float32 if scale_format == abi.SCALE_F32 else torch.uint8
+        self.ws = torch.empty(route_plan_workspace(tokens, topk, self.experts), dtype=torch.uint8, device=dev)
+        self.offsets = torch.empty(self.experts + 1, dtype=torch.int32, device=dev)
+        self.row_token = torch.empty(self.rows, dtype=torch.int32, device=dev)
+        self.row_weight = torch.empty(self.rows, dtype=torch.float32, device=dev)
+        self.token_rows = torch.empty(tokens, topk, dtype=torch.int32, device=dev)
+        self.xq = torch.empty(tokens, self.hidden, dtype=torch.uint8, device=dev)
+        self.xs = torch.empty(tokens, self.hidden // 128, dtype=sdt, device=dev)
+        self.mid = torch.empty(self.rows, self.inter, dtype=torch.bfloat16, device=dev)
+        self.mq = torch.empty(self.rows, self.inter, dtype=torch.uint8, device=dev)
+        self.ms = torch.empty(self.rows, self.inter // 128, dtype=sdt, device=dev)
+        self.y = torch.empty(self.rows, self.hidden, dtype=torch.bfloat16, device=dev)
+        self.out = torch.empty(tokens, self.hidden, dtype=torch.bfloat16, device=dev)
+        self.flag = error_flag()
+
+    STAGES = ("route_plan", "quant_x", "gate_up", "quant_mid", "down", "combine")
+
+    def forward(self, x, topk_ids, topk_weights, shared=None, marks=None):
+        """``marks``: optional list of len(STAGES)+1 events recorded on the
+        launch stream around the stages (for per-kernel timing)."""
+        L = _ln()
+        s = stream_handle()
+        f = ptr(self.flag)
+        mark = (lambda i: marks[i].record()) if marks is not None else (lambda i: None)
+        mark(0)
+        st = L.call("launch_route_plan", abi.request(
+            abi.LN["route_plan"], topk_ids_u32=ptr(topk_ids), topk_weights_f32=ptr(topk_weights),
+            expert_offsets_u32=ptr(self.offsets), row_token_u32=ptr(self.row_token),
+            row_weight_f32=ptr(self.row_weight), token_rows_u32=ptr(self.token_rows), workspace=ptr(self.ws),
+            workspace_bytes=self.ws.numel(), error_flag_u32=f, stream=s, token_count=self.tokens,
+            top_k=self.topk, expert_count=self.experts))
+        _check(st, "route_plan")
+        mark(1)
+        st = L.call("launch_fp8_quant", abi.request(
+            abi.LN["fp8_quant"], input_bf16=ptr(x), row_index_u32=0, output_e4m3=ptr(self.xq), scale=ptr(self.xs),
+            error_flag_u32=f, stream=s, row_count=self.tokens, logical_k=self.hidden, input_rows=self.tokens,
+            scale_format=self.fmt))
+        _check(st, "fp8_quant(x)")
+        mark(2)
+        st = L.call("launch_moe_fp8_gemm", abi.request(
+            abi.LN["moe_fp8_gemm"], activation_e4m3=ptr(self.xq), activation_scale=ptr(self.xs),
+            row_token_u32=ptr(self.row_token), weight_e4m3=ptr(self.w13), weight_scale=ptr(self.w13_scale),
+            expert_offsets_u32=ptr(self.offsets), row_weight_f32=ptr(self.row_weight), output=ptr(self.mid),
+            error_flag_u32=f, stream=s, row_capacity=self.rows, expert_count=self.experts, n=2 * self.inter,
+            k=self.hidden, activation_rows=self.tokens, scale_format=self.fmt,
+            output_type=abi.OUTPUT_SWIGLU_BF16, swiglu_limit=self.limit))
+        _check(st, "moe_fp8_gemm(gate/up)")
+        mark(3)
+        st = L.call("launch_fp8_quant", abi.request(
+            abi.LN["fp8_quant"], input_bf16=ptr(self.mid), row_index_u32=0, output_e4m3=ptr(self.mq),
+            scale=ptr(self.ms), error_flag_u32=f, stream=s, row_count=self.rows, logical_k=self.inter,
+            input_rows=self.rows, scale_format=self.fmt))
+        _check(st, "fp8_quant(mid)")
+        mark(4)
+        st = L.call("launch_moe_fp8_gemm", abi.request(
+            abi.LN["moe_fp8_gemm"], activation_e4m3=ptr(self.mq), activation_scale=ptr(self.ms),
+            row_token_u32=0, weight_e4m3=ptr(self.w2), weight_scale=ptr(self.w2_scale),
+            expert_offsets_u32=ptr(self.offsets), row_weight_f32=0, output=ptr(self.y), error_flag_u32=f,
+            stream=s, row_capacity=self.rows, expert_count=self.experts, n=self.hidden, k=self.inter,
+            activation_rows=self.rows, scale_format=self.fmt, output_type=abi.OUTPUT_BF16, swiglu_limit=0.0))
+        _check(st, "moe_fp8_gemm(down)")
+        mark(5)
+        st = L.call("launch_moe_combine", abi.request(
+            abi.LN["moe_combine"], expert_output_bf16=ptr(self.y), token_rows_u32=ptr(self.token_rows),
+            shared_bf16=ptr(shared), output_bf16=ptr(self.out), error_flag_u32=f, stream=s,
+            token_count=self.tokens, top_k=self.topk, hidden_size=self.hidden, row_count=self.rows))
+        _check(st, "moe_combine")
+        mark(6)
+        return self.out
