@@ -134,9 +134,11 @@ __global__ __launch_bounds__(THREADS, 2) void fp8_block_gemm_kernel(GemmParams p
 
   // A rows this thread stages (r = tid/8 + 32 i) and the row whose scale it
   // stages (r = tid, tid < BM).
-  auto a_source = [&](uint32_t r, bool& ok) -> uint64_t {
-    ok = r < rows;
-    if (!ok) return 0;
+  // Rows past the tile's end (and rejected gather indices) read A row 0:
+  // every load stays unconditional and in bounds, and the rows they feed
+  // are never stored (an output row depends on its own A row only).
+  auto a_source = [&](uint32_t r) -> uint64_t {
+    if (r >= rows) return 0;
     uint64_t src;
     if constexpr (MOE) {
       const uint32_t logical = row0 + r;
@@ -146,21 +148,14 @@ __global__ __launch_bounds__(THREADS, 2) void fp8_block_gemm_kernel(GemmParams p
     }
     if (src >= p.a_rows_total) {
       bad |= kErrCode;
-      ok = false;
       return 0;
     }
     return src;
   };
   const uint8_t* a_ptr[4];
-  bool a_ok[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint64_t src = a_source((tid >> 3) + 32 * i, a_ok[i]);
-    a_ptr[i] = p.a + src * K + col16 * 16;
-  }
-  bool s_ok = false;
-  uint64_t s_src = 0;
-  if (tid < BM) s_src = a_source(tid, s_ok);
+  for (int i = 0; i < 4; ++i) a_ptr[i] = p.a + a_source((tid >> 3) + 32 * i) * K + col16 * 16;
+  const uint64_t s_src = a_source(tid < BM ? tid : 0);
 
   const uint8_t* w_base = p.w + (uint64_t)prob * p.n * K;
   const uint8_t* w_ptr[4];
@@ -188,31 +183,28 @@ __global__ __launch_bounds__(THREADS, 2) void fp8_block_gemm_kernel(GemmParams p
     wblk0 = wblk1 = nt;
   }
 
-  uint4 ra[4], rb[4];
+  v4i ra[4], rb[4];
   uint32_t rsa = 0;
   auto gload = [&](uint32_t kb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      ra[i] = a_ok[i] ? *reinterpret_cast<const uint4*>(a_ptr[i] + (uint64_t)kb * BKB)
-                      : make_uint4(0, 0, 0, 0);
-      rb[i] = *reinterpret_cast<const uint4*>(w_ptr[i] + (uint64_t)kb * BKB);
+      ra[i] = *reinterpret_cast<const v4i*>(a_ptr[i] + (uint64_t)kb * BKB);
+      rb[i] = *reinterpret_cast<const v4i*>(w_ptr[i] + (uint64_t)kb * BKB);
     }
-    if (tid < BM) {
-      if (SCALE == kScaleF32) {
-        rsa = s_ok ? __float_as_uint(static_cast<const float*>(p.a_scale)[s_src * KB + kb]) : 0u;
-      } else {
-        rsa = s_ok ? static_cast<const uint8_t*>(p.a_scale)[s_src * KB + kb] : 127u;
-        if (rsa == 0xffu) bad |= kErrScale;
-      }
+    if (SCALE == kScaleF32) {
+      rsa = __float_as_uint(static_cast<const float*>(p.a_scale)[s_src * KB + kb]);
+    } else {
+      rsa = static_cast<const uint8_t*>(p.a_scale)[s_src * KB + kb];
+      if (rsa == 0xffu && tid < rows) bad |= kErrScale;
     }
     if constexpr (CHECK) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t t = e4m3_nan_bytes(ra[i].x) | e4m3_nan_bytes(ra[i].y) |
-                           e4m3_nan_bytes(ra[i].z) | e4m3_nan_bytes(ra[i].w) |
-                           e4m3_nan_bytes(rb[i].x) | e4m3_nan_bytes(rb[i].y) |
-                           e4m3_nan_bytes(rb[i].z) | e4m3_nan_bytes(rb[i].w);
-        if (t) bad |= kErrCode;
+        const uint32_t ta = e4m3_nan_bytes(ra[i][0]) | e4m3_nan_bytes(ra[i][1]) |
+                            e4m3_nan_bytes(ra[i][2]) | e4m3_nan_bytes(ra[i][3]);
+        const uint32_t tb = e4m3_nan_bytes(rb[i][0]) | e4m3_nan_bytes(rb[i][1]) |
+                            e4m3_nan_bytes(rb[i][2]) | e4m3_nan_bytes(rb[i][3]);
+        if ((ta && (tid >> 3) + 32 * i < rows) || tb) bad |= kErrCode;
       }
     }
   };
@@ -220,8 +212,8 @@ __global__ __launch_bounds__(THREADS, 2) void fp8_block_gemm_kernel(GemmParams p
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t r = (tid >> 3) + 32 * i;
-      *reinterpret_cast<uint4*>(&sA[buf][r * LDS_ROW + col16 * 16]) = ra[i];
-      *reinterpret_cast<uint4*>(&sB[buf][r * LDS_ROW + col16 * 16]) = rb[i];
+      *reinterpret_cast<v4i*>(&sA[buf][r * LDS_ROW + col16 * 16]) = ra[i];
+      *reinterpret_cast<v4i*>(&sB[buf][r * LDS_ROW + col16 * 16]) = rb[i];
     }
     if (tid < BM) sAs[buf][tid] = rsa;
   };
