@@ -35,7 +35,11 @@
  *                          u32-packed format;
  *   launch_silu_mul, launch_swiglu, launch_mxfp4_decode
  *                          pih_qwen_silu_mul_bf16_v1, expert/shared SwiGLU
- *                          (entries 11 and 28), deepseek_mxfp4_decode.
+ *                          (entries 11 and 28), deepseek_mxfp4_decode;
+ *   launch_w4a16_dequant   the INT4 unpack of the W4A16 GEMV on its own
+ *                          (the reference's quantizer format,
+ *                          plugins/offline-qwen/
+ *                          qwen3_int4_reference_quantizer.cpp:30-108).
  *
  * Conventions are those of the reference's pack tables: one request pointer
  * in, pih_status_v1 by value out; a NULL request, wrong struct_size or wrong
@@ -190,6 +194,15 @@ typedef struct pih_amd_w4a16_launch_v1 {
   uint32_t m, n, k, format;
 } pih_amd_w4a16_launch_v1;
 
+/* Exact INT4 dequant, the unpack the W4A16 GEMV applies: output fp32
+ * [N, K] with w = (q - z) * s (ASYMMETRIC) or q * s (SYMMETRIC); same
+ * layouts and error codes as pih_amd_w4a16_launch_v1. */
+typedef struct pih_amd_w4a16_dequant_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t qweight, scales, zeros, output_f32, error_flag_u32, stream;
+  uint32_t n, k, format;
+} pih_amd_w4a16_dequant_launch_v1;
+
 typedef struct pih_amd_silu_mul_launch_v1 {
   uint32_t struct_size, abi_version;
   uintptr_t gate_bf16, up_bf16, output_bf16, stream;
@@ -226,6 +239,7 @@ typedef struct pih_amd_linear_kernels_api_v1 {
   pih_status_v1 (*launch_silu_mul)(const pih_amd_silu_mul_launch_v1*);
   pih_status_v1 (*launch_swiglu)(const pih_amd_swiglu_launch_v1*);
   pih_status_v1 (*launch_mxfp4_decode)(const pih_amd_mxfp4_decode_launch_v1*);
+  pih_status_v1 (*launch_w4a16_dequant)(const pih_amd_w4a16_dequant_launch_v1*);
 } pih_amd_linear_kernels_api_v1;
 
 #ifdef __cplusplus

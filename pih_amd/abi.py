@@ -209,12 +209,14 @@ LN["swiglu"] = _struct("SwiGlu", _hdr(*_u("gate_bf16", "up_bf16", "route_weights
                                           "error_flag_u32", "stream"), *_i("rows", "cols"), ("limit", F32)))
 LN["mxfp4_decode"] = _struct("Mxfp4Decode", _hdr(*_u("packed", "scales_ue8m0", "output_bf16", "error_flag_u32",
                                                      "stream"), *_i("rows", "k")))
+LN["w4a16_dequant"] = _struct("W4a16Dequant", _hdr(*_u("qweight", "scales", "zeros", "output_f32", "error_flag_u32",
+                                                      "stream"), *_i("n", "k", "format")))
 LN_ORDER = [("query_workspace", "workspace_query"), ("launch_route_plan", "route_plan"),
             ("launch_fp8_quant", "fp8_quant"), ("launch_fp8_gemm", "fp8_gemm"),
             ("launch_moe_fp8_gemm", "moe_fp8_gemm"), ("launch_moe_mxfp4_gemm", "moe_mxfp4_gemm"),
             ("launch_moe_combine", "moe_combine"), ("launch_bf16_gemm", "bf16_gemm"),
             ("launch_w4a16_gemm", "w4a16"), ("launch_silu_mul", "silu_mul"), ("launch_swiglu", "swiglu"),
-            ("launch_mxfp4_decode", "mxfp4_decode")]
+            ("launch_mxfp4_decode", "mxfp4_decode"), ("launch_w4a16_dequant", "w4a16_dequant")]
 LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_version", U32),
                                          ("identity", C.POINTER(Identity))] +
                  [(f, C.CFUNCTYPE(Status, C.POINTER(LN[s]))) for f, s in LN_ORDER])
@@ -280,7 +282,10 @@ def load_pack(path: str, contract: str, expected_sha256: Optional[str] = None) -
     unloaded (kernel_pack_loader.cpp:117-119)."""
     path = os.path.abspath(path)
     if path in _loaded:
-        return _loaded[path]
+        pack = _loaded[path]
+        if pack.pack_abi != contract:
+            raise PackError(f"contract mismatch: pack exports {pack.pack_abi!r}, caller wants {contract!r}")
+        return pack
     if not os.path.exists(path):
         raise PackError(f"kernel_pack_load_failed: {path} not built (run __graft_entry__.build())")
     if expected_sha256 is not None:

@@ -1,0 +1,633 @@
+// MFMA GEMM family for gfx950: block-scaled FP8, MXFP4-weight and BF16
+// GEMMs over dense, strided-batched and MoE-segmented problems.
+//
+//   out = A . W^T   (A [rows, K] activations, W [N, K] weights, row-major)
+//
+// Operand kinds (one template instance each):
+//   kFp8     A e4m3, W e4m3, one scale per (A row, 128 k) and per
+//            (128 W rows, 128 k), fp32 or UE8M0
+//            (reference src/model/deepseek_fp8_gemm_oracle.cpp:10-80,
+//            plugins/kernels/deepseek-v4-sm89/native/deepseek_fp8_gemm.cu).
+//            One v_mfma_scale_f32_16x16x128_f8f6f4 covers exactly one
+//            128-deep scale block: UE8M0 scales ride in the instruction's
+//            E8M0 scale operands (hardware applies 2^(sa-127) 2^(sw-127) to
+//            the exact block product); fp32 scales are applied by one FMA per
+//            output and block (DeepSeek-V3 style).
+//   kFp4     A e4m3 + UE8M0 per (row, 128 k); W e2m1 packed two per byte
+//            (low nibble = even k) + UE8M0 per (W row, 32 k)
+//            (reference src/model/deepseek_fp4_gemm_oracle.cpp:11-91).  The
+//            same MX instruction with the B operand in FP4 format and the
+//            lane's own 32-element block scale: the MX-FP4 MFMA of CDNA4.
+//   kBf16    A, W bf16; two v_mfma_f32_16x16x32_bf16 per 64-deep step
+//            (the GemmPlan C = A.W^T of src/backend/cuda/gemm_plan.cpp).
+//   kBf16Fp4 A bf16; W MXFP4 dequantised exactly into bf16 in registers
+//            (every e2m1 value times 2^(s-127) is a bf16 number), then bf16
+//            MFMAs.
+//
+// Tiling: 256 threads = 4 waves, block tile 128 A rows x 128 W rows, each
+// wave 64x64 = 4x4 MFMA 16x16 tiles.  Per K step A and W tiles go through
+// LDS (rows padded by 16 B: the 16 rows one ds_read touches land on distinct
+// banks), double-buffered with one barrier per step, next step prefetched
+// into registers.  Every global load is unconditional and in bounds (rows
+// past a tile's end read row 0 and are never stored).
+//
+// Problems: strided (dense GEMM; the reference's grouped projection whose A
+// rows are t*G+g) or MoE segments from device-resident expert offsets; a
+// MoE tile finds its expert by a block-wide scan of per-expert tile counts.
+// The grid is renumbered so that each XCD walks one contiguous range of
+// tiles (tiles of the same expert and W slice share that XCD's L2).
+//
+// Epilogues: bf16 or fp32 store, or the fused gate/up SwiGLU: the W tile
+// holds 64 gate rows and the 64 matching up rows, so every lane owns a
+// gate/up pair and writes mid = bf16(silu(g') * u' * route_weight) with
+// g, u the bf16-rounded GEMM results (clamped when limit > 0).
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace pih_amd {
+namespace {
+
+enum Kind : int { kFp8 = 0, kFp4 = 1, kBf16 = 2, kBf16Fp4 = 3 };
+
+constexpr int BM = 128, BN = 128, THREADS = 256, A_STEP_BYTES = 128;
+constexpr int LDS_A = A_STEP_BYTES + 16;
+
+template <int KIND>
+struct Traits;
+template <>
+struct Traits<kFp8> {
+  static constexpr int K_STEP = 128, B_STEP_BYTES = 128, A_ELEM = 1;
+};
+template <>
+struct Traits<kFp4> {
+  static constexpr int K_STEP = 128, B_STEP_BYTES = 64, A_ELEM = 1;
+};
+template <>
+struct Traits<kBf16> {
+  static constexpr int K_STEP = 64, B_STEP_BYTES = 128, A_ELEM = 2;
+};
+template <>
+struct Traits<kBf16Fp4> {
+  static constexpr int K_STEP = 64, B_STEP_BYTES = 32, A_ELEM = 2;
+};
+
+struct GemmParams {
+  const uint8_t* a;
+  const void* a_scale;
+  const uint32_t* a_gather;
+  const uint8_t* w;
+  const void* w_scale;
+  void* out;
+  const float* row_weight;
+  const uint32_t* offsets;
+  uint32_t* err;
+  uint32_t m, n, k, problems, a_rows_total;
+  uint32_t a_row_stride, a_prob_row;
+  uint64_t out_row_stride;
+  uint32_t out_prob_col;
+  uint32_t n_tiles, m_tiles_per, tiles_total;
+  float limit;
+  uint32_t err_code, err_scale, err_nonfinite;
+};
+
+// Expert lookup for MoE tile g: returns false when g is past the last tile.
+__device__ bool moe_find_tile(const uint32_t* offsets, uint32_t experts, uint32_t m_bound, uint32_t g,
+                              uint32_t* err, uint32_t err_code, uint32_t& expert, uint32_t& row0,
+                              uint32_t& rows) {
+  __shared__ uint32_t s_scan[THREADS];
+  __shared__ uint32_t s_res[2];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t per = (experts + THREADS - 1) / THREADS;
+  uint32_t cnt = 0;
+  for (uint32_t j = 0; j < per; ++j) {
+    const uint32_t e = tid * per + j;
+    if (e < experts) {
+      const uint32_t lo = offsets[e], hi = offsets[e + 1];
+      cnt += hi > lo ? (hi - lo + BM - 1) / BM : 0;
+    }
+  }
+  if (tid == 0) s_res[0] = 0xffffffffu;
+  s_scan[tid] = cnt;
+  __syncthreads();
+  for (uint32_t off = 1; off < THREADS; off <<= 1) {
+    const uint32_t v = tid >= off ? s_scan[tid - off] : 0u;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  const uint32_t incl = s_scan[tid], excl = incl - cnt;
+  if (g >= excl && g < incl) {
+    uint32_t acc = excl;
+    for (uint32_t j = 0; j < per; ++j) {
+      const uint32_t e = tid * per + j;
+      if (e >= experts) break;
+      const uint32_t lo = offsets[e], hi = offsets[e + 1];
+      const uint32_t t = hi > lo ? (hi - lo + BM - 1) / BM : 0;
+      if (g < acc + t) {
+        s_res[0] = e;
+        s_res[1] = g - acc;
+        break;
+      }
+      acc += t;
+    }
+  }
+  __syncthreads();
+  if (s_res[0] == 0xffffffffu) return false;
+  expert = s_res[0];
+  const uint32_t lo = offsets[expert], hi = offsets[expert + 1];
+  if (hi > m_bound || lo > hi) {
+    if (tid == 0) atomicOr(err, err_code);
+    return false;
+  }
+  row0 = lo + s_res[1] * BM;
+  rows = min((uint32_t)BM, hi - row0);
+  return true;
+}
+
+__device__ __forceinline__ v8i cat8(v4i x, v4i y) {
+  return v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+
+__device__ __forceinline__ uint32_t ff_bytes(uint32_t w) {
+  // non-zero when any byte of w is 0xFF
+  const uint32_t n = ~w;
+  return (n - 0x01010101u) & ~n & 0x80808080u;
+}
+
+// 8 e2m1 nibbles of `w` times 2^(s-127) as 8 bf16 values (exact).
+__device__ __forceinline__ v8s dequant8_fp4(uint32_t w, float scale) {
+  v8s o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float v = e2m1_decode((w >> (4 * j)) & 0xfu) * scale;
+    o[j] = (short)(__float_as_uint(v) >> 16);
+  }
+  return o;
+}
+
+template <int KIND, int SCALE, int OUT, bool MOE, bool CHECK>
+__global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
+  using T = Traits<KIND>;
+  constexpr int B_STEP = T::B_STEP_BYTES;
+  constexpr int LDS_B = B_STEP + 16;
+  constexpr int B_CPR = B_STEP / 16;             // 16-byte chunks per W row per step
+  constexpr int B_LOADS = BN * B_CPR / THREADS;  // per thread
+  constexpr bool FP8A = KIND == kFp8 || KIND == kFp4;
+  constexpr bool BSCALE_ROW = KIND == kFp4 || KIND == kBf16Fp4;  // per-row MX scales
+  constexpr bool ASCALE = KIND == kFp8 || KIND == kFp4;
+  constexpr bool E8M0_A = (KIND == kFp8 && SCALE == kScaleUe8m0) || KIND == kFp4;
+
+  __shared__ __align__(16) uint8_t sA[2][BM * LDS_A];
+  __shared__ __align__(16) uint8_t sB[2][BN * LDS_B];
+  __shared__ __align__(16) uint32_t sAs[2][BM];
+  __shared__ __align__(16) uint32_t sBs[2][BSCALE_ROW ? BN : 1];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wm = wave >> 1, wn = wave & 1, lr = lane & 15, lg = lane >> 4;
+
+  const uint32_t tile = xcd_chunked_tile(blockIdx.x, gridDim.x);
+  if (tile >= p.tiles_total) return;
+  const uint32_t mtot = MOE ? p.tiles_total / p.n_tiles : p.problems * p.m_tiles_per;
+  const uint32_t nt = tile / mtot, g = tile % mtot;
+
+  uint32_t prob, row0, rows;
+  if constexpr (MOE) {
+    if (!moe_find_tile(p.offsets, p.problems, p.m, g, p.err, p.err_code, prob, row0, rows)) return;
+  } else {
+    prob = g / p.m_tiles_per;
+    row0 = (g % p.m_tiles_per) * BM;
+    rows = min((uint32_t)BM, p.m - row0);
+  }
+
+  const uint32_t K = p.k, KB = K / T::K_STEP;
+  const uint64_t a_row_bytes = (uint64_t)K * T::A_ELEM;
+  const uint64_t b_row_bytes = (uint64_t)K * B_STEP / T::K_STEP;
+  uint32_t bad = 0;
+
+  // Rows past the tile's end (and rejected gather indices) read A row 0:
+  // loads stay unconditional and in bounds, and the output rows they feed
+  // are never stored (an output row depends on its own A row only).
+  auto a_source = [&](uint32_t r) -> uint64_t {
+    if (r >= rows) return 0;
+    uint64_t src;
+    if constexpr (MOE) {
+      const uint32_t logical = row0 + r;
+      src = p.a_gather ? p.a_gather[logical] : logical;
+    } else {
+      src = (uint64_t)(row0 + r) * p.a_row_stride + (uint64_t)prob * p.a_prob_row;
+    }
+    if (src >= p.a_rows_total) {
+      bad |= kErrCode;
+      return 0;
+    }
+    return src;
+  };
+  const uint32_t a_col = tid & 7;
+  const uint8_t* a_ptr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a_ptr[i] = p.a + a_source((tid >> 3) + 32 * i) * a_row_bytes + a_col * 16;
+  const uint64_t s_src = a_source(tid < BM ? tid : 0);
+
+  // W rows this thread stages; for the SwiGLU epilogue the tile's 128 rows
+  // are 64 gate rows and the 64 matching up rows, arranged so that each
+  // wave's MFMA columns pair gate (ns = 0,1) with up (ns = 2,3).
+  auto w_row = [&](uint32_t r) -> uint32_t {
+    if constexpr (OUT == kOutSwiGlu) {
+      const uint32_t half = r >> 6, j = (r & 63) >> 4, rr = r & 15;
+      const uint32_t base = nt * 64 + half * 32 + (j & 1) * 16 + rr;
+      return j < 2 ? base : p.n / 2 + base;
+    } else {
+      return nt * BN + r;
+    }
+  };
+  const uint8_t* w_base = p.w + (uint64_t)prob * p.n * b_row_bytes;
+  const uint8_t* w_ptr[B_LOADS];
+#pragma unroll
+  for (int i = 0; i < B_LOADS; ++i) {
+    const uint32_t c = tid + THREADS * i;
+    w_ptr[i] = w_base + (uint64_t)w_row(c / B_CPR) * b_row_bytes + (c % B_CPR) * 16;
+  }
+  // per-row MX scale words (kFp4: 4 bytes per 128-deep step; kBf16Fp4: 2)
+  const uint8_t* ws_row = nullptr;
+  if constexpr (BSCALE_ROW)
+    ws_row = static_cast<const uint8_t*>(p.w_scale) +
+             ((uint64_t)prob * p.n + w_row(tid < BN ? tid : 0)) * (K / 32);
+  // FP8 block scales (128-row blocks) used by this tile
+  const uint64_t ws_prob = (uint64_t)prob * (p.n / 128) * (K / 128);
+  uint32_t wblk0 = nt, wblk1 = nt;
+  if constexpr (OUT == kOutSwiGlu) {
+    wblk0 = (nt * 64) / 128;
+    wblk1 = (p.n / 2 + nt * 64) / 128;
+  }
+
+  v4i ra[4], rb[B_LOADS];
+  uint32_t rsa = 0, rsb = 0;
+  auto gload = [&](uint32_t kb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const v4i*>(a_ptr[i] + (uint64_t)kb * A_STEP_BYTES);
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) rb[i] = *reinterpret_cast<const v4i*>(w_ptr[i] + (uint64_t)kb * B_STEP);
+    if constexpr (ASCALE) {
+      if constexpr (E8M0_A) {
+        rsa = static_cast<const uint8_t*>(p.a_scale)[s_src * (K / 128) + kb];
+        if (rsa == 0xffu && tid < rows) bad |= kErrScale;
+      } else {
+        rsa = __float_as_uint(static_cast<const float*>(p.a_scale)[s_src * (K / 128) + kb]);
+      }
+    }
+    if constexpr (KIND == kFp4) {
+      rsb = *reinterpret_cast<const uint32_t*>(ws_row + (uint64_t)kb * 4);
+      if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
+    } else if constexpr (KIND == kBf16Fp4) {
+      rsb = *reinterpret_cast<const uint16_t*>(ws_row + (uint64_t)kb * 2);
+      if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
+    }
+    if constexpr (CHECK && FP8A) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t t = e4m3_nan_bytes(ra[i][0]) | e4m3_nan_bytes(ra[i][1]) | e4m3_nan_bytes(ra[i][2]) |
+                           e4m3_nan_bytes(ra[i][3]);
+        if (t && (tid >> 3) + 32 * i < rows) bad |= kErrCode;
+      }
+      if constexpr (KIND == kFp8) {
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) {
+          const uint32_t t = e4m3_nan_bytes(rb[i][0]) | e4m3_nan_bytes(rb[i][1]) | e4m3_nan_bytes(rb[i][2]) |
+                             e4m3_nan_bytes(rb[i][3]);
+          if (t) bad |= kErrCode;
+        }
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<v4i*>(&sA[buf][((tid >> 3) + 32 * i) * LDS_A + a_col * 16]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+      const uint32_t c = tid + THREADS * i;
+      *reinterpret_cast<v4i*>(&sB[buf][(c / B_CPR) * LDS_B + (c % B_CPR) * 16]) = rb[i];
+    }
+    if constexpr (ASCALE)
+      if (tid < BM) sAs[buf][tid] = rsa;
+    if constexpr (BSCALE_ROW)
+      if (tid < BN) sBs[buf][tid] = rsb;
+  };
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t ms_live = 0;
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms)
+    if (wm * 64 + ms * 16 < rows) ms_live = ms + 1;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  for (uint32_t kb = 0; kb < KB; ++kb) {
+    const int buf = kb & 1;
+    if (kb + 1 < KB) gload(kb + 1);
+
+    uint32_t ws0b = 127, ws1b = 127;
+    float ws0f = 1.0f, ws1f = 1.0f;
+    if constexpr (KIND == kFp8) {
+      if constexpr (SCALE == kScaleF32) {
+        const float* ws = static_cast<const float*>(p.w_scale) + ws_prob;
+        ws0f = ws[(uint64_t)wblk0 * (K / 128) + kb];
+        ws1f = ws[(uint64_t)wblk1 * (K / 128) + kb];
+      } else {
+        const uint8_t* ws = static_cast<const uint8_t*>(p.w_scale) + ws_prob;
+        ws0b = ws[(uint64_t)wblk0 * (K / 128) + kb];
+        ws1b = ws[(uint64_t)wblk1 * (K / 128) + kb];
+        if (ws0b == 0xffu || ws1b == 0xffu) bad |= kErrScale;
+      }
+    }
+
+    if (ms_live) {
+      // W operands for this wave's four 16-column blocks
+      v8i bv[4];
+      uint32_t bsc[4];
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) {
+        const uint32_t brow = wn * 64 + ns * 16 + lr;
+        const uint8_t* pb = &sB[buf][brow * LDS_B];
+        if constexpr (KIND == kFp8 || KIND == kBf16) {
+          bv[ns] = cat8(*reinterpret_cast<const v4i*>(pb + lg * 32),
+                        *reinterpret_cast<const v4i*>(pb + lg * 32 + 16));
+        } else if constexpr (KIND == kFp4) {
+          bv[ns] = cat8(*reinterpret_cast<const v4i*>(pb + lg * 16), v4i{0, 0, 0, 0});
+          bsc[ns] = (sBs[buf][brow] >> (8 * lg)) & 0xffu;
+        } else {  // kBf16Fp4: 16 nibbles = k 16*lg .. 16*lg+15 of the step
+          const uint2 w2 = *reinterpret_cast<const uint2*>(pb + lg * 8);
+          const float sc = ue8m0_value((sBs[buf][brow] >> (8 * (lg >> 1))) & 0xffu);
+          const v8s lo = dequant8_fp4(w2.x, sc), hi = dequant8_fp4(w2.y, sc);
+          bv[ns] = cat8(__builtin_bit_cast(v4i, lo), __builtin_bit_cast(v4i, hi));
+        }
+      }
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) {
+        if (ms >= (int)ms_live) break;
+        const uint32_t arow = wm * 64 + ms * 16 + lr;
+        const uint8_t* pa = &sA[buf][arow * LDS_A + lg * 32];
+        const v4i a0 = *reinterpret_cast<const v4i*>(pa);
+        const v4i a1 = *reinterpret_cast<const v4i*>(pa + 16);
+        if constexpr (KIND == kFp8 && SCALE == kScaleF32) {
+          const v4i s4 = *reinterpret_cast<const v4i*>(&sAs[buf][wm * 64 + ms * 16 + 4 * lg]);
+          const v8i av = cat8(a0, a1);
+#pragma unroll
+          for (int ns = 0; ns < 4; ++ns) {
+            const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv[ns], v4f{0.f, 0.f, 0.f, 0.f},
+                                                                           0, 0, 0, 127, 0, 127);
+            const float wsv = (OUT == kOutSwiGlu && ns >= 2) ? ws1f : ws0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              acc[ms][ns][i] = __builtin_fmaf(t[i], __uint_as_float((uint32_t)s4[i]) * wsv, acc[ms][ns][i]);
+          }
+        } else if constexpr (KIND == kFp8) {
+          const int sab = (int)sAs[buf][arow];
+          const v8i av = cat8(a0, a1);
+#pragma unroll
+          for (int ns = 0; ns < 4; ++ns) {
+            const int wsb = (int)((OUT == kOutSwiGlu && ns >= 2) ? ws1b : ws0b);
+            acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv[ns], acc[ms][ns], 0, 0, 0, sab,
+                                                                           0, wsb);
+          }
+        } else if constexpr (KIND == kFp4) {
+          const int sab = (int)sAs[buf][arow];
+          const v8i av = cat8(a0, a1);
+#pragma unroll
+          for (int ns = 0; ns < 4; ++ns)
+            acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv[ns], acc[ms][ns], 0, 4, 0, sab,
+                                                                           0, (int)bsc[ns]);
+        } else {  // bf16 A: 16 k per lane = two 16x16x32 MFMAs
+#pragma unroll
+          for (int ns = 0; ns < 4; ++ns) {
+            const v4i b0 = v4i{bv[ns][0], bv[ns][1], bv[ns][2], bv[ns][3]};
+            const v4i b1 = v4i{bv[ns][4], bv[ns][5], bv[ns][6], bv[ns][7]};
+            acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(v8bf, a0), __builtin_bit_cast(v8bf, b0), acc[ms][ns], 0, 0, 0);
+            acc[ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(v8bf, a1), __builtin_bit_cast(v8bf, b1), acc[ms][ns], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (kb + 1 < KB) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = wm * 64 + ms * 16 + 4 * lg + i;
+      if (r >= rows) continue;
+      uint64_t orow;
+      if constexpr (MOE) {
+        orow = (uint64_t)(row0 + r) * p.out_row_stride;
+      } else {
+        orow = (uint64_t)(row0 + r) * p.out_row_stride + (uint64_t)prob * p.out_prob_col;
+      }
+      if constexpr (OUT == kOutSwiGlu) {
+        const float rw = p.row_weight ? p.row_weight[row0 + r] : 1.0f;
+#pragma unroll
+        for (int ns = 0; ns < 2; ++ns) {
+          float gt = bf16_round(acc[ms][ns][i]);
+          float up = bf16_round(acc[ms][ns + 2][i]);
+          if (!__builtin_isfinite(gt) || !__builtin_isfinite(up)) {
+            bad |= kErrNonFinite;
+            continue;
+          }
+          if (p.limit > 0.0f) {
+            gt = fminf(gt, p.limit);
+            up = fminf(fmaxf(up, -p.limit), p.limit);
+          }
+          float v = (gt / (1.0f + expf(-gt))) * up;
+          v = v * rw;
+          if (!__builtin_isfinite(v)) {
+            bad |= kErrNonFinite;
+            continue;
+          }
+          const uint32_t col = nt * 64 + wn * 32 + ns * 16 + lr;
+          static_cast<uint16_t*>(p.out)[orow + col] = (uint16_t)f32_to_bf16_bits(v);
+        }
+      } else {
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) {
+          const float v = acc[ms][ns][i];
+          if (!__builtin_isfinite(v) && p.err_nonfinite) {
+            bad |= kErrNonFinite;
+            continue;
+          }
+          const uint32_t col = nt * BN + wn * 64 + ns * 16 + lr;
+          if constexpr (OUT == kOutF32) {
+            static_cast<float*>(p.out)[orow + col] = v;
+          } else {
+            static_cast<uint16_t*>(p.out)[orow + col] = (uint16_t)f32_to_bf16_bits(v);
+          }
+        }
+      }
+    }
+  }
+  if (bad) {
+    const uint32_t bits = ((bad & kErrCode) ? p.err_code : 0u) | ((bad & kErrScale) ? p.err_scale : 0u) |
+                          ((bad & kErrNonFinite) ? p.err_nonfinite : 0u);
+    if (bits) atomicOr(p.err, bits);
+  }
+}
+
+template <int KIND, int SCALE, int OUT, bool MOE, bool CHECK>
+void launch_one(const GemmParams& gp, uint32_t grid, hipStream_t s) {
+  hipLaunchKernelGGL((mfma_gemm_kernel<KIND, SCALE, OUT, MOE, CHECK>), dim3(grid), dim3(THREADS), 0, s, gp);
+}
+
+template <int KIND, int SCALE, int OUT>
+void dispatch_mc(const GemmParams& gp, uint32_t grid, hipStream_t s, bool moe, bool check) {
+  if (moe) {
+    if (check) launch_one<KIND, SCALE, OUT, true, true>(gp, grid, s);
+    else launch_one<KIND, SCALE, OUT, true, false>(gp, grid, s);
+  } else {
+    if (check) launch_one<KIND, SCALE, OUT, false, true>(gp, grid, s);
+    else launch_one<KIND, SCALE, OUT, false, false>(gp, grid, s);
+  }
+}
+
+template <int KIND, int SCALE>
+void dispatch_out(const GemmParams& gp, uint32_t grid, hipStream_t s, OutKind out, bool moe, bool check) {
+  if (out == kOutBf16) dispatch_mc<KIND, SCALE, kOutBf16>(gp, grid, s, moe, check);
+  else if (out == kOutF32) dispatch_mc<KIND, SCALE, kOutF32>(gp, grid, s, moe, check);
+  else dispatch_mc<KIND, SCALE, kOutSwiGlu>(gp, grid, s, moe, check);
+}
+
+// Shared host setup: tile counts, grid, common fields.
+St prepare(GemmParams& gp, uint32_t& grid, uint32_t m, uint32_t n, uint32_t k, uint32_t problems, bool moe,
+           OutKind out, uint64_t out_row_stride) {
+  gp.m = m;
+  gp.n = n;
+  gp.k = k;
+  gp.problems = problems;
+  gp.n_tiles = n / BN;
+  gp.out_row_stride = out_row_stride ? out_row_stride : (out == kOutSwiGlu ? n / 2 : n);
+  uint64_t mt;
+  if (moe) {
+    // sum_e ceil(rows_e/BM) <= rows/BM + (number of non-empty experts)
+    mt = (uint64_t)m / BM + (problems < m ? problems : m);
+    gp.m_tiles_per = 0;
+  } else {
+    gp.m_tiles_per = (m + BM - 1) / BM;
+    mt = (uint64_t)gp.m_tiles_per * problems;
+  }
+  const uint64_t total = mt * gp.n_tiles;
+  if (total == 0 || total > 0x7fffffffull - 8) return Invalid("gemm_grid_too_large");
+  gp.tiles_total = (uint32_t)total;
+  grid = (uint32_t)((total + 7) / 8 * 8);
+  return RequireCleanLastError();
+}
+
+}  // namespace
+
+St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
+  if (!a.a || !a.a_scale || !a.w || !a.w_scale || !a.out || !a.error_flag || !a.stream)
+    return Invalid("fp8_gemm_null_argument");
+  if (a.k == 0 || a.k % 128 || a.n == 0 || a.n % 128 || a.problems == 0 || a.m == 0)
+    return Invalid("fp8_gemm_shape_invalid");
+  if (a.out_kind == kOutSwiGlu && (a.n % 256)) return Invalid("fp8_gemm_swiglu_shape_invalid");
+  if (a.scale_fmt != kScaleF32 && a.scale_fmt != kScaleUe8m0) return Invalid("fp8_gemm_scale_format_invalid");
+  if (a.out_kind != kOutBf16 && a.out_kind != kOutF32 && a.out_kind != kOutSwiGlu)
+    return Invalid("fp8_gemm_output_type_invalid");
+  if (a.moe && !a.offsets) return Invalid("fp8_gemm_offsets_missing");
+  if (a.a_rows_total == 0) return Invalid("fp8_gemm_a_rows_invalid");
+  GemmParams gp{};
+  gp.a = a.a;
+  gp.a_scale = a.a_scale;
+  gp.a_gather = a.a_gather;
+  gp.w = a.w;
+  gp.w_scale = a.w_scale;
+  gp.out = a.out;
+  gp.row_weight = a.row_weight;
+  gp.offsets = a.offsets;
+  gp.err = a.error_flag;
+  gp.a_rows_total = a.a_rows_total;
+  gp.a_row_stride = a.a_row_stride;
+  gp.a_prob_row = a.a_prob_row;
+  gp.out_prob_col = a.out_prob_col;
+  gp.limit = a.swiglu_limit;
+  gp.err_code = a.err_code_bit;
+  gp.err_scale = a.err_scale_bit;
+  gp.err_nonfinite = a.err_nonfinite_bit;
+  uint32_t grid;
+  St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, a.out_row_stride);
+  if (!s.ok()) return s;
+  if (a.scale_fmt == kScaleF32) dispatch_out<kFp8, kScaleF32>(gp, grid, a.stream, a.out_kind, a.moe, a.check_codes);
+  else dispatch_out<kFp8, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, a.check_codes);
+  return AfterLaunch("fp8_gemm_launch_failed");
+}
+
+St LaunchFp4Gemm(const Fp4GemmArgs& a) {
+  if (!a.a || !a.w || !a.w_scale || !a.out || !a.error_flag || !a.stream) return Invalid("fp4_gemm_null_argument");
+  if (a.act == kActE4m3 && !a.a_scale) return Invalid("fp4_gemm_null_argument");
+  if (a.k == 0 || a.k % 128 || a.n == 0 || a.n % 128 || a.problems == 0 || a.m == 0)
+    return Invalid("fp4_gemm_shape_invalid");
+  if (a.out_kind == kOutSwiGlu && (a.n % 256)) return Invalid("fp4_gemm_swiglu_shape_invalid");
+  if (a.out_kind != kOutBf16 && a.out_kind != kOutF32 && a.out_kind != kOutSwiGlu)
+    return Invalid("fp4_gemm_output_type_invalid");
+  if (a.act != kActE4m3 && a.act != kActBf16) return Invalid("fp4_gemm_activation_type_invalid");
+  if (a.moe && !a.offsets) return Invalid("fp4_gemm_offsets_missing");
+  if (a.a_rows_total == 0) return Invalid("fp4_gemm_a_rows_invalid");
+  GemmParams gp{};
+  gp.a = static_cast<const uint8_t*>(a.a);
+  gp.a_scale = a.a_scale;
+  gp.a_gather = a.a_gather;
+  gp.w = a.w;
+  gp.w_scale = a.w_scale;
+  gp.out = a.out;
+  gp.row_weight = a.row_weight;
+  gp.offsets = a.offsets;
+  gp.err = a.error_flag;
+  gp.a_rows_total = a.a_rows_total;
+  gp.a_row_stride = 1;
+  gp.limit = a.swiglu_limit;
+  gp.err_code = 1u;
+  gp.err_scale = 2u;
+  gp.err_nonfinite = 4u;
+  uint32_t grid;
+  St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, 0);
+  if (!s.ok()) return s;
+  if (a.act == kActE4m3) dispatch_out<kFp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, !a.moe);
+  else dispatch_out<kBf16Fp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, false);
+  return AfterLaunch("fp4_gemm_launch_failed");
+}
+
+St LaunchBf16Gemm(const Bf16GemmArgs& a) {
+  if (!a.a || !a.w || !a.out || !a.stream) return Invalid("bf16_gemm_null_argument");
+  if (a.m == 0 || a.n == 0 || a.k == 0) return Invalid("bf16_gemm_shape_invalid");
+  if (a.out_kind != kOutBf16 && a.out_kind != kOutF32) return Invalid("bf16_gemm_output_type_invalid");
+  if (a.m <= 64) return LaunchBf16Gemv(a);
+  if (a.n % 128 || a.k % 64) return Invalid("bf16_gemm_shape_invalid");
+  GemmParams gp{};
+  gp.a = reinterpret_cast<const uint8_t*>(a.a);
+  gp.w = reinterpret_cast<const uint8_t*>(a.w);
+  gp.out = a.out;
+  gp.a_rows_total = a.m;
+  gp.a_row_stride = 1;
+  uint32_t grid;
+  St s = prepare(gp, grid, a.m, a.n, a.k, 1, false, a.out_kind, 0);
+  if (!s.ok()) return s;
+  // no error flag in the GemmPlan contract: nothing for the kernel to report
+  gp.err = nullptr;
+  if (a.out_kind == kOutBf16) launch_one<kBf16, kScaleUe8m0, kOutBf16, false, false>(gp, grid, a.stream);
+  else launch_one<kBf16, kScaleUe8m0, kOutF32, false, false>(gp, grid, a.stream);
+  return AfterLaunch("bf16_gemm_launch_failed");
+}
+
+uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k) {
+  return m <= 64 ? Bf16GemvWorkspaceBytes(m, n, k) : 0;
+}
+
+}  // namespace pih_amd

@@ -106,6 +106,9 @@ struct Bf16GemmArgs {
 };
 St LaunchBf16Gemm(const Bf16GemmArgs& a);
 uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
+// decode shapes (m <= 64): the weight-streaming GEMV with split-K
+St LaunchBf16Gemv(const Bf16GemmArgs& a);
+uint64_t Bf16GemvWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
 
 // ------------------------------------------------------------- W4A16 GEMV
 struct W4a16Args {
@@ -123,6 +126,8 @@ struct W4a16Args {
 };
 St LaunchW4a16(const W4a16Args& a);
 uint64_t W4a16WorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
+// exact dequant (q - z) * s (or q * s) to fp32 [n, k]
+St LaunchW4a16Dequant(const W4a16Args& a, float* out);
 
 // --------------------------------------------------------------- MoE glue
 struct RoutePlanArgs {

@@ -256,6 +256,22 @@ St Mxfp4Decode(const pih_amd_mxfp4_decode_launch_v1* r) {
   return LaunchMxfp4Decode(a);
 }
 
+St W4a16Dequant(const pih_amd_w4a16_dequant_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) ||
+      (r->format != PIH_AMD_W4A16_SYMMETRIC_V1 && r->format != PIH_AMD_W4A16_ASYMMETRIC_V1))
+    return Invalid("w4a16_dequant_request_invalid");
+  W4a16Args a;
+  a.qweight = Ptr<const void>(r->qweight);
+  a.scales = Ptr<const uint16_t>(r->scales);
+  a.zeros = Ptr<const uint32_t>(r->zeros);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.n = r->n;
+  a.k = r->k;
+  a.symmetric = r->format == PIH_AMD_W4A16_SYMMETRIC_V1;
+  return LaunchW4a16Dequant(a, Ptr<float>(r->output_f32));
+}
+
 PIH_AMD_CONTAINED(CQueryWorkspace, QueryWorkspace, pih_amd_workspace_query_v1)
 PIH_AMD_CONTAINED(CRoutePlan, RoutePlan, pih_amd_route_plan_launch_v1)
 PIH_AMD_CONTAINED(CFp8Quant, Fp8Quant, pih_amd_fp8_quant_launch_v1)
@@ -268,11 +284,12 @@ PIH_AMD_CONTAINED(CW4a16, W4a16, pih_amd_w4a16_launch_v1)
 PIH_AMD_CONTAINED(CSiluMul, SiluMul, pih_amd_silu_mul_launch_v1)
 PIH_AMD_CONTAINED(CSwiGlu, SwiGlu, pih_amd_swiglu_launch_v1)
 PIH_AMD_CONTAINED(CMxfp4Decode, Mxfp4Decode, pih_amd_mxfp4_decode_launch_v1)
+PIH_AMD_CONTAINED(CW4a16Dequant, W4a16Dequant, pih_amd_w4a16_dequant_launch_v1)
 
 const pih_amd_linear_kernels_api_v1 kContract = {
     sizeof(pih_amd_linear_kernels_api_v1), kAbi, &kIdentity, &CQueryWorkspace, &CRoutePlan,
     &CFp8Quant, &CFp8Gemm, &CMoeFp8Gemm, &CMoeMxfp4Gemm, &CMoeCombine, &CBf16Gemm, &CW4a16,
-    &CSiluMul, &CSwiGlu, &CMxfp4Decode};
+    &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant};
 
 pih_status_v1 BindOrigin(const char* path) noexcept {
   return ToAbi(path && path[0] == '/' ? Ok() : Invalid("bind_origin_path_not_absolute"));

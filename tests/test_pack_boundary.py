@@ -1,0 +1,184 @@
+"""CPU tests of the drop-in boundary (no device work):
+  - every C struct the packs exchange has the size and field offsets the
+    ctypes mirror assumes (headers compiled with gcc);
+  - each pack exports exactly the two Kernel Pack symbols and passes the
+    reference loader's checks (src/microkernel/kernel_pack_loader.cpp:90-123);
+  - request validation: NULL request, wrong struct_size or abi_version give
+    INVALID_ARGUMENT; stream 0 and bad shapes are rejected before any
+    launch; entries outside the linear path answer UNAVAILABLE.
+"""
+import ctypes as C
+import json
+import os
+import subprocess
+import tempfile
+
+import pytest
+
+from pih_amd import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+DS_C = {n: f"pih_deepseek_{n}_launch_v1" for n in abi.DS}
+LN_C = {n: f"pih_amd_{n}_launch_v1" for n in abi.LN}
+LN_C["workspace_query"] = "pih_amd_workspace_query_v1"
+LN_C["w4a16"] = "pih_amd_w4a16_launch_v1"
+
+
+def _layout_program():
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "pih/contracts/deepseek_kernels_v1.h"',
+             '#include "pih/contracts/amd_linear_kernels_v1.h"', '#include "pih/contracts/qwen_kernels_v1.h"',
+             "int main(void) {", 'printf("{");']
+    first = True
+
+    def emit(key, ctype, fields):
+        nonlocal first
+        sep = "" if first else ","
+        first = False
+        lines.append(f'printf("{sep}\\"{key}\\": [%zu", sizeof({ctype}));')
+        for f in fields:
+            lines.append(f'printf(", %zu", offsetof({ctype}, {f}));')
+        lines.append('printf("]");')
+
+    for n, t in abi.DS.items():
+        emit("ds." + n, DS_C[n], [f[0] for f in t._fields_])
+    for n, t in abi.LN.items():
+        emit("ln." + n, LN_C[n], [f[0] for f in t._fields_])
+    emit("status", "pih_status_v1", [f[0] for f in abi.Status._fields_])
+    emit("identity", "pih_kernel_pack_identity_v1", [f[0] for f in abi.Identity._fields_])
+    emit("api", "pih_kernel_pack_api_v1", [f[0] for f in abi.PackApi._fields_])
+    emit("ds_api", "pih_deepseek_kernels_api_v1", [f[0] for f in abi.DS_API._fields_])
+    emit("ln_api", "pih_amd_linear_kernels_api_v1", [f[0] for f in abi.LN_API._fields_])
+    lines += ['printf("}\\n");', "return 0; }"]
+    return "\n".join(lines)
+
+
+def test_c_struct_layouts_match_ctypes_mirror():
+    with tempfile.TemporaryDirectory() as d:
+        src = os.path.join(d, "layout.c")
+        exe = os.path.join(d, "layout")
+        with open(src, "w") as f:
+            f.write(_layout_program())
+        subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", INCLUDE, src, "-o", exe], check=True)
+        got = json.loads(subprocess.run([exe], check=True, capture_output=True, text=True).stdout)
+
+    def mirror(t):
+        return [C.sizeof(t)] + [getattr(t, f[0]).offset for f in t._fields_]
+
+    want = {"ds." + n: mirror(t) for n, t in abi.DS.items()}
+    want.update({"ln." + n: mirror(t) for n, t in abi.LN.items()})
+    want.update(status=mirror(abi.Status), identity=mirror(abi.Identity), api=mirror(abi.PackApi),
+                ds_api=mirror(abi.DS_API), ln_api=mirror(abi.LN_API))
+    assert got == want
+    assert got["status"][0] == 268
+    assert len(abi.DS_ORDER) == 29
+
+
+@pytest.mark.parametrize("path", [abi.DEEPSEEK_PACK, abi.LINEAR_PACK])
+def test_pack_exports_exactly_two_symbols(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True, text=True).stdout
+    syms = sorted(line.split()[-1] for line in out.splitlines() if line.split() and line.split()[-2] in "TtDdBbRr")
+    assert syms == ["pih_kernel_pack_api_v1_get", "pih_kernel_pack_identity_v1_get"], syms
+
+
+def test_packs_pass_reference_loader_checks():
+    ds = abi.deepseek_pack()
+    assert (ds.pack_id, ds.pack_abi, ds.architecture) == (
+        "pih.kernels.deepseek-v4.gfx950", "pih.deepseek-gfx950-kernel-pack.v1", "gfx950")
+    ln = abi.linear_pack()
+    assert (ln.pack_id, ln.pack_abi, ln.architecture) == (
+        "pih.kernels.amd-linear.gfx950", "pih.amd-linear-kernels.v1", "gfx950")
+    for name in abi.DS_ORDER:
+        assert getattr(ds.table, "launch_" + name), name
+    for f, _ in abi.LN_ORDER:
+        assert getattr(ln.table, f), f
+    # bind_origin: absolute path OK, relative path rejected, no device work
+    assert ds.api.bind_origin(b"/opt/pack.so").code == abi.OK
+    assert ds.api.bind_origin(b"relative.so").code == abi.INVALID_ARGUMENT
+    with pytest.raises(abi.PackError):
+        abi.load_pack(abi.LINEAR_PACK, "pih.deepseek-gfx950-kernel-pack.v1")
+
+
+def test_canonical_id_rules():
+    ok = [b"pih.kernels.x", b"a-b.c0"]
+    bad = [b"", b".a", b"a.", b"a..b", b"A", b"a_b", b"a b"]
+    assert all(abi.valid_canonical_id(v, 64) for v in ok)
+    assert not any(abi.valid_canonical_id(v, 64) for v in bad)
+
+
+def _all_entries():
+    for n in abi.DS_ORDER:
+        yield "ds", "launch_" + n, abi.DS[n]
+    for f, s in abi.LN_ORDER:
+        yield "ln", f, abi.LN[s]
+
+
+@pytest.mark.parametrize("pack,entry,rtype", list(_all_entries()), ids=lambda v: v if isinstance(v, str) else "")
+def test_header_validation(pack, entry, rtype):
+    p = abi.deepseek_pack() if pack == "ds" else abi.linear_pack()
+    fn = getattr(p.table, entry)
+    st = fn(None)
+    assert st.code == abi.INVALID_ARGUMENT and st.struct_size == 268 and st.abi_version == 1
+    r = abi.request(rtype)
+    r.struct_size -= 4
+    assert fn(C.byref(r)).code == abi.INVALID_ARGUMENT
+    r = abi.request(rtype)
+    r.abi_version = 2
+    assert fn(C.byref(r)).code == abi.INVALID_ARGUMENT
+
+
+HOT_DS = {"fp8_activation_quant", "fp8_gemm", "grouped_fp8_gemm", "route_gather", "fp4_gemm", "expert_swiglu",
+          "expert_accumulate", "router_gemm", "shared_swiglu", "expert_finalize"}
+
+
+@pytest.mark.parametrize("name", [n for n in abi.DS_ORDER if n not in HOT_DS])
+def test_non_linear_entries_unavailable(name):
+    st = abi.deepseek_pack().call("launch_" + name, abi.request(abi.DS[name]))
+    assert st.code == abi.UNAVAILABLE, st
+
+
+@pytest.mark.parametrize("name", sorted(HOT_DS))
+def test_hot_entries_reject_zero_stream(name):
+    r = abi.request(abi.DS[name])
+    for f, t in r._fields_:
+        if t is abi.UPTR and f != "stream":
+            setattr(r, f, 0x1000)
+    for f in ("m", "n", "k", "token_count", "route_count", "packed_token_count", "logical_k", "group_count",
+              "output_per_group", "input_per_group", "expert_count", "hidden_size"):
+        if hasattr(r, f):
+            setattr(r, f, 128)
+    if hasattr(r, "output_type"):
+        r.output_type = 1
+    st = abi.deepseek_pack().call("launch_" + name, r)
+    assert st.code == abi.INVALID_ARGUMENT, st
+
+
+def test_linear_entries_reject_bad_requests():
+    ln = abi.linear_pack()
+    r = abi.request(abi.LN["moe_fp8_gemm"], activation_e4m3=0x1000, activation_scale=0x1000, weight_e4m3=0x1000,
+                    weight_scale=0x1000, expert_offsets_u32=0x1000, output=0x1000, error_flag_u32=0x1000, stream=0,
+                    row_capacity=128, expert_count=8, n=256, k=128, activation_rows=16, scale_format=1, output_type=1)
+    assert ln.call("launch_moe_fp8_gemm", r).code == abi.INVALID_ARGUMENT  # stream 0
+    r.stream = 0x2000
+    r.k = 100
+    assert ln.call("launch_moe_fp8_gemm", r).code == abi.INVALID_ARGUMENT  # k % 128
+    r.k = 128
+    r.scale_format = 9
+    assert ln.call("launch_moe_fp8_gemm", r).code == abi.INVALID_ARGUMENT
+    r.scale_format = 1
+    r.output_type = 3
+    r.n = 128
+    assert ln.call("launch_moe_fp8_gemm", r).code == abi.INVALID_ARGUMENT  # SwiGLU needs n % 256
+    q = abi.request(abi.LN["route_plan"], topk_ids_u32=1, topk_weights_f32=1, expert_offsets_u32=1, row_token_u32=1,
+                    row_weight_f32=1, token_rows_u32=1, workspace=1, workspace_bytes=1, error_flag_u32=1, stream=1,
+                    token_count=10, top_k=33, expert_count=8)
+    assert ln.call("launch_route_plan", q).code == abi.INVALID_ARGUMENT  # top_k > 32
+    q.top_k = 4
+    assert ln.call("launch_route_plan", q).code == abi.INVALID_ARGUMENT  # workspace too small
+    out = (C.c_uint64 * 1)()
+    w = abi.request(abi.LN["workspace_query"], kind=abi.WORKSPACE_ROUTE_PLAN, m=4096, n=8, k=256,
+                    bytes_u64=C.addressof(out))
+    assert ln.call("query_workspace", w).code == abi.OK and out[0] > 0
+    w.kind = 77
+    assert ln.call("query_workspace", w).code == abi.INVALID_ARGUMENT
