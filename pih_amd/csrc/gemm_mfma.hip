@@ -373,9 +373,13 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
       for (int ms = 0; ms < 4; ++ms) {
         if (ms >= (int)ms_live) break;
         const uint32_t arow = wm * 64 + ms * 16 + lr;
-        const uint8_t* pa = &sA[buf][arow * LDS_A + lg * 32];
+        // FP8 A against FP4 B: the instruction pairs an FP8 lane group g's
+        // two 16-byte halves with k [16g, 16g+16) and [64+16g, 64+16g+16),
+        // while an FP4 lane group g holds k [32g, 32g+32) contiguously
+        // (measured on gfx950); same-format operands just use the same map.
+        const uint8_t* pa = &sA[buf][arow * LDS_A + (KIND == kFp4 ? lg * 16 : lg * 32)];
         const v4i a0 = *reinterpret_cast<const v4i*>(pa);
-        const v4i a1 = *reinterpret_cast<const v4i*>(pa + 16);
+        const v4i a1 = *reinterpret_cast<const v4i*>(pa + (KIND == kFp4 ? 64 : 16));
         if constexpr (KIND == kFp8 && SCALE == kScaleF32) {
           const v4i s4 = *reinterpret_cast<const v4i*>(&sAs[buf][wm * 64 + ms * 16 + 4 * lg]);
           const v8i av = cat8(a0, a1);
