@@ -102,12 +102,137 @@ def cpu_baseline(ids, wts, x_bits, budget_s: float = 12.0):
                       f"{elapsed:.2f} s"}
 
 
+QWEN8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+          ("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+
+
+def _timed(torch, fn, iters: int):
+    """Mean ms per call of fn(i) measured with HIP events on the launch stream."""
+    s = torch.cuda.current_stream()
+    fn(0)
+    s.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(s)
+    for i in range(iters):
+        fn(i)
+    ev1.record(s)
+    ev1.synchronize()
+    return ev0.elapsed_time(ev1) / iters
+
+
+def bench_decode(torch, iters: int):
+    """BASELINE configs[1] decode (bf16, M=1) and configs[2] (W4A16 asym,
+    M=1): one pass = the 7 Qwen3-8B projections; weight sets rotate through
+    > 512 MB so HBM, not the 256 MB Infinity Cache, serves them."""
+    from pih_amd import abi
+    from pih_amd.device import ptr, stream_handle
+
+    L = abi.linear_pack()
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x50494802)
+    out = {}
+
+    def query(kind, m, n, k):
+        b = (abi.C.c_uint64 * 1)()
+        L.call("query_workspace", abi.request(abi.LN["workspace_query"], kind=kind, m=m, n=n, k=k,
+                                              bytes_u64=abi.C.addressof(b)))
+        return int(b[0])
+
+    # ---- W4A16 asymmetric, M = 1, 4, 16
+    set_bytes = sum(n * k // 2 + (n * k // 128) * 2 + n * ((k // 128 + 7) // 8) * 4 for _, n, k in QWEN8B)
+    nsets = max(2, -(-600_000_000 // set_bytes))
+    sets = []
+    for _ in range(nsets):
+        layer = []
+        for _, n, k in QWEN8B:
+            q = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), dtype=torch.int32, device=dev, generator=gen)
+            s = (torch.rand(n, k // 128, device=dev, generator=gen) * 0.019 + 0.001).to(torch.bfloat16)
+            z = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, (k // 128 + 7) // 8), dtype=torch.int32, device=dev,
+                              generator=gen)
+            layer.append((q, s, z))
+        sets.append(layer)
+    for m in (1, 4, 16):
+        xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for k in (4096, 12288)}
+        ys = [torch.empty(m, n, dtype=torch.bfloat16, device=dev) for _, n, _ in QWEN8B]
+        ws = [torch.zeros(max(1, query(abi.WORKSPACE_W4A16, m, n, k)), dtype=torch.uint8, device=dev)
+              for _, n, k in QWEN8B]
+        flag = torch.zeros(1, dtype=torch.int32, device=dev)
+        reqs = []
+        for layer in sets:
+            rs = []
+            for j, (_, n, k) in enumerate(QWEN8B):
+                q, s, z = layer[j]
+                rs.append(abi.request(abi.LN["w4a16"], input_bf16=ptr(xs[k]), qweight=ptr(q), scales=ptr(s),
+                                      zeros=ptr(z), output_bf16=ptr(ys[j]), workspace=ptr(ws[j]),
+                                      workspace_bytes=ws[j].numel(), error_flag_u32=ptr(flag),
+                                      stream=stream_handle(), m=m, n=n, k=k, format=abi.W4A16_ASYMMETRIC))
+            reqs.append(rs)
+
+        def run(i):
+            for r in reqs[i % nsets]:
+                L.call("launch_w4a16_gemm", r)
+
+        ms = _timed(torch, run, iters)
+        if int(flag.item()):
+            raise RuntimeError(f"w4a16 error flag {int(flag.item())}")
+        algo = set_bytes + sum(m * k * 2 + m * n * 2 for _, n, k in QWEN8B)
+        out[f"w4a16_m{m}"] = {"us_per_pass": round(ms * 1e3, 2), "launches": 7,
+                              "gbs": round(algo / (ms * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "algorithmic_bytes": algo, "weight_sets": nsets}
+    del sets
+    # ---- BF16 decode, M = 1, 8, 64
+    set_bytes = sum(n * k * 2 for _, n, k in QWEN8B)
+    nsets = max(2, -(-600_000_000 // set_bytes))
+    sets = [[(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16) for _, n, k in QWEN8B]
+            for _ in range(nsets)]
+    for m in (1, 8, 64):
+        xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for k in (4096, 12288)}
+        ys = [torch.empty(m, n, dtype=torch.bfloat16, device=dev) for _, n, _ in QWEN8B]
+        ws = [torch.zeros(max(1, query(abi.WORKSPACE_BF16_GEMM, m, n, k)), dtype=torch.uint8, device=dev)
+              for _, n, k in QWEN8B]
+        reqs = [[abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xs[k]), w_bf16=ptr(layer[j]), output=ptr(ys[j]),
+                             workspace=ptr(ws[j]), workspace_bytes=ws[j].numel(), stream=stream_handle(),
+                             m=m, n=n, k=k, output_type=abi.OUTPUT_BF16)
+                 for j, (_, n, k) in enumerate(QWEN8B)] for layer in sets]
+
+        def run(i):
+            for r in reqs[i % nsets]:
+                L.call("launch_bf16_gemm", r)
+
+        ms = _timed(torch, run, iters)
+        algo = set_bytes + sum(m * k * 2 + m * n * 2 for _, n, k in QWEN8B)
+        out[f"bf16_m{m}"] = {"us_per_pass": round(ms * 1e3, 2), "launches": 7,
+                             "gbs": round(algo / (ms * 1e-3) / 1e9, 1),
+                             "frac_hbm": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": algo, "weight_sets": nsets}
+    # ---- BF16 prefill, M = 2048
+    m = 2048
+    xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for k in (4096, 12288)}
+    ys = [torch.empty(m, n, dtype=torch.bfloat16, device=dev) for _, n, _ in QWEN8B]
+    reqs = [abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xs[k]), w_bf16=ptr(sets[0][j]), output=ptr(ys[j]),
+                        workspace=0, workspace_bytes=0, stream=stream_handle(), m=m, n=n, k=k,
+                        output_type=abi.OUTPUT_BF16) for j, (_, n, k) in enumerate(QWEN8B)]
+
+    def run_prefill(i):
+        for r in reqs:
+            L.call("launch_bf16_gemm", r)
+
+    ms = _timed(torch, run_prefill, max(3, iters // 4))
+    flop = sum(2.0 * m * n * k for _, n, k in QWEN8B)
+    out["bf16_prefill_m2048"] = {"ms_per_pass": round(ms, 4), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                                 "frac_mfma": round(flop / (ms * 1e-3) / 1e12 / 2516.6, 4)}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode GEMV / prefill side measurements")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU (the north-star path is a single-GPU kernel "
@@ -162,6 +287,15 @@ def main() -> int:
     gu_gbs = bytes_gu / (gu_ms * 1e-3) / 1e9
     log("stage ms: " + ", ".join(f"{k}={v:.3f}" for k, v in stage_ms.items()))
 
+    decode = None
+    if not args.no_decode:
+        log("decode GEMV / prefill side measurements")
+        del layer, w13, w2
+        torch.cuda.empty_cache()
+        with engine_stream():
+            decode = bench_decode(torch, iters=max(10, args.steps))
+        log("decode: " + json.dumps(decode))
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -192,6 +326,7 @@ def main() -> int:
                      "algorithmic_bytes": int(bytes_gu), "flop": flop_gu, "ms": round(gu_ms, 4),
                      "mfma_tflops": round(flop_gu / (gu_ms * 1e-3) / 1e12, 1),
                      "mfma_frac": round(flop_gu / (gu_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)},
+        "decode_gemv": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -2,13 +2,14 @@
 // (1..64), with W in bf16 or INT4 (W4A16, symmetric reference format or
 // asymmetric u32-packed format).  Memory-bound: the kernel streams W once.
 //
-// Layout of the work: a wave owns 16 W rows (one MFMA column block) and a
-// contiguous K range; four waves of a block split the block's K range, and
-// `ksplit` blocks split K further.  Each lane loads 16 contiguous bytes of a
-// W row per step (lanes 16g..16g+15 take the g-th 16-byte piece of 16
-// different rows), so a wave-wide load covers 16 rows x 64 bytes.  The x
-// operand comes from global memory (it is small and L2-resident); rows
-// m >= M of the 16-row MFMA tile are zero.
+// Layout of the work: a block owns 16 W rows (one MFMA column block) and
+// its 4, 8 or 16 waves split K into contiguous runs (more waves for small N,
+// so every shape keeps ~2048 waves streaming).  Each lane loads 16
+// contiguous bytes of a W row per step (lanes 16g..16g+15 take the g-th
+// 16-byte piece of 16 different rows), so a wave-wide load covers 16 rows x
+// 64 bytes, and a wave issues U steps of loads before consuming them.  The
+// x operand comes from global memory (small, L2-resident); rows m >= M of
+// the 16-row MFMA tile are zero.
 //   bf16 : one v_mfma_f32_16x16x32_bf16 per 16-byte W piece.
 //   INT4 : one 16-byte piece is 32 nibbles = a quarter of a 128-deep quant
 //          group per lane group, so a wave-wide load covers exactly one
@@ -17,11 +18,9 @@
 //          sum_k x * (q - z) over the group, and the group's scale is
 //          applied once: acc += s[n, g] * partial.  The unpack is the same
 //          function the dequant entry uses (pinned bit-exact by tests).
-// Reduction: waves of a block through LDS in fixed order; blocks of a
-// k-split through an fp32 workspace, the last-arriving block (atomic
-// ticket) summing the partials in split order, so results do not depend on
-// timing.  Ticket counters live at the start of the workspace, must be zero
-// before the first call and are left zero by every completed call.
+// Reduction: the block's waves through LDS in fixed wave order.  There is
+// no split across blocks: combining blocks needs a device-scope fence, which
+// on gfx950 writes back and invalidates L2 and cost more than the GEMV.
 //
 // Error reporting for INT4 follows the reference kernel
 // (kernels/cuda/qwen_bf16_primitives.cu:98-149): the first failure's code
@@ -35,8 +34,6 @@ namespace {
 
 enum WFmt : int { kWBf16 = 0, kWSym = 1, kWAsym = 2 };
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
 constexpr uint32_t kQwenReservedNibble = 12, kQwenBadScale = 13, kQwenNonFinite = 14;
 
 struct GemvParams {
@@ -45,12 +42,8 @@ struct GemvParams {
   const uint16_t* scales;
   const uint32_t* zeros;
   void* out;
-  float* partial;       // [ksplit][m][n] fp32 when ksplit > 1
-  uint32_t* tickets;    // [n/16]
   uint32_t* err;
   uint32_t m, n, k;
-  uint32_t ksplit;      // blocks along K
-  uint32_t k_per_block; // multiple of kStepK
   uint32_t out_f32;
 };
 
@@ -88,76 +81,140 @@ __device__ __forceinline__ bool unpack32(uint4 piece, int zero, v8s out[4]) {
   return ok;
 }
 
-template <int FMT, int MT>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
-  __shared__ float s_red[kWaves][MT][4][64];
-  __shared__ uint32_t s_last;
+template <int FMT, int MT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
+  __shared__ float s_red[WAVES][MT][4][64];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
-  const uint32_t rowblk = blockIdx.x, ks = blockIdx.y;
-  const uint32_t n0 = rowblk * 16;
+  const uint32_t n0 = blockIdx.x * 16;
   const uint32_t nrow = n0 + lr;  // W row this lane loads
   constexpr uint32_t SK = step_k<FMT>();
-  const uint32_t k_begin = ks * p.k_per_block;
-  const uint32_t k_end = min(p.k, k_begin + p.k_per_block);
-  const uint32_t steps = (k_end - k_begin) / SK;
-  // waves interleave over the block's steps
+  const uint32_t k_begin = 0;
+  const uint32_t steps = p.k / SK;
   v4f acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   uint32_t bad = 0;
 
-  for (uint32_t st = wave; st < steps; st += kWaves) {
-    const uint32_t k0 = k_begin + st * SK;
+  // Each wave owns a contiguous run of steps; U steps at a time it issues
+  // every weight (and x) load first and only then unpacks and multiplies,
+  // so U x 16 bytes per lane are in flight per wave.
+  // (1024-thread blocks leave 128 VGPRs per lane: INT4 batches shrink there)
+  constexpr int U = FMT == kWBf16 ? (MT == 1 ? 8 : MT == 2 ? 4 : 2)
+                                  : (WAVES == 16 ? (MT == 1 ? 2 : 1) : (MT == 1 ? 4 : 2));
+  constexpr int XL = FMT == kWBf16 ? 1 : 4;  // x loads per step per M tile
+  const uint32_t spw = (steps + WAVES - 1) / WAVES;
+  const uint32_t s_begin = min(steps, wave * spw), s_end = min(steps, s_begin + spw);
+  const uint32_t zwords = (p.k / 128 + 7) / 8;
+  auto w_piece = [&](uint32_t k0) -> v4i {
+    if constexpr (FMT == kWBf16)
+      return *reinterpret_cast<const v4i*>(static_cast<const uint16_t*>(p.w) + (uint64_t)nrow * p.k + k0 + lg * 8);
+    else if constexpr (FMT == kWSym)
+      return *reinterpret_cast<const v4i*>(static_cast<const uint8_t*>(p.w) + (uint64_t)nrow * (p.k / 2) + k0 / 2 +
+                                           lg * 16);
+    else
+      return *reinterpret_cast<const v4i*>(static_cast<const uint32_t*>(p.w) + (uint64_t)nrow * (p.k / 8) + k0 / 8 +
+                                           lg * 4);
+  };
+  auto x_piece = [&](uint32_t t, uint32_t k0, int i) -> v4i {
+    const uint32_t mrow = t * 16 + lr;
+    if (mrow >= p.m) return v4i{0, 0, 0, 0};
+    const uint32_t off = FMT == kWBf16 ? lg * 8 : lg * 32 + i * 8;
+    return *reinterpret_cast<const v4i*>(p.x + (uint64_t)mrow * p.k + k0 + off);
+  };
+  auto step = [&](uint32_t k0, v4i wp, const v4i* xp, float sc, int zero) {
     if constexpr (FMT == kWBf16) {
-      const uint16_t* wrow = static_cast<const uint16_t*>(p.w) + (uint64_t)nrow * p.k;
-      const uint4 wp = *reinterpret_cast<const uint4*>(wrow + k0 + lg * 8);
-      const v8bf b = __builtin_bit_cast(v8bf, wp);
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const uint32_t mrow = t * 16 + lr;
-        uint4 xp = make_uint4(0, 0, 0, 0);
-        if (mrow < p.m) xp = *reinterpret_cast<const uint4*>(p.x + (uint64_t)mrow * p.k + k0 + lg * 8);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xp), b, acc[t], 0, 0, 0);
-      }
+      for (int t = 0; t < MT; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xp[t]),
+                                                         __builtin_bit_cast(v8bf, wp), acc[t], 0, 0, 0);
     } else {
-      // one 128-deep quant group: lane group lg owns k0 + 32*lg .. +32
-      const uint32_t grp = k0 / 128u;
-      uint4 wp;
-      int zero = 0;
-      float sc;
-      if constexpr (FMT == kWSym) {
-        const uint8_t* wrow = static_cast<const uint8_t*>(p.w) + (uint64_t)nrow * (p.k / 2);
-        wp = *reinterpret_cast<const uint4*>(wrow + k0 / 2 + lg * 16);
-        const uint16_t hb = p.scales[(uint64_t)nrow * (p.k / 128) + grp];
-        sc = (float)__builtin_bit_cast(_Float16, hb);
-      } else {
-        const uint32_t* wrow = static_cast<const uint32_t*>(p.w) + (uint64_t)nrow * (p.k / 8);
-        wp = *reinterpret_cast<const uint4*>(wrow + k0 / 8 + lg * 4);
-        const uint32_t zwords = (p.k / 128 + 7) / 8;
-        zero = (int)((p.zeros[(uint64_t)nrow * zwords + grp / 8] >> (4 * (grp % 8))) & 0xfu);
-        sc = bf16_bits_to_f32(p.scales[(uint64_t)nrow * (p.k / 128) + grp]);
-      }
+      // One 128-deep quant group: lane group lg owns k0 + 32*lg .. +32.
+      // Nibble u becomes the bf16 number 128 + u by OR-ing it into the
+      // mantissa of 128 (0x4300 | u), two per 32-bit word, three ALU ops a
+      // pair; then sum_k x (u - z) = sum_k x (128 + u) - (128 + z) sum_k x,
+      // with sum_k x from one more MFMA against ones.  The symmetric format
+      // is u = nibble ^ 8 with z = 8 (4-bit two's complement).
       if (!(sc > 0.0f) || !__builtin_isfinite(sc)) bad = bad ? bad : kQwenBadScale;
-      v8s q[4];
-      if (!unpack32<FMT>(wp, zero, q)) bad = kQwenReservedNibble;
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const uint32_t mrow = t * 16 + lr;
-        const uint16_t* xr = p.x + (uint64_t)mrow * p.k + k0 + lg * 32;
-        v4f part = v4f{0.f, 0.f, 0.f, 0.f};
+      uint32_t wd[4] = {(uint32_t)wp[0], (uint32_t)wp[1], (uint32_t)wp[2], (uint32_t)wp[3]};
+      if constexpr (FMT == kWSym) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          uint4 xp = make_uint4(0, 0, 0, 0);
-          if (mrow < p.m) xp = *reinterpret_cast<const uint4*>(xr + i * 8);
-          part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xp),
-                                                        __builtin_bit_cast(v8bf, q[i]), part, 0, 0, 0);
+          const uint32_t t = wd[i] ^ 0x88888888u;  // reserved nibble 8 -> 0
+          if ((t - 0x11111111u) & ~t & 0x88888888u) bad = kQwenReservedNibble;
+          wd[i] = t;
         }
-        // output column of this lane is n0 + lr: its group scale is sc
+        zero = 8;
+      }
+      v4i qb[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_fmaf(part[i], sc, acc[t][i]);
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          const uint32_t t = (wd[i] >> (8 * pr)) & 0xffu;
+          qb[i][pr] = (int)((t & 0xfu) | ((t & 0xf0u) << 12) | 0x43004300u);
+        }
+      const v8bf ones = __builtin_bit_cast(v8bf, v4i{0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80});
+      const float zc = 128.0f + (float)zero;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        v4f pq = v4f{0.f, 0.f, 0.f, 0.f}, p1 = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v8bf xb = __builtin_bit_cast(v8bf, xp[t * 4 + i]);
+          pq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb, __builtin_bit_cast(v8bf, qb[i]), pq, 0, 0, 0);
+          p1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xb, ones, p1, 0, 0, 0);
+        }
+        // output column of this lane is n0 + lr: its group scale / zero
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_fmaf(__builtin_fmaf(-zc, p1[i], pq[i]), sc, acc[t][i]);
       }
     }
+  };
+  auto group_scale = [&](uint32_t k0, float& sc, int& zero) {
+    const uint32_t grp = k0 / 128u;
+    if constexpr (FMT == kWSym) {
+      sc = (float)__builtin_bit_cast(_Float16, p.scales[(uint64_t)nrow * (p.k / 128) + grp]);
+      zero = 0;
+    } else if constexpr (FMT == kWAsym) {
+      zero = (int)((p.zeros[(uint64_t)nrow * zwords + grp / 8] >> (4 * (grp % 8))) & 0xfu);
+      sc = bf16_bits_to_f32(p.scales[(uint64_t)nrow * (p.k / 128) + grp]);
+    } else {
+      sc = 1.0f;
+      zero = 0;
+    }
+  };
+
+  uint32_t st = s_begin;
+  for (; st + U <= s_end; st += U) {
+    v4i wv[U], xv[U][MT * XL];
+    float sc[U];
+    int zr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t k0 = k_begin + (st + u) * SK;
+      wv[u] = w_piece(k0);
+      group_scale(k0, sc[u], zr[u]);
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < XL; ++i) xv[u][t * XL + i] = x_piece(t, k0, i);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) step(k_begin + (st + u) * SK, wv[u], xv[u], sc[u], zr[u]);
+  }
+  for (; st < s_end; ++st) {
+    const uint32_t k0 = k_begin + st * SK;
+    v4i xv[MT * XL];
+    float sc;
+    int zr;
+    const v4i wp = w_piece(k0);
+    group_scale(k0, sc, zr);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < XL; ++i) xv[t * XL + i] = x_piece(t, k0, i);
+    step(k0, wp, xv, sc, zr);
   }
   if (bad) publish(p.err, bad);
 
@@ -167,53 +224,22 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) s_red[wave][t][i][lane] = acc[t][i];
   __syncthreads();
-  // thread -> (t, i, lane) output slot; output element m = t*16 + 4*lg + i, n = n0 + lr
+  // thread -> (t, i, lane) output slot; output element m = t*16 + 4*lg + i,
+  // n = n0 + lr; the waves' partial sums are added in wave order
   const uint32_t slots = MT * 4 * 64;
-  for (uint32_t slot = tid; slot < slots; slot += kThreads) {
-    const uint32_t t = slot / 256, i = (slot / 64) % 4, l = slot % 64;
-    float v = 0.0f;
-#pragma unroll
-    for (int wv = 0; wv < kWaves; ++wv) v += s_red[wv][t][i][l];
-    s_red[0][t][i][l] = v;
-  }
-  __syncthreads();
-
-  if (p.ksplit > 1) {
-    for (uint32_t slot = tid; slot < slots; slot += kThreads) {
-      const uint32_t t = slot / 256, i = (slot / 64) % 4, l = slot % 64;
-      const uint32_t mrow = t * 16 + 4 * (l >> 4) + i, col = n0 + (l & 15);
-      if (mrow < p.m) p.partial[((uint64_t)ks * p.m + mrow) * p.n + col] = s_red[0][t][i][l];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t prev = atomicAdd(&p.tickets[rowblk], 1u);
-      s_last = prev == p.ksplit - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-  }
   uint32_t nonfinite = 0;
-  for (uint32_t slot = tid; slot < slots; slot += kThreads) {
+  for (uint32_t slot = tid; slot < slots; slot += WAVES * 64) {
     const uint32_t t = slot / 256, i = (slot / 64) % 4, l = slot % 64;
     const uint32_t mrow = t * 16 + 4 * (l >> 4) + i, col = n0 + (l & 15);
     if (mrow >= p.m) continue;
-    float v;
-    if (p.ksplit > 1) {
-      v = 0.0f;
-      for (uint32_t s = 0; s < p.ksplit; ++s)
-        v += __hip_atomic_load(&p.partial[((uint64_t)s * p.m + mrow) * p.n + col], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      v = s_red[0][t][i][l];
-    }
+    float v = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < WAVES; ++wv) v += s_red[wv][t][i][l];
     if (!__builtin_isfinite(v)) nonfinite = 1;
     if (p.out_f32) static_cast<float*>(p.out)[(uint64_t)mrow * p.n + col] = v;
     else static_cast<uint16_t*>(p.out)[(uint64_t)mrow * p.n + col] = (uint16_t)f32_to_bf16_bits(v);
   }
   if (nonfinite && FMT != kWBf16) publish(p.err, kQwenNonFinite);
-  if (p.ksplit > 1 && tid == 0) p.tickets[rowblk] = 0u;
 }
 
 // Exact dequant of an INT4 weight to fp32: w[n, k] = (q - z) * s (asym) or
@@ -253,57 +279,30 @@ __global__ __launch_bounds__(256) void dequant_kernel(const void* wq, const uint
   if (bad) publish(err, bad);
 }
 
-struct Plan {
-  uint32_t ksplit, k_per_block, mt;
-};
-
+// Waves per block: each block owns 16 W rows and its waves split K, so
+// small N gets more waves per block to keep >= ~2048 waves in flight.
 template <int FMT>
-Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
-  Plan pl;
-  pl.mt = (m + 15) / 16;
-  const uint32_t sk = step_k<FMT>();
+int waves_for(uint32_t n) {
   const uint32_t rowblks = n / 16;
-  const uint32_t steps = k / sk;
-  // aim for >= 2048 waves in flight while each wave keeps >= 4 steps
-  uint32_t ks = (2048 + rowblks * kWaves - 1) / (rowblks * kWaves);
-  const uint32_t max_ks = steps / (kWaves * 4) > 0 ? steps / (kWaves * 4) : 1;
-  if (ks > max_ks) ks = max_ks;
-  if (ks < 1) ks = 1;
-  if (ks > 64) ks = 64;
-  const uint32_t steps_per_block = (steps + ks - 1) / ks;
-  pl.k_per_block = steps_per_block * sk;
-  pl.ksplit = (k + pl.k_per_block - 1) / pl.k_per_block;
-  return pl;
+  return rowblks >= 512 ? 4 : rowblks >= 256 ? 8 : 16;
 }
 
-uint64_t workspace_for(uint32_t m, uint32_t n, const Plan& pl) {
-  if (pl.ksplit <= 1) return 0;
-  const uint64_t tickets = ((uint64_t)(n / 16) * 4 + 255) / 256 * 256;
-  return tickets + (uint64_t)pl.ksplit * m * n * 4;
+template <int FMT, int MT>
+void launch_mt(const GemvParams& p, int waves, hipStream_t s) {
+  const dim3 grid(p.n / 16);
+  if (waves == 4) hipLaunchKernelGGL((gemv_kernel<FMT, MT, 4>), grid, dim3(256), 0, s, p);
+  else if (waves == 8) hipLaunchKernelGGL((gemv_kernel<FMT, MT, 8>), grid, dim3(512), 0, s, p);
+  else hipLaunchKernelGGL((gemv_kernel<FMT, MT, 16>), grid, dim3(1024), 0, s, p);
 }
 
 template <int FMT>
-St launch_gemv(const GemvParams& base, Plan pl, void* ws, uint64_t ws_bytes, hipStream_t s) {
-  GemvParams p = base;
-  if (!ws) {
-    // no workspace: one block column per 16 rows, waves split K in-block
-    pl.ksplit = 1;
-    pl.k_per_block = p.k;
-  }
-  p.ksplit = pl.ksplit;
-  p.k_per_block = pl.k_per_block;
-  if (pl.ksplit > 1) {
-    if (!ws || ws_bytes < workspace_for(p.m, p.n, pl)) return Invalid("gemv_workspace_too_small");
-    p.tickets = static_cast<uint32_t*>(ws);
-    const uint64_t tickets = ((uint64_t)(p.n / 16) * 4 + 255) / 256 * 256;
-    p.partial = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + tickets);
-  }
-  dim3 grid(p.n / 16, pl.ksplit);
-  switch (pl.mt) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<FMT, 1>), grid, dim3(kThreads), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<FMT, 2>), grid, dim3(kThreads), 0, s, p); break;
-    case 3: hipLaunchKernelGGL((gemv_kernel<FMT, 3>), grid, dim3(kThreads), 0, s, p); break;
-    default: hipLaunchKernelGGL((gemv_kernel<FMT, 4>), grid, dim3(kThreads), 0, s, p); break;
+St launch_gemv(const GemvParams& p, hipStream_t s) {
+  const int waves = waves_for<FMT>(p.n);
+  switch ((p.m + 15) / 16) {
+    case 1: launch_mt<FMT, 1>(p, waves, s); break;
+    case 2: launch_mt<FMT, 2>(p, waves, s); break;
+    case 3: launch_mt<FMT, 3>(p, waves, s); break;
+    default: launch_mt<FMT, 4>(p, waves, s); break;
   }
   return AfterLaunch("gemv_launch_failed");
 }
@@ -312,12 +311,18 @@ St launch_gemv(const GemvParams& base, Plan pl, void* ws, uint64_t ws_bytes, hip
 
 uint64_t W4a16WorkspaceBytes(uint32_t m, uint32_t n, uint32_t k) {
   if (m == 0 || n == 0 || k == 0 || k % 128) return 0;
-  return workspace_for(m, n, plan_for<kWAsym>(m, n, k));
+  (void)m;
+  (void)n;
+  (void)k;
+  return 0;
 }
 
 uint64_t Bf16GemvWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k) {
   if (m == 0 || n == 0 || k == 0 || k % 32) return 0;
-  return workspace_for(m, n, plan_for<kWBf16>(m, n, k));
+  (void)m;
+  (void)n;
+  (void)k;
+  return 0;
 }
 
 St LaunchBf16Gemv(const Bf16GemmArgs& a) {
@@ -334,7 +339,7 @@ St LaunchBf16Gemv(const Bf16GemmArgs& a) {
   p.n = a.n;
   p.k = a.k;
   p.out_f32 = a.out_kind == kOutF32;
-  return launch_gemv<kWBf16>(p, plan_for<kWBf16>(a.m, a.n, a.k), a.workspace, a.workspace_bytes, a.stream);
+  return launch_gemv<kWBf16>(p, a.stream);
 }
 
 St LaunchW4a16(const W4a16Args& a) {
@@ -356,8 +361,8 @@ St LaunchW4a16(const W4a16Args& a) {
   p.n = a.n;
   p.k = a.k;
   if (a.symmetric)
-    return launch_gemv<kWSym>(p, plan_for<kWSym>(a.m, a.n, a.k), a.workspace, a.workspace_bytes, a.stream);
-  return launch_gemv<kWAsym>(p, plan_for<kWAsym>(a.m, a.n, a.k), a.workspace, a.workspace_bytes, a.stream);
+    return launch_gemv<kWSym>(p, a.stream);
+  return launch_gemv<kWAsym>(p, a.stream);
 }
 
 St LaunchW4a16Dequant(const W4a16Args& a, float* out) {
