@@ -1,0 +1,472 @@
+// MoE-segmented FP8 block-scaled grouped GEMM for gfx950, 128 x 256 tiles.
+//
+//   out[row, :] = A[gather[row], :] . W[e]^T   for the rows of expert e
+//
+// A e4m3 [a_rows_total, K] with one scale per (A row, 128 k); W e4m3
+// [E][N][K] with one scale per (128 W rows, 128 k); scales fp32 or UE8M0
+// (reference src/model/deepseek_fp8_gemm_oracle.cpp:10-80 per element; the
+// expert segments are the device offsets of the route plan, the reference's
+// host plan deepseek_expert_subwave_plan.cpp:32-101).
+//
+// Design (measured on MI355X; the per-CU limits are 128 B/clk of LDS, about
+// 64 B/clk of vector-memory loads and one 16x16x128 FP8 MFMA per 32 clk per
+// SIMD):
+//   * one block of 512 threads (8 waves, two per SIMD) per CU owns a tile of
+//     128 A rows x 256 W rows; each 128-deep K step loads 48 KB with full
+//     128-byte lines (8 lanes per row) and stages both operands in LDS (rows
+//     padded to 144 B: the 16 rows one ds_read_b128 touches hit distinct
+//     banks);
+//   * the output is computed transposed, C^T = W . A^T: the MFMA's first
+//     operand is a 16-row W block and its second a 16-row A block, so a lane
+//     owns four consecutive output columns of one row.  That makes the fp32
+//     A-row scale a single value per lane and 16-byte block, and the
+//     epilogue stores 8 or 16 contiguous bytes per lane;
+//   * wave (wm, wn) computes A rows wm*64 + [0,64) against W rows
+//     wn*64 + [0,64): 4 x 4 MFMAs of 16x16x128 per K step;
+//   * global loads run three steps ahead in three register sets; the main
+//     loop is six whole steps with no branch around a memory operation, so
+//     the compiler's in-order vmcnt waits stay exact and every load has two
+//     whole steps to land;
+//   * fp32 scales: each MFMA starts from zero and the lane adds
+//     t * (a_scale[row] * w_scale[block]) in fp32 (DeepSeek-V3 promotion,
+//     bit-identical to the 128x128-tile kernel); UE8M0 scales ride in the
+//     MFMA's E8M0 operands and the MFMAs chain on the accumulator.
+// Tiles are numbered expert-major and, inside an expert, in groups of up to
+// 32 M-tiles walked M-fastest; each XCD (blocks b % 8) walks one contiguous
+// range of that order so concurrently running tiles share W and A in its L2.
+#include "device_common.hpp"
+#include "kernels.hpp"
+
+namespace pih_amd {
+namespace {
+
+constexpr int BM = 128, BN = 256, NTH = 512, LDS_ROW = 144, GROUP_M = 32;
+
+struct MoeParams {
+  const uint8_t* a;
+  const void* a_scale;
+  const uint32_t* a_gather;
+  const uint8_t* w;
+  const void* w_scale;
+  void* out;
+  const float* row_weight;
+  const uint32_t* offsets;
+  uint32_t* err;
+  uint32_t m, n, k, experts, a_rows_total;
+  uint64_t out_row_stride;
+  uint32_t n_tiles;
+  float limit;
+  uint32_t err_code, err_scale, err_nonfinite;
+};
+
+__device__ __forceinline__ v8i cat8(v4i x, v4i y) {
+  return v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+
+// Block -> (expert, first row, rows, N tile); false for blocks past the
+// last tile.  The per-expert M-tile counts are scanned by the whole block
+// (one wave-level shuffle scan plus the eight wave totals).
+__device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, uint32_t& rows, uint32_t& nt) {
+  __shared__ uint32_t s_wave[NTH / 64];
+  __shared__ uint32_t s_res[3];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t E = p.experts, NTL = p.n_tiles;
+  const uint32_t per_t = (E + NTH - 1) / NTH;
+  uint32_t cnt = 0;
+  for (uint32_t j = 0; j < per_t; ++j) {
+    const uint32_t e = tid * per_t + j;
+    if (e < E) {
+      const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
+      cnt += hi > lo ? (hi - lo + BM - 1) / BM : 0u;
+    }
+  }
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t v = __shfl_up(incl, off, 64);
+    if ((int)lane >= off) incl += v;
+  }
+  if (lane == 63) s_wave[wave] = incl;
+  if (tid == 0) s_res[0] = 0xffffffffu;
+  __syncthreads();
+  uint32_t before = 0, total_m = 0;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) {
+    const uint32_t v = s_wave[w];
+    if (w < (int)wave) before += v;
+    total_m += v;
+  }
+  incl += before;
+  const uint32_t excl = incl - cnt;
+  const uint32_t total = total_m * NTL;
+  const uint32_t per = (total + 7) / 8;
+  const uint32_t xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const uint32_t t = xcd * per + jj;
+  if (jj >= per || t >= total) return false;  // same for every thread
+  const uint32_t slot = t / NTL;              // M tile, expert-major
+  if (slot >= excl && slot < incl) {
+    uint32_t acc = excl;
+    for (uint32_t j = 0; j < per_t; ++j) {
+      const uint32_t e = tid * per_t + j;
+      if (e >= E) break;
+      const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
+      const uint32_t c = hi > lo ? (hi - lo + BM - 1) / BM : 0u;
+      if (slot < acc + c) {
+        s_res[0] = e;
+        s_res[1] = acc;
+        s_res[2] = c;
+        break;
+      }
+      acc += c;
+    }
+  }
+  __syncthreads();
+  const uint32_t e = s_res[0];
+  if (e == 0xffffffffu) return false;
+  const uint32_t mbase = s_res[1], mt = s_res[2];
+  const uint32_t local = t - mbase * NTL;
+  const uint32_t mg = local / (GROUP_M * NTL);
+  const uint32_t gsize = min((uint32_t)GROUP_M, mt - mg * GROUP_M);
+  const uint32_t r = local - mg * GROUP_M * NTL;
+  const uint32_t mtile = mg * GROUP_M + r % gsize;
+  nt = r / gsize;
+  const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
+  if (hi > p.m || lo > hi) {
+    if (tid == 0) atomicOr(p.err, p.err_code);
+    return false;
+  }
+  expert = e;
+  row0 = lo + mtile * BM;
+  rows = min((uint32_t)BM, hi - row0);
+  return true;
+}
+
+template <int SCALE, int OUT>
+__global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
+  __shared__ __align__(16) uint8_t sA[2][BM * LDS_ROW];
+  __shared__ __align__(16) uint8_t sB[2][BN * LDS_ROW];
+  // A-row scales of a stage: row wm*64 + rb*16 + l at [wm*64 + l*4 + rb]
+  __shared__ __align__(16) uint32_t sSa[2][BM];
+  __shared__ __align__(16) uint32_t sSw[2][2];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t lr = lane & 15, lg = lane >> 4;
+  const uint32_t wm = __builtin_amdgcn_readfirstlane(wave >> 2), wn = __builtin_amdgcn_readfirstlane(wave & 3);
+
+  uint32_t expert, row0, rows, nt;
+  if (!moe_tile(p, expert, row0, rows, nt)) return;
+  expert = __builtin_amdgcn_readfirstlane(expert);
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  rows = __builtin_amdgcn_readfirstlane(rows);
+  nt = __builtin_amdgcn_readfirstlane(nt);
+
+  const uint32_t K = p.k, KB = K / 128;
+  uint32_t bad = 0;
+
+  // Rows past the tile's end (and rejected gather indices) read A row 0:
+  // loads stay unconditional and in bounds, and the output rows they feed
+  // are never stored (an output row depends on its own A row only).
+  auto a_source = [&](uint32_t r) -> uint64_t {
+    if (r >= rows) return 0;
+    const uint32_t logical = row0 + r;
+    const uint64_t src = p.a_gather ? p.a_gather[logical] : logical;
+    if (src >= p.a_rows_total) {
+      bad |= kErrCode;
+      return 0;
+    }
+    return src;
+  };
+  // staging: chunk c = tid + 512 i -> tile row c >> 3, 16-byte column c & 7
+  const uint32_t ccol = (tid & 7) * 16;
+  const uint8_t* a_ptr[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) a_ptr[i] = p.a + a_source((tid >> 3) + 64 * i) * K + ccol;
+  const uint64_t sa_off = a_source(tid & (BM - 1)) * KB;
+
+  // W tile row R: for SwiGLU, wave block R >> 6 holds 32 gate rows (R & 63
+  // below 32) and the 32 matching up rows, so each wave owns gate/up pairs
+  auto w_row = [&](uint32_t R) -> uint32_t {
+    if constexpr (OUT == kOutSwiGlu) {
+      const uint32_t wv = R >> 6, j = (R & 63) >> 4, rr = R & 15;
+      const uint32_t base = nt * 128 + wv * 32 + (j & 1) * 16 + rr;
+      return j >= 2 ? p.n / 2 + base : base;
+    } else {
+      const uint32_t row = nt * BN + R;
+      return row < p.n ? row : p.n - 1;
+    }
+  };
+  const uint8_t* w_base = p.w + (uint64_t)expert * p.n * K;
+  const uint8_t* w_ptr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w_ptr[i] = w_base + (uint64_t)w_row((tid >> 3) + 64 * i) * K + ccol;
+  // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
+  uint32_t wblk0, wblk1;
+  if constexpr (OUT == kOutSwiGlu) {
+    wblk0 = nt;
+    wblk1 = (p.n / 2 + nt * 128) / 128;
+  } else {
+    wblk0 = min(2 * nt, p.n / 128 - 1);
+    wblk1 = min(2 * nt + 1, p.n / 128 - 1);
+  }
+  const uint64_t ws0_off = ((uint64_t)expert * (p.n / 128) + wblk0) * KB;
+  const uint64_t ws1_off = ((uint64_t)expert * (p.n / 128) + wblk1) * KB;
+  // live 16-row blocks of this wave's 64-row half
+  const uint32_t rb_live =
+      __builtin_amdgcn_readfirstlane(rows > wm * 64 ? min(4u, (rows - wm * 64 + 15) / 16) : 0u);
+
+  v4i ra[3][2], rw[3][4];
+  uint32_t sar[3], swr0[3], swr1[3];
+  auto gload = [&](int set, uint32_t kb) {
+    const uint64_t o = (uint64_t)kb * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ra[set][i] = *reinterpret_cast<const v4i*>(a_ptr[i] + o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rw[set][i] = *reinterpret_cast<const v4i*>(w_ptr[i] + o);
+    if constexpr (SCALE == kScaleUe8m0) {
+      sar[set] = static_cast<const uint8_t*>(p.a_scale)[sa_off + kb];
+      swr0[set] = static_cast<const uint8_t*>(p.w_scale)[ws0_off + kb];
+      swr1[set] = static_cast<const uint8_t*>(p.w_scale)[ws1_off + kb];
+    } else {
+      sar[set] = static_cast<const uint32_t*>(p.a_scale)[sa_off + kb];
+      swr0[set] = static_cast<const uint32_t*>(p.w_scale)[ws0_off + kb];
+      swr1[set] = static_cast<const uint32_t*>(p.w_scale)[ws1_off + kb];
+    }
+  };
+  auto lstore = [&](int set, int stage) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<v4i*>(&sA[stage][((tid >> 3) + 64 * i) * LDS_ROW + ccol]) = ra[set][i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<v4i*>(&sB[stage][((tid >> 3) + 64 * i) * LDS_ROW + ccol]) = rw[set][i];
+    if (tid < BM) {
+      sSa[stage][(tid >> 6) * 64 + (tid & 15) * 4 + ((tid >> 4) & 3)] = sar[set];
+      if constexpr (SCALE == kScaleUe8m0)
+        bad |= ((sar[set] == 0xffu && tid < rows) || swr0[set] == 0xffu || swr1[set] == 0xffu) ? kErrScale : 0u;
+      if (tid < 2) sSw[stage][tid] = tid ? swr1[set] : swr0[set];
+    }
+  };
+
+  v4f acc[4][4];  // [W block nb][A block rb]
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int stage) {
+    if (rb_live == 0) return;
+    // operand fragments: lane (lr, lg) holds row lr, bytes [16lg, 16lg+16)
+    // and [64+16lg, 64+16lg+16) of the step (the same map for both)
+    v8i wf[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const uint8_t* pb = &sB[stage][(wn * 64 + nb * 16 + lr) * LDS_ROW + lg * 16];
+      wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb), *reinterpret_cast<const v4i*>(pb + 64));
+    }
+    const v4i sa4 = *reinterpret_cast<const v4i*>(&sSa[stage][wm * 64 + lr * 4]);
+    const uint32_t sw0 = sSw[stage][OUT == kOutSwiGlu ? 0 : (wn >> 1)];
+    const uint32_t sw1 = sSw[stage][OUT == kOutSwiGlu ? 1 : (wn >> 1)];
+    auto a_frag = [&](int r) -> v8i {
+      const uint8_t* pa = &sA[stage][(wm * 64 + r * 16 + lr) * LDS_ROW + lg * 16];
+      return cat8(*reinterpret_cast<const v4i*>(pa), *reinterpret_cast<const v4i*>(pa + 64));
+    };
+    auto mma = [&](int r, const v8i& af) {
+      if constexpr (SCALE == kScaleF32) {
+        const float sa = __uint_as_float((uint32_t)sa4[r]);
+        const float c0 = sa * __uint_as_float(sw0), c1 = sa * __uint_as_float(sw1);
+        v4f t[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          t[nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[nb], af, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
+                                                                   127, 0, 127);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          const float c = (OUT == kOutSwiGlu && nb >= 2) ? c1 : c0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[nb][r][i] = __builtin_fmaf(t[nb][i], c, acc[nb][r][i]);
+        }
+      } else {
+        const int sb = (int)sa4[r];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[nb][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              wf[nb], af, acc[nb][r], 0, 0, 0, (int)((OUT == kOutSwiGlu && nb >= 2) ? sw1 : sw0), 0, sb);
+      }
+    };
+    // A fragments one block ahead (at most four LDS reads in flight)
+    v8i af = a_frag(0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (r < (int)rb_live) {
+        const v8i afn = a_frag(r < 3 ? r + 1 : 3);
+        mma(r, af);
+        af = afn;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // prologue: steps 0, 1, 2 into sets 0, 1, 2; stage 0 <- step 0
+  const uint32_t last = KB - 1;
+  gload(0, 0);
+  gload(1, min(1u, last));
+  gload(2, min(2u, last));
+  lstore(0, 0);
+  __syncthreads();
+
+  // Step j: compute stage j&1; store step j+1 (set (j+1)%3) into stage
+  // (j+1)&1; barrier; load step j+3 into set j%3.  Loads past the last step
+  // re-read it (in bounds, never stored).
+#define PIH_MOE_STEP(J, TAIL)                                           \
+  {                                                                     \
+    const uint32_t j = kb + (J);                                        \
+    compute((J) & 1);                                                   \
+    if (!(TAIL) || j + 1 < KB) lstore(((J) + 1) % 3, ((J) + 1) & 1);    \
+    __syncthreads();                                                    \
+    if ((TAIL) && j + 1 >= KB) goto done;                               \
+    gload((J) % 3, min(j + 3, last));                                   \
+  }
+  {
+    uint32_t kb = 0;
+    for (; kb + 6 < KB; kb += 6) {
+      PIH_MOE_STEP(0, false)
+      PIH_MOE_STEP(1, false)
+      PIH_MOE_STEP(2, false)
+      PIH_MOE_STEP(3, false)
+      PIH_MOE_STEP(4, false)
+      PIH_MOE_STEP(5, false)
+    }
+    PIH_MOE_STEP(0, true)
+    PIH_MOE_STEP(1, true)
+    PIH_MOE_STEP(2, true)
+    PIH_MOE_STEP(3, true)
+    PIH_MOE_STEP(4, true)
+    PIH_MOE_STEP(5, true)
+  }
+#undef PIH_MOE_STEP
+done:
+
+  // ---- epilogue: lane holds out[row wm*64 + r*16 + lr][4*lg + i] of block nb
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t rr = wm * 64 + r * 16 + lr;
+    if (rr >= rows) continue;
+    const uint64_t orow = (uint64_t)(row0 + rr) * p.out_row_stride;
+    if constexpr (OUT == kOutSwiGlu) {
+      const float rwt = p.row_weight ? p.row_weight[row0 + rr] : 1.0f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t o[4];
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float gt = bf16_round(acc[h][r][i]);
+          float up = bf16_round(acc[h + 2][r][i]);
+          float v = 0.0f;
+          if (!__builtin_isfinite(gt) || !__builtin_isfinite(up)) {
+            ok = false;
+          } else {
+            if (p.limit > 0.0f) {
+              gt = fminf(gt, p.limit);
+              up = fminf(fmaxf(up, -p.limit), p.limit);
+            }
+            v = (gt / (1.0f + expf(-gt))) * up;
+            v = v * rwt;
+            if (!__builtin_isfinite(v)) ok = false;
+          }
+          o[i] = __builtin_isfinite(v) ? f32_to_bf16_bits(v) : 0xffffffffu;
+        }
+        uint16_t* dst = static_cast<uint16_t*>(p.out) + orow + nt * 128 + wn * 32 + h * 16 + 4 * lg;
+        if (ok) {
+          *reinterpret_cast<uint2*>(dst) = uint2{o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+        } else {
+          bad |= kErrNonFinite;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (o[i] != 0xffffffffu) dst[i] = (uint16_t)o[i];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const uint32_t col = nt * BN + wn * 64 + nb * 16 + 4 * lg;
+        if (col >= p.n) continue;
+        const v4f v = acc[nb][r];
+        const bool fin = __builtin_isfinite(v[0]) && __builtin_isfinite(v[1]) && __builtin_isfinite(v[2]) &&
+                         __builtin_isfinite(v[3]);
+        if constexpr (OUT == kOutF32) {
+          float* dst = static_cast<float*>(p.out) + orow + col;
+          if (fin || !p.err_nonfinite) {
+            *reinterpret_cast<v4f*>(dst) = v;
+          } else {
+            bad |= kErrNonFinite;
+            for (int i = 0; i < 4; ++i)
+              if (__builtin_isfinite(v[i])) dst[i] = v[i];
+          }
+        } else {
+          uint16_t* dst = static_cast<uint16_t*>(p.out) + orow + col;
+          if (fin || !p.err_nonfinite) {
+            *reinterpret_cast<uint2*>(dst) = uint2{f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16),
+                                                   f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16)};
+          } else {
+            bad |= kErrNonFinite;
+            for (int i = 0; i < 4; ++i)
+              if (__builtin_isfinite(v[i])) dst[i] = (uint16_t)f32_to_bf16_bits(v[i]);
+          }
+        }
+      }
+    }
+  }
+  if (bad) {
+    const uint32_t bits = ((bad & kErrCode) ? p.err_code : 0u) | ((bad & kErrScale) ? p.err_scale : 0u) |
+                          ((bad & kErrNonFinite) ? p.err_nonfinite : 0u);
+    if (bits) atomicOr(p.err, bits);
+  }
+}
+
+template <int SCALE>
+void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out) {
+  if (out == kOutSwiGlu) hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutSwiGlu>), dim3(grid), dim3(NTH), 0, s, mp);
+  else if (out == kOutF32) hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutF32>), dim3(grid), dim3(NTH), 0, s, mp);
+  else hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutBf16>), dim3(grid), dim3(NTH), 0, s, mp);
+}
+
+}  // namespace
+
+// Called by LaunchFp8BlockGemm for MoE problems without the code scan; the
+// shape, format and pointer checks are the caller's.
+St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
+  MoeParams mp{};
+  mp.a = a.a;
+  mp.a_scale = a.a_scale;
+  mp.a_gather = a.a_gather;
+  mp.w = a.w;
+  mp.w_scale = a.w_scale;
+  mp.out = a.out;
+  mp.row_weight = a.row_weight;
+  mp.offsets = a.offsets;
+  mp.err = a.error_flag;
+  mp.m = a.m;
+  mp.n = a.n;
+  mp.k = a.k;
+  mp.experts = a.problems;
+  mp.a_rows_total = a.a_rows_total;
+  mp.out_row_stride = a.out_row_stride ? a.out_row_stride : (a.out_kind == kOutSwiGlu ? a.n / 2 : a.n);
+  mp.n_tiles = a.out_kind == kOutSwiGlu ? a.n / 256 : (a.n + BN - 1) / BN;
+  mp.limit = a.swiglu_limit;
+  mp.err_code = a.err_code_bit;
+  mp.err_scale = a.err_scale_bit;
+  mp.err_nonfinite = a.err_nonfinite_bit;
+  // sum_e ceil(rows_e / BM) <= m / BM + (number of non-empty experts)
+  const uint64_t mt = (uint64_t)a.m / BM + (a.problems < a.m ? a.problems : a.m);
+  const uint64_t total = mt * mp.n_tiles;
+  if (total == 0 || total > 0x7fffffffull - 8) return Invalid("fp8_gemm_grid_too_large");
+  const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  St s = RequireCleanLastError();
+  if (!s.ok()) return s;
+  if (a.scale_fmt == kScaleF32) launch_out<kScaleF32>(mp, grid, a.stream, a.out_kind);
+  else launch_out<kScaleUe8m0>(mp, grid, a.stream, a.out_kind);
+  return AfterLaunch("fp8_moe_gemm_launch_failed");
+}
+
+}  // namespace pih_amd

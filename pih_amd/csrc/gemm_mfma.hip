@@ -547,6 +547,7 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
     return Invalid("fp8_gemm_output_type_invalid");
   if (a.moe && !a.offsets) return Invalid("fp8_gemm_offsets_missing");
   if (a.a_rows_total == 0) return Invalid("fp8_gemm_a_rows_invalid");
+  if (a.moe && !a.check_codes) return LaunchFp8MoeGemm(a);
   GemmParams gp{};
   gp.a = a.a;
   gp.a_scale = a.a_scale;

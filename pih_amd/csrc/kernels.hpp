@@ -68,6 +68,9 @@ struct BlockGemmArgs {
   uint32_t err_code_bit = 1u, err_scale_bit = 2u, err_nonfinite_bit = 4u;
 };
 St LaunchFp8BlockGemm(const BlockGemmArgs& a);
+// MoE problems without the code scan (called by LaunchFp8BlockGemm after its
+// checks): the 128x256-tile grouped kernel of gemm_fp8_moe.hip
+St LaunchFp8MoeGemm(const BlockGemmArgs& a);
 
 // ----------------------------------------------------- MXFP4 weight GEMM
 // out = A . W^T with W e2m1 packed two per byte (low nibble = even k) and a
