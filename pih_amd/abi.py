@@ -21,6 +21,7 @@ U32, U64, UPTR, F32, F64, I32 = C.c_uint32, C.c_uint64, C.c_size_t, C.c_float, C
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib")
 DEEPSEEK_PACK = os.path.join(LIB_DIR, "libpih_kernels_deepseek_v4_gfx950.so")
 LINEAR_PACK = os.path.join(LIB_DIR, "libpih_kernels_amd_linear_gfx950.so")
+QWEN_PACK = os.path.join(LIB_DIR, "libpih_kernels_qwen3_gfx950.so")
 
 # pih_status_code_v1
 OK, INVALID_ARGUMENT, FAILED_PRECONDITION, INTERNAL, UNAVAILABLE, RESOURCE_EXHAUSTED, DEADLINE_EXCEEDED = range(7)
@@ -221,6 +222,10 @@ LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_versio
                                          ("identity", C.POINTER(Identity))] +
                  [(f, C.CFUNCTYPE(Status, C.POINTER(LN[s]))) for f, s in LN_ORDER])
 
+# pih_qwen_kernels_api_v1 (include/pih/contracts/qwen_kernels_v1.h)
+QWEN_API = _struct("QwenKernelsApi", [("struct_size", U32), ("contract_version", U32), ("target_sm", U32),
+                                      ("root", C.CFUNCTYPE(Status, C.POINTER(C.c_char_p)))])
+
 SCALE_F32, SCALE_UE8M0 = 1, 2
 OUTPUT_BF16, OUTPUT_F32, OUTPUT_SWIGLU_BF16 = 1, 2, 3
 ACTIVATION_E4M3, ACTIVATION_BF16 = 1, 2
@@ -322,7 +327,8 @@ def load_pack(path: str, contract: str, expected_sha256: Optional[str] = None) -
     bound = api.bind_origin(path.encode())
     if bound.struct_size != C.sizeof(Status) or bound.abi_version != 1 or bound.code != OK:
         raise PackError("kernel_pack_origin_binding_failed")
-    table_type = {"pih.deepseek-gfx950-kernel-pack.v1": DS_API, "pih.amd-linear-kernels.v1": LN_API}.get(contract)
+    table_type = {"pih.deepseek-gfx950-kernel-pack.v1": DS_API, "pih.amd-linear-kernels.v1": LN_API,
+                  "pih.qwen-kernels.v1": QWEN_API}.get(contract)
     if table_type is None or ident.pack_abi.decode() != contract:
         raise PackError(f"contract mismatch: pack exports {ident.pack_abi!r}, caller wants {contract!r}")
     table = C.cast(api.contract_api, C.POINTER(table_type)).contents
@@ -339,6 +345,10 @@ def deepseek_pack() -> KernelPack:
 
 def linear_pack() -> KernelPack:
     return load_pack(LINEAR_PACK, "pih.amd-linear-kernels.v1")
+
+
+def qwen_pack() -> KernelPack:
+    return load_pack(QWEN_PACK, "pih.qwen-kernels.v1")
 
 
 def request(struct_type, **fields):

@@ -1,0 +1,136 @@
+"""GPU parity of the gfx950 Qwen code object, launched the way the Qwen model
+launches the reference cubin: resolved through the pack's root(), checked
+against its manifest, loaded with hipModuleLoadData and launched by name with
+the 64-byte kernarg packet and the plan's geometry (ceil(m*n/256) blocks of
+256 threads; qwen3_int4_gemm_plan.cpp:55-85).
+
+W4A16 results are compared with the oracle's po_w4a16_sym (the reference's
+strict-k fp32 sum, qwen_bf16_primitives.cu:98-149) at max_rel <= 1e-2 and
+cos >= 0.9999; the error protocol (first-wins codes 11-14, failing elements
+not written) and SiLU-mul are checked against the same file.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from pih_amd import synth
+from tests.helpers import assert_close, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+QWEN06B = [(2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072)]
+SENTINEL = 0x7E7E
+
+
+@pytest.fixture(scope="module")
+def co():
+    import torch
+
+    from pih_amd.device import engine_stream
+    from pih_amd.qwen import QwenCodeObject
+
+    with engine_stream() as s:
+        yield QwenCodeObject(), s
+        torch.cuda.synchronize()
+
+
+def _run_w4a16(co, x, q, s, m, n, k, grid=None, block=256):
+    import torch
+
+    obj, stream = co
+    xd, qd, sd = to_dev(x), to_dev(q), to_dev(s)
+    out = torch.full((m, n), SENTINEL, dtype=torch.int16, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    obj.w4a16_gemm(xd.data_ptr(), qd.data_ptr(), sd.data_ptr(), out.data_ptr(), flag.data_ptr(), m, n, k,
+                   stream.cuda_stream, grid=grid, block=block)
+    stream.synchronize()
+    return out.cpu().numpy().view(np.uint16), int(flag.item()) & 0xFFFFFFFF
+
+
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("n,k", QWEN06B)
+def test_w4a16_compat_qwen06b_shapes(co, m, n, k):
+    q, s = synth.int4_sym_weight(synth.config_seed(3, 900 + n + k), n, k)
+    x = synth.bf16_normal(synth.config_seed(3, 950 + m), (m, k))
+    got, flag = _run_w4a16(co, x, q, s, m, n, k)
+    assert flag == 0
+    ref = oracle.w4a16_sym(x, q, s)
+    assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref), f"compat w4a16 {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (3, 1024, 4096), (1, 12288, 4096), (1, 4096, 12288),
+                                   (2, 256, 640)])
+def test_w4a16_compat_relaxed_shapes(co, m, n, k):
+    """Qwen3-8B projections and a K that is not a multiple of 1024."""
+    q, s = synth.int4_sym_weight(synth.config_seed(3, 1900 + n + k), n, k)
+    x = synth.bf16_normal(synth.config_seed(3, 1950 + m), (m, k))
+    got, flag = _run_w4a16(co, x, q, s, m, n, k)
+    assert flag == 0
+    ref = oracle.w4a16_sym(x, q, s)
+    assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref), f"compat w4a16 {m}x{n}x{k}")
+
+
+def test_w4a16_compat_errors(co):
+    m, n, k = 2, 1024, 1024
+    q, s = synth.int4_sym_weight(synth.config_seed(3, 4242), n, k)
+    x = synth.bf16_normal(synth.config_seed(3, 4243), (m, k))
+    ref = oracle.w4a16_sym(x, q, s)
+
+    # reserved nibble in W row 5: only column 5 is left unwritten, code 12
+    q2 = q.copy()
+    q2[5, 300] = (q2[5, 300] & 0x0F) | 0x80
+    got, flag = _run_w4a16(co, x, q2, s, m, n, k)
+    assert flag == 12
+    assert (got[:, 5] == SENTINEL).all()
+    keep = np.ones(n, bool)
+    keep[5] = False
+    assert_close(oracle.bf16_bits_to_f32(got[:, keep]), oracle.bf16_bits_to_f32(ref[:, keep]), "rows kept")
+
+    # a zero, a negative and a NaN fp16 scale: code 13, those columns unwritten
+    for bad in (0x0000, 0xBC00, 0x7E00):
+        s2 = s.copy()
+        s2[700, 3] = bad
+        got, flag = _run_w4a16(co, x, q, s2, m, n, k)
+        assert flag == 13, hex(bad)
+        assert (got[:, 700] == SENTINEL).all()
+        assert (got[:, 699] != SENTINEL).all()
+
+    # launch contract: wrong grid, wrong block size, n not a multiple of 256
+    for grid, block in (((m * n + 255) // 256 - 1, 256), ((m * n + 255) // 256 + 1, 256), ((m * n + 127) // 128, 128)):
+        got, flag = _run_w4a16(co, x, q, s, m, n, k, grid=grid, block=block)
+        assert flag == 11
+        assert (got == SENTINEL).all()
+    q3, s3 = synth.int4_sym_weight(5, 320, k)
+    got, flag = _run_w4a16(co, x, q3, s3, m, 320, k)
+    assert flag == 11 and (got == SENTINEL).all()
+    got, flag = _run_w4a16(co, synth.bf16_normal(1, (4097, 128)), *synth.int4_sym_weight(6, 256, 128), 4097, 256,
+                           128)
+    assert flag == 11
+
+
+def test_w4a16_compat_nonfinite_output(co):
+    m, n, k = 1, 256, 128
+    q, s = synth.int4_sym_weight(synth.config_seed(3, 31), n, k)
+    x = synth.bf16_normal(synth.config_seed(3, 32), (m, k))
+    x[0, 7] = 0x7F80  # +inf
+    got, flag = _run_w4a16(co, x, q, s, m, n, k)
+    assert flag == 14
+
+
+def test_silu_mul_code_object(co):
+    import torch
+
+    obj, stream = co
+    count = 3 * 1024 + 17
+    g = synth.bf16_normal(synth.config_seed(1, 70), (count,))
+    u = synth.bf16_normal(synth.config_seed(1, 71), (count,))
+    gd, ud = to_dev(g), to_dev(u)
+    out = torch.empty(count, dtype=torch.bfloat16, device="cuda")
+    obj.silu_mul(gd.data_ptr(), ud.data_ptr(), out.data_ptr(), count, stream.cuda_stream)
+    stream.synchronize()
+    got = to_host(out)
+    ref = oracle.silu_mul(g, u)
+    assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref), "code-object silu_mul")
+    # at most one bf16 ulp from the reference formula
+    diff = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    assert diff.max() <= 1

@@ -50,6 +50,7 @@ def _layout_program():
     emit("api", "pih_kernel_pack_api_v1", [f[0] for f in abi.PackApi._fields_])
     emit("ds_api", "pih_deepseek_kernels_api_v1", [f[0] for f in abi.DS_API._fields_])
     emit("ln_api", "pih_amd_linear_kernels_api_v1", [f[0] for f in abi.LN_API._fields_])
+    emit("qwen_api", "pih_qwen_kernels_api_v1", [f[0] for f in abi.QWEN_API._fields_])
     lines += ['printf("}\\n");', "return 0; }"]
     return "\n".join(lines)
 
@@ -69,13 +70,13 @@ def test_c_struct_layouts_match_ctypes_mirror():
     want = {"ds." + n: mirror(t) for n, t in abi.DS.items()}
     want.update({"ln." + n: mirror(t) for n, t in abi.LN.items()})
     want.update(status=mirror(abi.Status), identity=mirror(abi.Identity), api=mirror(abi.PackApi),
-                ds_api=mirror(abi.DS_API), ln_api=mirror(abi.LN_API))
+                ds_api=mirror(abi.DS_API), ln_api=mirror(abi.LN_API), qwen_api=mirror(abi.QWEN_API))
     assert got == want
     assert got["status"][0] == 268
     assert len(abi.DS_ORDER) == 29
 
 
-@pytest.mark.parametrize("path", [abi.DEEPSEEK_PACK, abi.LINEAR_PACK])
+@pytest.mark.parametrize("path", [abi.DEEPSEEK_PACK, abi.LINEAR_PACK, abi.QWEN_PACK])
 def test_pack_exports_exactly_two_symbols(path):
     out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True, text=True).stdout
     syms = sorted(line.split()[-1] for line in out.splitlines() if line.split() and line.split()[-2] in "TtDdBbRr")
