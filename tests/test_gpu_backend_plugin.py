@@ -57,7 +57,8 @@ def test_full_resource_lifecycle(dev):
     pattern = rng.integers(0, 256, MIB, dtype=np.uint8)
     _ok(d.copy_h2d(0, a.address, pattern.ctypes.data, MIB))
     assert d.copy_h2d(0, a.address + 16, pattern.ctypes.data, MIB).code == FAILED_PRECONDITION
-    assert d.copy_h2d(0, a.address + MIB, pattern.ctypes.data, 1).code == FAILED_PRECONDITION
+    # a range running past the end of `a` (even into a neighbouring allocation) is not owned
+    assert d.copy_h2d(0, a.address + MIB - 8, pattern.ctypes.data, 16).code == FAILED_PRECONDITION
 
     st, tok = d.retain(0)
     _ok(st)
