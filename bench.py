@@ -120,10 +120,37 @@ def _timed(torch, fn, iters: int):
     return ev0.elapsed_time(ev1) / iters
 
 
+def _graphed(torch, make_calls, nsets: int, iters: int):
+    """Mean ms per pass with each weight set's pass captured once in a HIP
+    graph (torch.cuda.CUDAGraph) and replayed; the launches inside are the
+    same C-ABI calls, captured on the graph's stream."""
+    from pih_amd.device import stream_handle
+
+    graphs = []
+    for j in range(nsets):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            keep = make_calls(j, stream_handle())
+        graphs.append((g, keep))
+    torch.cuda.synchronize()
+    return _timed(torch, lambda i: graphs[i % nsets][0].replay(), iters)
+
+
+def _decode_line(ms: float, ms_graph: float, algo: int, nsets: int, launches: int = 7) -> dict:
+    gbs = algo / (ms * 1e-3) / 1e9
+    gbs_graph = algo / (ms_graph * 1e-3) / 1e9
+    return {"us_per_pass": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "us_per_pass_graph": round(ms_graph * 1e3, 2), "gbs_graph": round(gbs_graph, 1),
+            "frac_hbm_graph": round(gbs_graph / HBM_PEAK_GBS, 4), "launches": launches,
+            "algorithmic_bytes": algo, "weight_sets": nsets}
+
+
 def bench_decode(torch, iters: int):
-    """BASELINE configs[1] decode (bf16, M=1) and configs[2] (W4A16 asym,
-    M=1): one pass = the 7 Qwen3-8B projections; weight sets rotate through
-    > 512 MB so HBM, not the 256 MB Infinity Cache, serves them."""
+    """BASELINE configs[1] decode (bf16, M=1, 8, 64) and configs[2] (W4A16
+    asymmetric, M=1, 4, 16): one pass = the 7 Qwen3-8B projections; weight
+    sets rotate through > 512 MB so HBM, not the 256 MB Infinity Cache,
+    serves them.  Each pass is timed twice: eager launches through the C-ABI
+    (host launch cost included) and replayed from a captured HIP graph."""
     from pih_amd import abi
     from pih_amd.device import ptr, stream_handle
 
@@ -158,60 +185,62 @@ def bench_decode(torch, iters: int):
         ws = [torch.zeros(max(1, query(abi.WORKSPACE_W4A16, m, n, k)), dtype=torch.uint8, device=dev)
               for _, n, k in QWEN8B]
         flag = torch.zeros(1, dtype=torch.int32, device=dev)
-        reqs = []
-        for layer in sets:
+
+        def calls(i, stream, m=m, xs=xs, ys=ys, ws=ws, flag=flag):
             rs = []
             for j, (_, n, k) in enumerate(QWEN8B):
-                q, s, z = layer[j]
-                rs.append(abi.request(abi.LN["w4a16"], input_bf16=ptr(xs[k]), qweight=ptr(q), scales=ptr(s),
-                                      zeros=ptr(z), output_bf16=ptr(ys[j]), workspace=ptr(ws[j]),
-                                      workspace_bytes=ws[j].numel(), error_flag_u32=ptr(flag),
-                                      stream=stream_handle(), m=m, n=n, k=k, format=abi.W4A16_ASYMMETRIC))
-            reqs.append(rs)
+                q, s, z = sets[i][j]
+                r = abi.request(abi.LN["w4a16"], input_bf16=ptr(xs[k]), qweight=ptr(q), scales=ptr(s),
+                                zeros=ptr(z), output_bf16=ptr(ys[j]), workspace=ptr(ws[j]),
+                                workspace_bytes=ws[j].numel(), error_flag_u32=ptr(flag), stream=stream,
+                                m=m, n=n, k=k, format=abi.W4A16_ASYMMETRIC)
+                st = L.call("launch_w4a16_gemm", r)
+                if st.code != abi.OK:
+                    raise RuntimeError(f"w4a16 launch: {st}")
+                rs.append(r)
+            return rs
 
-        def run(i):
-            for r in reqs[i % nsets]:
-                L.call("launch_w4a16_gemm", r)
-
-        ms = _timed(torch, run, iters)
+        reqs = [calls(i, stream_handle()) for i in range(nsets)]  # also the warm pass
+        ms = _timed(torch, lambda i: [L.call("launch_w4a16_gemm", r) for r in reqs[i % nsets]], iters)
+        ms_graph = _graphed(torch, calls, nsets, iters)
         if int(flag.item()):
             raise RuntimeError(f"w4a16 error flag {int(flag.item())}")
         algo = set_bytes + sum(m * k * 2 + m * n * 2 for _, n, k in QWEN8B)
-        out[f"w4a16_m{m}"] = {"us_per_pass": round(ms * 1e3, 2), "launches": 7,
-                              "gbs": round(algo / (ms * 1e-3) / 1e9, 1),
-                              "frac_hbm": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                              "algorithmic_bytes": algo, "weight_sets": nsets}
+        out[f"w4a16_m{m}"] = _decode_line(ms, ms_graph, algo, nsets)
     del sets
     # ---- BF16 decode, M = 1, 8, 64
     set_bytes = sum(n * k * 2 for _, n, k in QWEN8B)
     nsets = max(2, -(-600_000_000 // set_bytes))
-    sets = [[(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16) for _, n, k in QWEN8B]
-            for _ in range(nsets)]
+    wsets = [[(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16) for _, n, k in QWEN8B]
+             for _ in range(nsets)]
     for m in (1, 8, 64):
         xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for k in (4096, 12288)}
         ys = [torch.empty(m, n, dtype=torch.bfloat16, device=dev) for _, n, _ in QWEN8B]
         ws = [torch.zeros(max(1, query(abi.WORKSPACE_BF16_GEMM, m, n, k)), dtype=torch.uint8, device=dev)
               for _, n, k in QWEN8B]
-        reqs = [[abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xs[k]), w_bf16=ptr(layer[j]), output=ptr(ys[j]),
-                             workspace=ptr(ws[j]), workspace_bytes=ws[j].numel(), stream=stream_handle(),
-                             m=m, n=n, k=k, output_type=abi.OUTPUT_BF16)
-                 for j, (_, n, k) in enumerate(QWEN8B)] for layer in sets]
 
-        def run(i):
-            for r in reqs[i % nsets]:
-                L.call("launch_bf16_gemm", r)
+        def calls(i, stream, m=m, xs=xs, ys=ys, ws=ws):
+            rs = []
+            for j, (_, n, k) in enumerate(QWEN8B):
+                r = abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xs[k]), w_bf16=ptr(wsets[i][j]), output=ptr(ys[j]),
+                                workspace=ptr(ws[j]), workspace_bytes=ws[j].numel(), stream=stream,
+                                m=m, n=n, k=k, output_type=abi.OUTPUT_BF16)
+                st = L.call("launch_bf16_gemm", r)
+                if st.code != abi.OK:
+                    raise RuntimeError(f"bf16 launch: {st}")
+                rs.append(r)
+            return rs
 
-        ms = _timed(torch, run, iters)
+        reqs = [calls(i, stream_handle()) for i in range(nsets)]
+        ms = _timed(torch, lambda i: [L.call("launch_bf16_gemm", r) for r in reqs[i % nsets]], iters)
+        ms_graph = _graphed(torch, calls, nsets, iters)
         algo = set_bytes + sum(m * k * 2 + m * n * 2 for _, n, k in QWEN8B)
-        out[f"bf16_m{m}"] = {"us_per_pass": round(ms * 1e3, 2), "launches": 7,
-                             "gbs": round(algo / (ms * 1e-3) / 1e9, 1),
-                             "frac_hbm": round(algo / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                             "algorithmic_bytes": algo, "weight_sets": nsets}
+        out[f"bf16_m{m}"] = _decode_line(ms, ms_graph, algo, nsets)
     # ---- BF16 prefill, M = 2048
     m = 2048
     xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for k in (4096, 12288)}
     ys = [torch.empty(m, n, dtype=torch.bfloat16, device=dev) for _, n, _ in QWEN8B]
-    reqs = [abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xs[k]), w_bf16=ptr(sets[0][j]), output=ptr(ys[j]),
+    reqs = [abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xs[k]), w_bf16=ptr(wsets[0][j]), output=ptr(ys[j]),
                         workspace=0, workspace_bytes=0, stream=stream_handle(), m=m, n=n, k=k,
                         output_type=abi.OUTPUT_BF16) for j, (_, n, k) in enumerate(QWEN8B)]
 
@@ -226,6 +255,38 @@ def bench_decode(torch, iters: int):
     return out
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_fp8_cfg4_hbm_traffic.md")
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the gate/up kernel, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (its ``traffic_bytes_per_launch``
+    line); None when that summary is absent."""
+    import re
+
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", f.read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(nbytes: int = 1 << 30, reps: int = 3) -> int:
+    """Three D2D copies of exactly ``nbytes``: under rocprofv3 --pmc their
+    FETCH_SIZE and WRITE_SIZE (KiB per dispatch) give the factors that turn
+    those counters into bytes for the path's kernels."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {nbytes} bytes x {reps}")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -233,7 +294,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode GEMV / prefill side measurements")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 1 GiB device-to-device copies (the reference kernel for scaling the "
+                         "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU (the north-star path is a single-GPU kernel "
               "pack); --gpus must be 1", file=sys.stderr)
@@ -276,7 +342,7 @@ def main() -> int:
             layer.forward(x_d, ids_d, wts_d, marks=marks[i])
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        stage_ms = {name: float(np.mean([m[j].elapsed_time(m[j + 1]) for m in marks]))
+        stage_ms = {name: float(np.median([m[j].elapsed_time(m[j + 1]) for m in marks]))
                     for j, name in enumerate(MoeFp8Layer.STAGES)}
         if flag_value(layer.flag):
             log(f"device error flag {flag_value(layer.flag):#x}")
@@ -320,9 +386,9 @@ def main() -> int:
         "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
         "layer_hbm_gbs": round(bytes_layer / (ms * 1e-3) / 1e9, 1),
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
-        "roofline": {"kernel": "fp8_block_gemm_kernel (MoE gate/up, SwiGLU epilogue)", "bound": "hbm",
+        "roofline": {"kernel": "fp8_moe_gemm_kernel<1, 3> (MoE gate/up, SwiGLU epilogue)", "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                      "algorithmic_bytes": int(bytes_gu), "flop": flop_gu, "ms": round(gu_ms, 4),
                      "mfma_tflops": round(flop_gu / (gu_ms * 1e-3) / 1e12, 1),
                      "mfma_frac": round(flop_gu / (gu_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)},
