@@ -242,6 +242,252 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   if (nonfinite && FMT != kWBf16) publish(p.err, kQwenNonFinite);
 }
 
+// ---------------------------------------------------------------------------
+// Small-M decode GEMV (M <= 4): the path BASELINE decode shapes take.
+//
+// Same 16-row blocks and MFMA operand layout as gemv_kernel; the waves of a
+// block split K into equal runs of spw steps (the host picks WAVES dividing
+// the step count and U dividing spw).  What makes it stream near HBM speed
+// on gfx950 (each point measured on MI355X with a stripped copy of the
+// kernel):
+//   * W is read with non-temporal loads: it is used exactly once, and the
+//     hint measured ~20 % more streaming bandwidth than plain loads;
+//   * a wave loads its own slice of x (rows < M, its K run) first, then its
+//     first U steps of W, then writes x to a wave-private LDS area: waiting
+//     for x leaves W in flight, and no block barrier precedes the math;
+//   * the group scales of a batch arrive in one vector load (U bf16 / fp16
+//     values of the lane's row) and the zero points in one u32, instead of
+//     two scalar-per-step loads that cost more than the nibble math;
+//   * INT4: the 32 nibbles of a lane's 16-byte piece become bf16 (128 + u)
+//     values with two masks and four v_perm per 8 nibbles (x is staged in
+//     the matching k order), four MFMAs give sum_k x (128 + u), and the
+//     group correction (128 + z) * sum_k x uses row sums of x formed from
+//     the same x registers while staging them;
+//   * MFMA rows >= M take a copy of row M - 1 instead of zeros (no per-step
+//     selects); their sums are discarded.
+// Outputs: the waves' partial sums meet in LDS in fixed wave order.
+constexpr uint32_t kSmallM = 4;
+
+template <int FMT>
+__device__ __forceinline__ v4i nt_piece(const void* w, uint64_t elem_offset) {
+  if constexpr (FMT == kWBf16)
+    return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(static_cast<const uint16_t*>(w) + elem_offset));
+  else if constexpr (FMT == kWSym)
+    return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(static_cast<const uint8_t*>(w) + elem_offset));
+  else
+    return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(static_cast<const uint32_t*>(w) + elem_offset));
+}
+
+// 8 nibbles of one word (nibble j = k offset j) -> eight bf16 values
+// 128 + u_j in the order k = 0, 2, 4, 6, 1, 3, 5, 7: the low nibbles of the
+// four bytes are the even k, the high nibbles the odd k, and one v_perm per
+// pair places two of them under the 0x43 exponent byte of 128.  x is staged
+// in LDS in the same order (x_in_nibble_order), so the MFMA sees matching
+// k on both operands.
+__device__ __forceinline__ void nibbles_to_bf16(uint32_t w, v4i& out) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  constexpr uint32_t kExp = 0x43434343u;
+  out[0] = (int)__builtin_amdgcn_perm(kExp, lo, 0x04010400u);  // k0, k2
+  out[1] = (int)__builtin_amdgcn_perm(kExp, lo, 0x04030402u);  // k4, k6
+  out[2] = (int)__builtin_amdgcn_perm(kExp, hi, 0x04010400u);  // k1, k3
+  out[3] = (int)__builtin_amdgcn_perm(kExp, hi, 0x04030402u);  // k5, k7
+}
+
+// Eight bf16 x values (k = 0..7) into the order nibbles_to_bf16 produces.
+__device__ __forceinline__ v4i x_in_nibble_order(v4i v) {
+  const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
+  return v4i{(int)__builtin_amdgcn_perm(w1, w0, 0x05040100u), (int)__builtin_amdgcn_perm(w3, w2, 0x05040100u),
+             (int)__builtin_amdgcn_perm(w1, w0, 0x07060302u), (int)__builtin_amdgcn_perm(w3, w2, 0x07060302u)};
+}
+
+// U consecutive 16-bit scales of one row, starting at a multiple of U.
+template <int U>
+struct ScaleVec {
+  uint32_t w[(U + 1) / 2];
+  __device__ __forceinline__ void load(const uint16_t* p) {
+    if constexpr (U == 8) {
+      const v4i v = *reinterpret_cast<const v4i*>(p);
+      w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
+    } else if constexpr (U == 4) {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      w[0] = v.x, w[1] = v.y;
+    } else if constexpr (U == 2) {
+      w[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else {
+      w[0] = *p;
+    }
+  }
+  __device__ __forceinline__ uint32_t bits(int u) const { return (w[u / 2] >> (16 * (u & 1))) & 0xffffu; }
+};
+
+// Bytes of LDS the small-M kernel needs: per wave its x slice (rows < M,
+// spw steps) and U... per-group row sums, plus the reduction area.
+template <int FMT>
+constexpr uint32_t small_m_lds(uint32_t m, uint32_t spw, uint32_t waves) {
+  return waves * (m * spw * step_k<FMT>() * 2 + (FMT != kWBf16 ? spw * 16 * 4 : 0)) + waves * 4 * 64 * 4;
+}
+
+template <int FMT, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvParams p, uint32_t spw) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr bool kInt4 = FMT != kWBf16;
+  constexpr uint32_t SK = step_k<FMT>();
+  constexpr int XR = 8;  // x chunks per lane loaded ahead of the weights (M * spw * 16 <= 512)
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t lr = lane & 15, lg = lane >> 4;
+  const uint32_t n0 = blockIdx.x * 16, nrow = n0 + lr;
+  const uint32_t K = p.k, M = p.m, G = K / 128;
+  const uint32_t s0 = wave * spw, s1 = s0 + spw;  // WAVES * spw == K / SK
+  const uint32_t span = spw * SK;                 // this wave's K run
+  const uint32_t zwords = (G + 7) / 8;
+  // wave-private LDS: x[M][span] bf16, then (INT4) row sums [spw][16] fp32
+  const uint32_t wave_bytes = M * span * 2 + (kInt4 ? spw * 16 * 4 : 0);
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + wave * wave_bytes);
+  float* xsum = reinterpret_cast<float*>(smem + wave * wave_bytes + M * span * 2);
+  float* red = reinterpret_cast<float*>(smem + WAVES * wave_bytes);  // [WAVES][4][64]
+
+  // ---- this wave's x slice: chunk c = (row m, 16-byte piece j of the run)
+  const uint32_t row_chunks = span / 8, chunks = M * row_chunks;
+  auto x_chunk = [&](uint32_t c) -> v4i {
+    const uint32_t m = c / row_chunks, j = c % row_chunks;
+    return *reinterpret_cast<const v4i*>(p.x + (uint64_t)m * K + s0 * SK + j * 8);
+  };
+  v4i xr[XR];
+#pragma unroll
+  for (int j = 0; j < XR; ++j) {
+    const uint32_t c = lane + 64 * j;
+    xr[j] = c < chunks ? x_chunk(c) : v4i{0, 0, 0, 0};
+  }
+
+  // ---- first batch of W, its scales and zero points
+  v4i wv[U];
+  ScaleVec<U> sv;
+  uint32_t zw = 0;
+  auto issue = [&](uint32_t sb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t k0 = (sb + u) * SK;
+      if constexpr (FMT == kWBf16)
+        wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * K + k0 + lg * 8);
+      else if constexpr (FMT == kWSym)
+        wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * (K / 2) + k0 / 2 + lg * 16);
+      else
+        wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * (K / 8) + k0 / 8 + lg * 4);
+    }
+    if constexpr (kInt4) sv.load(p.scales + (uint64_t)nrow * G + sb);
+    if constexpr (FMT == kWAsym) zw = p.zeros[(uint64_t)nrow * zwords + sb / 8];
+  };
+  issue(s0);
+
+  // ---- x to LDS; INT4: row sums of x per 128-group from the same registers
+  // (16 lanes hold one group of one row: 16 chunks x 8 values)
+  auto stage = [&](uint32_t c, v4i v) {
+    const bool live = c < chunks;
+    if (live) reinterpret_cast<v4i*>(xs)[c] = kInt4 ? x_in_nibble_order(v) : v;
+    if constexpr (kInt4) {
+      float s = 0.0f;
+      if (live) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          s += __uint_as_float((uint32_t)v[q] << 16) + __uint_as_float((uint32_t)v[q] & 0xffff0000u);
+      }
+      s += __shfl_xor(s, 1);
+      s += __shfl_xor(s, 2);
+      s += __shfl_xor(s, 4);
+      s += __shfl_xor(s, 8);
+      if (live && (c & 15) == 0) xsum[((c % row_chunks) / 16) * 16 + c / row_chunks] = s;
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < XR; ++j) stage(lane + 64 * j, xr[j]);
+  for (uint32_t base = 64 * XR; base < chunks; base += 64) {
+    const uint32_t c = base + lane;
+    stage(c, c < chunks ? x_chunk(c) : v4i{0, 0, 0, 0});
+  }
+  // the wave reads back only what it wrote: no block barrier needed
+
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  uint32_t bad = 0;
+  // MFMA rows >= M read row M - 1 of x: their sums are never stored
+  const uint16_t* xrow_ptr = xs + min(lr, M - 1) * span;
+  auto compute = [&](uint32_t sb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t st = sb + u;            // global step
+      const uint32_t kl = (st - s0) * SK;    // k offset inside the wave's run
+      if constexpr (FMT == kWBf16) {
+        const v4i xv = *reinterpret_cast<const v4i*>(xrow_ptr + kl + lg * 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xv), __builtin_bit_cast(v8bf, wv[u]),
+                                                      acc, 0, 0, 0);
+      } else {
+        v4i xv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const v4i*>(xrow_ptr + kl + lg * 32 + i * 8);
+        const v4f xsv = *reinterpret_cast<const v4f*>(xsum + (st - s0) * 16 + lg * 4);
+        float sc;
+        int zero;
+        if constexpr (FMT == kWSym) {
+          sc = (float)__builtin_bit_cast(_Float16, (uint16_t)sv.bits(u));
+          zero = 8;
+        } else {
+          sc = bf16_bits_to_f32(sv.bits(u));
+          zero = (int)((zw >> (4 * (st % 8))) & 0xfu);
+        }
+        if (!(sc > 0.0f) || !__builtin_isfinite(sc)) bad = bad ? bad : kQwenBadScale;
+        uint32_t wd[4] = {(uint32_t)wv[u][0], (uint32_t)wv[u][1], (uint32_t)wv[u][2], (uint32_t)wv[u][3]};
+        if constexpr (FMT == kWSym) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t t = wd[i] ^ 0x88888888u;  // two's complement nibble -> u = q + 8; reserved 8 -> 0
+            if ((t - 0x11111111u) & ~t & 0x88888888u) bad = kQwenReservedNibble;
+            wd[i] = t;
+          }
+        }
+        v4i qb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nibbles_to_bf16(wd[i], qb[i]);
+        v4f pq = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xv[i]),
+                                                       __builtin_bit_cast(v8bf, qb[i]), pq, 0, 0, 0);
+        // rows >= M (copies of row M - 1, stale row sums) are never stored
+        const float zc = 128.0f + (float)zero;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(__builtin_fmaf(-zc, xsv[i], pq[i]), sc, acc[i]);
+      }
+    }
+  };
+
+  compute(s0);
+  for (uint32_t sb = s0 + U; sb < s1; sb += U) {
+    issue(sb);
+    compute(sb);
+  }
+  if constexpr (kInt4)
+    if (bad) publish(p.err, bad);
+
+  // ---- reduce the block's waves in wave order
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+  __syncthreads();
+  uint32_t nonfinite = 0;
+  if (tid < 256) {
+    const uint32_t i = tid / 64, l = tid % 64;
+    const uint32_t mrow = 4 * (l >> 4) + i, col = n0 + (l & 15);
+    if (mrow < M) {
+      float v = 0.0f;
+#pragma unroll
+      for (int wv2 = 0; wv2 < WAVES; ++wv2) v += red[(wv2 * 4 + i) * 64 + l];
+      if (!__builtin_isfinite(v)) nonfinite = 1;
+      if (p.out_f32) static_cast<float*>(p.out)[(uint64_t)mrow * p.n + col] = v;
+      else static_cast<uint16_t*>(p.out)[(uint64_t)mrow * p.n + col] = (uint16_t)f32_to_bf16_bits(v);
+    }
+  }
+  if constexpr (kInt4)
+    if (nonfinite) publish(p.err, kQwenNonFinite);
+}
+
 // Exact dequant of an INT4 weight to fp32: w[n, k] = (q - z) * s (asym) or
 // q * s (sym), the values the GEMV multiplies (as integers times the
 // group scale).
@@ -295,8 +541,65 @@ void launch_mt(const GemvParams& p, int waves, hipStream_t s) {
   else hipLaunchKernelGGL((gemv_kernel<FMT, MT, 16>), grid, dim3(1024), 0, s, p);
 }
 
+template <int FMT, int WAVES, int U>
+St launch_lds(const GemvParams& p, uint32_t spw, hipStream_t s) {
+  const uint32_t lds = small_m_lds<FMT>(p.m, spw, WAVES);
+  static bool raised = false;  // LDS above 64 KB must be allowed once per kernel
+  if (lds > 65536 && !raised) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_lds_kernel<FMT, WAVES, U>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+      return Internal("gemv_lds_attribute_failed");
+    raised = true;
+  }
+  hipLaunchKernelGGL((gemv_lds_kernel<FMT, WAVES, U>), dim3(p.n / 16), dim3(WAVES * 64), lds, s, p, spw);
+  return AfterLaunch("gemv_launch_failed");
+}
+
+// Waves per block and steps per batch for the LDS kernel: the waves split
+// the K steps evenly (WAVES divides steps); among 4, 8, 12 and 16 waves take
+// the first that gives the grid >= 2048 waves (else the largest that
+// divides), with U the largest of 8, 4, 2, 1 dividing the steps per wave.
+// Returns false when no split divides the steps.
+template <int FMT>
+bool pick_lds_split(uint32_t n, uint32_t k, int& waves, uint32_t& spw, int& u) {
+  const uint32_t steps = k / step_k<FMT>(), rowblks = n / 16;
+  waves = 0;
+  for (int w : {4, 8, 12, 16}) {
+    if (steps % (uint32_t)w) continue;
+    waves = w;
+    if (rowblks * (uint32_t)w >= 2048) break;
+  }
+  if (!waves) return false;
+  spw = steps / waves;
+  u = spw % 8 == 0 ? 8 : spw % 4 == 0 ? 4 : spw % 2 == 0 ? 2 : 1;
+  return true;
+}
+
+template <int FMT, int WAVES>
+St launch_lds_u(const GemvParams& p, uint32_t spw, int u, hipStream_t s) {
+  if (u == 8) return launch_lds<FMT, WAVES, 8>(p, spw, s);
+  if (u == 4) return launch_lds<FMT, WAVES, 4>(p, spw, s);
+  if (u == 2) return launch_lds<FMT, WAVES, 2>(p, spw, s);
+  return launch_lds<FMT, WAVES, 1>(p, spw, s);
+}
+
+template <int FMT>
+St launch_gemv_lds(const GemvParams& p, int waves, uint32_t spw, int u, hipStream_t s) {
+  switch (waves) {
+    case 4: return launch_lds_u<FMT, 4>(p, spw, u, s);
+    case 8: return launch_lds_u<FMT, 8>(p, spw, u, s);
+    case 12: return launch_lds_u<FMT, 12>(p, spw, u, s);
+    default: return launch_lds_u<FMT, 16>(p, spw, u, s);
+  }
+}
+
 template <int FMT>
 St launch_gemv(const GemvParams& p, hipStream_t s) {
+  int lw, lu;
+  uint32_t lspw;
+  if (p.m <= kSmallM && pick_lds_split<FMT>(p.n, p.k, lw, lspw, lu) &&
+      small_m_lds<FMT>(p.m, lspw, lw) <= 160 * 1024)
+    return launch_gemv_lds<FMT>(p, lw, lspw, lu, s);
   const int waves = waves_for<FMT>(p.n);
   switch ((p.m + 15) / 16) {
     case 1: launch_mt<FMT, 1>(p, waves, s); break;
