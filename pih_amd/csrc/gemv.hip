@@ -322,9 +322,14 @@ struct ScaleVec {
 
 // Bytes of LDS the small-M kernel needs: per wave its x slice (rows < M,
 // spw steps) and U... per-group row sums, plus the reduction area.
+// W pairs of steps pass through a [16 rows][128 + 16 bytes] LDS tile per
+// pair (the 16-byte pad keeps the MFMA-layout reads conflict-free).
+constexpr uint32_t kWTileRow = 144, kWTile = 16 * kWTileRow;
+
 template <int FMT>
-constexpr uint32_t small_m_lds(uint32_t m, uint32_t spw, uint32_t waves) {
-  return waves * (m * spw * step_k<FMT>() * 2 + (FMT != kWBf16 ? spw * 16 * 4 : 0)) + waves * 4 * 64 * 4;
+constexpr uint32_t small_m_lds(uint32_t m, uint32_t spw, uint32_t waves, uint32_t u) {
+  const uint32_t wtile = u % 2 == 0 ? u / 2 * kWTile : 0;
+  return waves * (wtile + m * spw * step_k<FMT>() * 2 + (FMT != kWBf16 ? spw * 16 * 4 : 0)) + waves * 4 * 64 * 4;
 }
 
 template <int FMT, int WAVES, int U>
@@ -340,69 +345,115 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvParams p, uint
   const uint32_t s0 = wave * spw, s1 = s0 + spw;  // WAVES * spw == K / SK
   const uint32_t span = spw * SK;                 // this wave's K run
   const uint32_t zwords = (G + 7) / 8;
-  // wave-private LDS: x[M][span] bf16, then (INT4) row sums [spw][16] fp32
-  const uint32_t wave_bytes = M * span * 2 + (kInt4 ? spw * 16 * 4 : 0);
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem + wave * wave_bytes);
-  float* xsum = reinterpret_cast<float*>(smem + wave * wave_bytes + M * span * 2);
+  // Even U: W is loaded as whole 128-byte lines (8 rows x 128 B per load:
+  // two steps of eight rows) and turned into the MFMA layout (16 rows x
+  // 64 B per step) through an LDS tile.  Loading the MFMA layout directly
+  // touches 16 half lines per instruction and streamed ~17 % slower.
+  constexpr bool kT = U % 2 == 0;
+  constexpr uint32_t kWBytes = kT ? U / 2 * kWTile : 0;
+  // wave-private LDS: W tiles, x[M][span] bf16, then (INT4) row sums [spw][16]
+  const uint32_t wave_bytes = kWBytes + M * span * 2 + (kInt4 ? spw * 16 * 4 : 0);
+  uint8_t* wt = smem + wave * wave_bytes;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(wt + kWBytes);
+  float* xsum = reinterpret_cast<float*>(wt + kWBytes + M * span * 2);
   float* red = reinterpret_cast<float*>(smem + WAVES * wave_bytes);  // [WAVES][4][64]
 
   // ---- this wave's x slice: chunk c = (row m, 16-byte piece j of the run)
   const uint32_t row_chunks = span / 8, chunks = M * row_chunks;
+  // chunk -> (row m, piece j); M <= 4, so the row is a count of boundaries
+  auto row_of = [&](uint32_t c) -> uint32_t {
+    return (uint32_t)(c >= row_chunks) + (uint32_t)(c >= 2 * row_chunks) + (uint32_t)(c >= 3 * row_chunks);
+  };
   auto x_chunk = [&](uint32_t c) -> v4i {
-    const uint32_t m = c / row_chunks, j = c % row_chunks;
+    const uint32_t m = row_of(c), j = c - m * row_chunks;
     return *reinterpret_cast<const v4i*>(p.x + (uint64_t)m * K + s0 * SK + j * 8);
   };
+  // unconditional loads (lanes past the end repeat the last chunk): a load
+  // under a branch makes the compiler wait for it on the spot
   v4i xr[XR];
 #pragma unroll
-  for (int j = 0; j < XR; ++j) {
-    const uint32_t c = lane + 64 * j;
-    xr[j] = c < chunks ? x_chunk(c) : v4i{0, 0, 0, 0};
-  }
+  for (int j = 0; j < XR; ++j) xr[j] = x_chunk(min(lane + 64 * j, chunks - 1));
 
   // ---- first batch of W, its scales and zero points
   v4i wv[U];
   ScaleVec<U> sv;
   uint32_t zw = 0;
+  // scales and zero points go first: loads complete in issue order, so the
+  // math of step 0 then waits only for W[0], not for the whole batch
   auto issue = [&](uint32_t sb) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t k0 = (sb + u) * SK;
-      if constexpr (FMT == kWBf16)
-        wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * K + k0 + lg * 8);
-      else if constexpr (FMT == kWSym)
-        wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * (K / 2) + k0 / 2 + lg * 16);
-      else
-        wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * (K / 8) + k0 / 8 + lg * 4);
-    }
     if constexpr (kInt4) sv.load(p.scales + (uint64_t)nrow * G + sb);
     if constexpr (FMT == kWAsym) zw = p.zeros[(uint64_t)nrow * zwords + sb / 8];
+    if constexpr (kT) {
+      // load 2q + h: rows n0 + 8h + lane / 8, bytes [64 (sb + 2q), +128) of
+      // the row, 16 of them per lane
+      const uint8_t* wb = static_cast<const uint8_t*>(p.w);
+      const uint64_t row_bytes = kInt4 ? K / 2 : (uint64_t)K * 2;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t row = n0 + 8 * (u & 1) + lane / 8;
+        wv[u] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(
+            wb + (uint64_t)row * row_bytes + (uint64_t)(sb + (u & ~1)) * 64 + (lane % 8) * 16));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t k0 = (sb + u) * SK;
+        if constexpr (FMT == kWBf16)
+          wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * K + k0 + lg * 8);
+        else if constexpr (FMT == kWSym)
+          wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * (K / 2) + k0 / 2 + lg * 16);
+        else
+          wv[u] = nt_piece<FMT>(p.w, (uint64_t)nrow * (K / 8) + k0 / 8 + lg * 4);
+      }
+    }
+  };
+  // Even U: the line pair (loads u, u + 1 = rows 0-7 and 8-15 of steps u and
+  // u + 1) through the LDS tile into the MFMA layout of steps u and u + 1.
+  auto to_mfma_layout = [&](int u) {
+    if constexpr (kT) {
+      uint8_t* tile = wt + (u / 2) * kWTile;
+      *reinterpret_cast<v4i*>(tile + (lane / 8) * kWTileRow + (lane % 8) * 16) = wv[u];
+      *reinterpret_cast<v4i*>(tile + (8 + lane / 8) * kWTileRow + (lane % 8) * 16) = wv[u + 1];
+      wv[u] = *reinterpret_cast<const v4i*>(tile + lr * kWTileRow + lg * 16);
+      wv[u + 1] = *reinterpret_cast<const v4i*>(tile + lr * kWTileRow + 64 + lg * 16);
+    }
   };
   issue(s0);
+  // every load of the wave is in flight before anything waits on one
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- x to LDS; INT4: row sums of x per 128-group from the same registers
   // (16 lanes hold one group of one row: 16 chunks x 8 values)
+  // Branch-free on purpose: a value used only under a branch gets its load
+  // sunk into the branch, where the compiler then waits for every earlier
+  // load (the W batch included).  Lanes past the end rewrite the last chunk
+  // with its own value.
   auto stage = [&](uint32_t c, v4i v) {
     const bool live = c < chunks;
-    if (live) reinterpret_cast<v4i*>(xs)[c] = kInt4 ? x_in_nibble_order(v) : v;
+    const uint32_t cc = min(c, chunks - 1);
+    reinterpret_cast<v4i*>(xs)[cc] = kInt4 ? x_in_nibble_order(v) : v;
     if constexpr (kInt4) {
       float s = 0.0f;
-      if (live) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          s += __uint_as_float((uint32_t)v[q] << 16) + __uint_as_float((uint32_t)v[q] & 0xffff0000u);
-      }
+      for (int q = 0; q < 4; ++q)
+        s += __uint_as_float((uint32_t)v[q] << 16) + __uint_as_float((uint32_t)v[q] & 0xffff0000u);
+      s = live ? s : 0.0f;
       s += __shfl_xor(s, 1);
       s += __shfl_xor(s, 2);
       s += __shfl_xor(s, 4);
       s += __shfl_xor(s, 8);
-      if (live && (c & 15) == 0) xsum[((c % row_chunks) / 16) * 16 + c / row_chunks] = s;
+      if (live && (c & 15) == 0) {
+        const uint32_t m = row_of(c);
+        xsum[((c - m * row_chunks) / 16) * 16 + m] = s;
+      }
     }
   };
 #pragma unroll
-  for (int j = 0; j < XR; ++j) stage(lane + 64 * j, xr[j]);
+  for (int j = 0; j < XR; ++j)
+    if (64 * j < chunks) stage(lane + 64 * j, xr[j]);  // wave-uniform: skips rounds with no live chunk
   for (uint32_t base = 64 * XR; base < chunks; base += 64) {
     const uint32_t c = base + lane;
-    stage(c, c < chunks ? x_chunk(c) : v4i{0, 0, 0, 0});
+    stage(c, x_chunk(min(c, chunks - 1)));
   }
   // the wave reads back only what it wrote: no block barrier needed
 
@@ -413,6 +464,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvParams p, uint
   auto compute = [&](uint32_t sb) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if (u % 2 == 0) to_mfma_layout(u);
       const uint32_t st = sb + u;            // global step
       const uint32_t kl = (st - s0) * SK;    // k offset inside the wave's run
       if constexpr (FMT == kWBf16) {
@@ -543,7 +595,7 @@ void launch_mt(const GemvParams& p, int waves, hipStream_t s) {
 
 template <int FMT, int WAVES, int U>
 St launch_lds(const GemvParams& p, uint32_t spw, hipStream_t s) {
-  const uint32_t lds = small_m_lds<FMT>(p.m, spw, WAVES);
+  const uint32_t lds = small_m_lds<FMT>(p.m, spw, WAVES, U);
   static bool raised = false;  // LDS above 64 KB must be allowed once per kernel
   if (lds > 65536 && !raised) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_lds_kernel<FMT, WAVES, U>),
@@ -598,7 +650,7 @@ St launch_gemv(const GemvParams& p, hipStream_t s) {
   int lw, lu;
   uint32_t lspw;
   if (p.m <= kSmallM && pick_lds_split<FMT>(p.n, p.k, lw, lspw, lu) &&
-      small_m_lds<FMT>(p.m, lspw, lw) <= 160 * 1024)
+      small_m_lds<FMT>(p.m, lspw, lw, lu) <= 160 * 1024)
     return launch_gemv_lds<FMT>(p, lw, lspw, lu, s);
   const int waves = waves_for<FMT>(p.n);
   switch ((p.m + 15) / 16) {
