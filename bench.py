@@ -200,13 +200,39 @@ def bench_decode(torch, iters: int):
                 rs.append(r)
             return rs
 
+        # the same pass as a decode step can issue it with the grouped entry:
+        # [q, k, v] (one input), o, [gate, up] (one input), down
+        groups = [[0, 1, 2], [3], [4, 5], [6]]
+
+        def grouped_calls(i, stream, m=m, xs=xs, ys=ys, flag=flag):
+            keep = []
+            for g in groups:
+                k = QWEN8B[g[0]][2]
+                probs = (abi.W4A16_PROBLEM * len(g))()
+                for slot, j in enumerate(g):
+                    q, s, z = sets[i][j]
+                    pr = probs[slot]
+                    pr.input_bf16, pr.qweight, pr.scales, pr.zeros = ptr(xs[k]), ptr(q), ptr(s), ptr(z)
+                    pr.output_bf16, pr.n = ptr(ys[j]), QWEN8B[j][1]
+                r = abi.request(abi.LN["w4a16_grouped"], problems=abi.C.addressof(probs), error_flag_u32=ptr(flag),
+                                stream=stream, problem_count=len(g), m=m, k=k, format=abi.W4A16_ASYMMETRIC)
+                st = L.call("launch_w4a16_grouped", r)
+                if st.code != abi.OK:
+                    raise RuntimeError(f"w4a16 grouped launch: {st}")
+                keep.append((probs, r))
+            return keep
+
         reqs = [calls(i, stream_handle()) for i in range(nsets)]  # also the warm pass
         ms = _timed(torch, lambda i: [L.call("launch_w4a16_gemm", r) for r in reqs[i % nsets]], iters)
         ms_graph = _graphed(torch, calls, nsets, iters)
+        gkeep = [grouped_calls(i, stream_handle()) for i in range(nsets)]
+        ms_grp = _timed(torch, lambda i: [L.call("launch_w4a16_grouped", r) for _, r in gkeep[i % nsets]], iters)
+        ms_grp_graph = _graphed(torch, grouped_calls, nsets, iters)
         if int(flag.item()):
             raise RuntimeError(f"w4a16 error flag {int(flag.item())}")
         algo = set_bytes + sum(m * k * 2 + m * n * 2 for _, n, k in QWEN8B)
         out[f"w4a16_m{m}"] = _decode_line(ms, ms_graph, algo, nsets)
+        out[f"w4a16_m{m}_grouped"] = _decode_line(ms_grp, ms_grp_graph, algo, nsets, launches=len(groups))
     del sets
     # ---- BF16 decode, M = 1, 8, 64
     set_bytes = sum(n * k * 2 for _, n, k in QWEN8B)

@@ -39,7 +39,12 @@
  *   launch_w4a16_dequant   the INT4 unpack of the W4A16 GEMV on its own
  *                          (the reference's quantizer format,
  *                          plugins/offline-qwen/
- *                          qwen3_int4_reference_quantizer.cpp:30-108).
+ *                          qwen3_int4_reference_quantizer.cpp:30-108);
+ *   launch_w4a16_grouped   several launch_w4a16_gemm problems with one m
+ *                          and K in one launch (the Qwen decode step's
+ *                          q/k/v and gate/up projections each read the
+ *                          same input; the reference issues one launch per
+ *                          projection, qwen3_int4_gemm_plan.cpp:55-85).
  *
  * Conventions are those of the reference's pack tables: one request pointer
  * in, pih_status_v1 by value out; a NULL request, wrong struct_size or wrong
@@ -194,6 +199,25 @@ typedef struct pih_amd_w4a16_launch_v1 {
   uint32_t m, n, k, format;
 } pih_amd_w4a16_launch_v1;
 
+/* Several independent W4A16 GEMVs in one launch (for example q, k and v,
+ * or gate and up, of one decode step): problem i computes
+ * output_i[m, n_i] = input_i[m, k] . w_i^T exactly as
+ * pih_amd_w4a16_launch_v1 would, with one m, k and format for the whole
+ * group.  `problems` is a HOST pointer to problem_count (1..8) entries,
+ * read during the call (so a captured launch keeps its own copy). */
+#define PIH_AMD_W4A16_GROUP_MAX_V1 8U
+typedef struct pih_amd_w4a16_problem_v1 {
+  uintptr_t input_bf16, qweight, scales, zeros, output_bf16;
+  uint32_t n, reserved;
+} pih_amd_w4a16_problem_v1;
+
+typedef struct pih_amd_w4a16_grouped_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t problems; /* const pih_amd_w4a16_problem_v1* (host) */
+  uintptr_t error_flag_u32, stream;
+  uint32_t problem_count, m, k, format;
+} pih_amd_w4a16_grouped_launch_v1;
+
 /* Exact INT4 dequant, the unpack the W4A16 GEMV applies: output fp32
  * [N, K] with w = (q - z) * s (ASYMMETRIC) or q * s (SYMMETRIC); same
  * layouts and error codes as pih_amd_w4a16_launch_v1. */
@@ -240,6 +264,7 @@ typedef struct pih_amd_linear_kernels_api_v1 {
   pih_status_v1 (*launch_swiglu)(const pih_amd_swiglu_launch_v1*);
   pih_status_v1 (*launch_mxfp4_decode)(const pih_amd_mxfp4_decode_launch_v1*);
   pih_status_v1 (*launch_w4a16_dequant)(const pih_amd_w4a16_dequant_launch_v1*);
+  pih_status_v1 (*launch_w4a16_grouped)(const pih_amd_w4a16_grouped_launch_v1*);
 } pih_amd_linear_kernels_api_v1;
 
 #ifdef __cplusplus

@@ -212,12 +212,19 @@ LN["mxfp4_decode"] = _struct("Mxfp4Decode", _hdr(*_u("packed", "scales_ue8m0", "
                                                      "stream"), *_i("rows", "k")))
 LN["w4a16_dequant"] = _struct("W4a16Dequant", _hdr(*_u("qweight", "scales", "zeros", "output_f32", "error_flag_u32",
                                                       "stream"), *_i("n", "k", "format")))
+LN["w4a16_grouped"] = _struct("W4a16Grouped", _hdr(*_u("problems", "error_flag_u32", "stream"),
+                                                    *_i("problem_count", "m", "k", "format")))
+# pih_amd_w4a16_problem_v1: one entry of the grouped launch's host array
+W4A16_PROBLEM = _struct("W4a16Problem", _u("input_bf16", "qweight", "scales", "zeros", "output_bf16") +
+                        _i("n", "reserved"))
+W4A16_GROUP_MAX = 8
 LN_ORDER = [("query_workspace", "workspace_query"), ("launch_route_plan", "route_plan"),
             ("launch_fp8_quant", "fp8_quant"), ("launch_fp8_gemm", "fp8_gemm"),
             ("launch_moe_fp8_gemm", "moe_fp8_gemm"), ("launch_moe_mxfp4_gemm", "moe_mxfp4_gemm"),
             ("launch_moe_combine", "moe_combine"), ("launch_bf16_gemm", "bf16_gemm"),
             ("launch_w4a16_gemm", "w4a16"), ("launch_silu_mul", "silu_mul"), ("launch_swiglu", "swiglu"),
-            ("launch_mxfp4_decode", "mxfp4_decode"), ("launch_w4a16_dequant", "w4a16_dequant")]
+            ("launch_mxfp4_decode", "mxfp4_decode"), ("launch_w4a16_dequant", "w4a16_dequant"),
+            ("launch_w4a16_grouped", "w4a16_grouped")]
 LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_version", U32),
                                          ("identity", C.POINTER(Identity))] +
                  [(f, C.CFUNCTYPE(Status, C.POINTER(LN[s]))) for f, s in LN_ORDER])

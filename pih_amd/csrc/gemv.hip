@@ -332,15 +332,36 @@ constexpr uint32_t small_m_lds(uint32_t m, uint32_t spw, uint32_t waves, uint32_
   return waves * (wtile + m * spw * step_k<FMT>() * 2 + (FMT != kWBf16 ? spw * 16 * 4 : 0)) + waves * 4 * 64 * 4;
 }
 
+// Up to kMaxGroup independent problems with the same m and K share one
+// launch (the blocks of problem i are block_start[i] .. block_start[i+1]-1);
+// a single GEMV is a group of one.
+constexpr int kMaxGroup = 8;
+struct GemvGroup {
+  GemvParams prob[kMaxGroup];
+  uint32_t block_start[kMaxGroup + 1];
+  uint32_t count;
+};
+
 template <int FMT, int WAVES, int U>
-__global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvParams p, uint32_t spw) {
+__global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uint32_t spw) {
   extern __shared__ __align__(16) uint8_t smem[];
+  // this block's problem: selected field by field with constant indices
+  // (indexing the by-value argument with a variable would copy it to scratch)
+  uint32_t pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGroup; ++i)
+    if ((uint32_t)i < grp.count && blockIdx.x >= grp.block_start[i]) pi = i;
+  GemvParams p = grp.prob[0];
+#pragma unroll
+  for (int i = 1; i < kMaxGroup; ++i)
+    if (pi == (uint32_t)i) p = grp.prob[i];
+  const uint32_t block = blockIdx.x - grp.block_start[pi];
   constexpr bool kInt4 = FMT != kWBf16;
   constexpr uint32_t SK = step_k<FMT>();
   constexpr int XR = 8;  // x chunks per lane loaded ahead of the weights (M * spw * 16 <= 512)
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
-  const uint32_t n0 = blockIdx.x * 16, nrow = n0 + lr;
+  const uint32_t n0 = block * 16, nrow = n0 + lr;
   const uint32_t K = p.k, M = p.m, G = K / 128;
   const uint32_t s0 = wave * spw, s1 = s0 + spw;  // WAVES * spw == K / SK
   const uint32_t span = spw * SK;                 // this wave's K run
@@ -594,8 +615,8 @@ void launch_mt(const GemvParams& p, int waves, hipStream_t s) {
 }
 
 template <int FMT, int WAVES, int U>
-St launch_lds(const GemvParams& p, uint32_t spw, hipStream_t s) {
-  const uint32_t lds = small_m_lds<FMT>(p.m, spw, WAVES, U);
+St launch_lds(const GemvGroup& g, uint32_t spw, hipStream_t s) {
+  const uint32_t lds = small_m_lds<FMT>(g.prob[0].m, spw, WAVES, U);
   static bool raised = false;  // LDS above 64 KB must be allowed once per kernel
   if (lds > 65536 && !raised) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_lds_kernel<FMT, WAVES, U>),
@@ -603,7 +624,8 @@ St launch_lds(const GemvParams& p, uint32_t spw, hipStream_t s) {
       return Internal("gemv_lds_attribute_failed");
     raised = true;
   }
-  hipLaunchKernelGGL((gemv_lds_kernel<FMT, WAVES, U>), dim3(p.n / 16), dim3(WAVES * 64), lds, s, p, spw);
+  hipLaunchKernelGGL((gemv_lds_kernel<FMT, WAVES, U>), dim3(g.block_start[g.count]), dim3(WAVES * 64), lds, s, g,
+                     spw);
   return AfterLaunch("gemv_launch_failed");
 }
 
@@ -613,8 +635,8 @@ St launch_lds(const GemvParams& p, uint32_t spw, hipStream_t s) {
 // divides), with U the largest of 8, 4, 2, 1 dividing the steps per wave.
 // Returns false when no split divides the steps.
 template <int FMT>
-bool pick_lds_split(uint32_t n, uint32_t k, int& waves, uint32_t& spw, int& u) {
-  const uint32_t steps = k / step_k<FMT>(), rowblks = n / 16;
+bool pick_lds_split(uint32_t rowblks, uint32_t k, int& waves, uint32_t& spw, int& u) {
+  const uint32_t steps = k / step_k<FMT>();
   waves = 0;
   for (int w : {4, 8, 12, 16}) {
     if (steps % (uint32_t)w) continue;
@@ -628,30 +650,47 @@ bool pick_lds_split(uint32_t n, uint32_t k, int& waves, uint32_t& spw, int& u) {
 }
 
 template <int FMT, int WAVES>
-St launch_lds_u(const GemvParams& p, uint32_t spw, int u, hipStream_t s) {
-  if (u == 8) return launch_lds<FMT, WAVES, 8>(p, spw, s);
-  if (u == 4) return launch_lds<FMT, WAVES, 4>(p, spw, s);
-  if (u == 2) return launch_lds<FMT, WAVES, 2>(p, spw, s);
-  return launch_lds<FMT, WAVES, 1>(p, spw, s);
+St launch_lds_u(const GemvGroup& g, uint32_t spw, int u, hipStream_t s) {
+  if (u == 8) return launch_lds<FMT, WAVES, 8>(g, spw, s);
+  if (u == 4) return launch_lds<FMT, WAVES, 4>(g, spw, s);
+  if (u == 2) return launch_lds<FMT, WAVES, 2>(g, spw, s);
+  return launch_lds<FMT, WAVES, 1>(g, spw, s);
 }
 
+// The small-M path for a group (every problem has the same m and k);
+// returns false in `taken` when the shape has no even split (the caller
+// then uses gemv_kernel per problem).
 template <int FMT>
-St launch_gemv_lds(const GemvParams& p, int waves, uint32_t spw, int u, hipStream_t s) {
+St launch_group_lds(const GemvGroup& g, hipStream_t s, bool& taken) {
+  taken = false;
+  const GemvParams& p = g.prob[0];
+  int waves, u;
+  uint32_t spw;
+  if (p.m > kSmallM || !pick_lds_split<FMT>(g.block_start[g.count], p.k, waves, spw, u) ||
+      small_m_lds<FMT>(p.m, spw, waves, u) > 160 * 1024)
+    return Ok();
+  taken = true;
   switch (waves) {
-    case 4: return launch_lds_u<FMT, 4>(p, spw, u, s);
-    case 8: return launch_lds_u<FMT, 8>(p, spw, u, s);
-    case 12: return launch_lds_u<FMT, 12>(p, spw, u, s);
-    default: return launch_lds_u<FMT, 16>(p, spw, u, s);
+    case 4: return launch_lds_u<FMT, 4>(g, spw, u, s);
+    case 8: return launch_lds_u<FMT, 8>(g, spw, u, s);
+    case 12: return launch_lds_u<FMT, 12>(g, spw, u, s);
+    default: return launch_lds_u<FMT, 16>(g, spw, u, s);
   }
+}
+
+GemvGroup single(const GemvParams& p) {
+  GemvGroup g{};
+  g.prob[0] = p;
+  g.count = 1;
+  g.block_start[1] = p.n / 16;
+  return g;
 }
 
 template <int FMT>
 St launch_gemv(const GemvParams& p, hipStream_t s) {
-  int lw, lu;
-  uint32_t lspw;
-  if (p.m <= kSmallM && pick_lds_split<FMT>(p.n, p.k, lw, lspw, lu) &&
-      small_m_lds<FMT>(p.m, lspw, lw, lu) <= 160 * 1024)
-    return launch_gemv_lds<FMT>(p, lw, lspw, lu, s);
+  bool taken;
+  const St st = launch_group_lds<FMT>(single(p), s, taken);
+  if (taken) return st;
   const int waves = waves_for<FMT>(p.n);
   switch ((p.m + 15) / 16) {
     case 1: launch_mt<FMT, 1>(p, waves, s); break;
@@ -718,6 +757,44 @@ St LaunchW4a16(const W4a16Args& a) {
   if (a.symmetric)
     return launch_gemv<kWSym>(p, a.stream);
   return launch_gemv<kWAsym>(p, a.stream);
+}
+
+St LaunchW4a16Grouped(const W4a16Args* probs, uint32_t count) {
+  if (!probs || count == 0 || count > (uint32_t)kMaxGroup) return Invalid("w4a16_group_size_invalid");
+  const W4a16Args& a0 = probs[0];
+  if (!a0.error_flag || !a0.stream) return Invalid("w4a16_null_argument");
+  if (a0.m == 0 || a0.m > 64 || a0.k == 0 || a0.k % 128) return Invalid("w4a16_shape_invalid");
+  GemvGroup g{};
+  g.count = count;
+  for (uint32_t i = 0; i < count; ++i) {
+    const W4a16Args& a = probs[i];
+    if (!a.x || !a.qweight || !a.scales || !a.out) return Invalid("w4a16_null_argument");
+    if (!a.symmetric && !a.zeros) return Invalid("w4a16_zeros_missing");
+    if (a.m != a0.m || a.k != a0.k || a.symmetric != a0.symmetric || a.n == 0 || a.n % 16)
+      return Invalid("w4a16_group_shape_invalid");
+    GemvParams& p = g.prob[i];
+    p.x = a.x;
+    p.w = a.qweight;
+    p.scales = a.scales;
+    p.zeros = a.zeros;
+    p.out = a.out;
+    p.err = a0.error_flag;
+    p.m = a.m;
+    p.n = a.n;
+    p.k = a.k;
+    g.block_start[i + 1] = g.block_start[i] + a.n / 16;
+  }
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  bool taken;
+  const St st = a0.symmetric ? launch_group_lds<kWSym>(g, a0.stream, taken)
+                             : launch_group_lds<kWAsym>(g, a0.stream, taken);
+  if (taken) return st;
+  for (uint32_t i = 0; i < count; ++i) {  // shapes without the small-M path: one launch each
+    const St one = a0.symmetric ? launch_gemv<kWSym>(g.prob[i], a0.stream) : launch_gemv<kWAsym>(g.prob[i], a0.stream);
+    if (!one.ok()) return one;
+  }
+  return Ok();
 }
 
 St LaunchW4a16Dequant(const W4a16Args& a, float* out) {

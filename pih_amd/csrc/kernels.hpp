@@ -128,6 +128,9 @@ struct W4a16Args {
   bool symmetric = false;
 };
 St LaunchW4a16(const W4a16Args& a);
+// up to 8 problems with one m, k and format in one launch (x, qweight,
+// scales, zeros, out and n per problem; the rest from probs[0])
+St LaunchW4a16Grouped(const W4a16Args* probs, uint32_t count);
 uint64_t W4a16WorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
 // exact dequant (q - z) * s (or q * s) to fp32 [n, k]
 St LaunchW4a16Dequant(const W4a16Args& a, float* out);

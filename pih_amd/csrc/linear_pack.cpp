@@ -217,6 +217,30 @@ St W4a16(const pih_amd_w4a16_launch_v1* r) {
   return LaunchW4a16(a);
 }
 
+St W4a16Grouped(const pih_amd_w4a16_grouped_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) ||
+      (r->format != PIH_AMD_W4A16_SYMMETRIC_V1 && r->format != PIH_AMD_W4A16_ASYMMETRIC_V1))
+    return Invalid("w4a16_grouped_request_invalid");
+  if (!r->problems || r->problem_count == 0 || r->problem_count > PIH_AMD_W4A16_GROUP_MAX_V1)
+    return Invalid("w4a16_grouped_problem_count_invalid");
+  const auto* probs = Ptr<const pih_amd_w4a16_problem_v1>(r->problems);
+  W4a16Args a[PIH_AMD_W4A16_GROUP_MAX_V1];
+  for (uint32_t i = 0; i < r->problem_count; ++i) {
+    a[i].x = Ptr<const uint16_t>(probs[i].input_bf16);
+    a[i].qweight = Ptr<const void>(probs[i].qweight);
+    a[i].scales = Ptr<const uint16_t>(probs[i].scales);
+    a[i].zeros = Ptr<const uint32_t>(probs[i].zeros);
+    a[i].out = Ptr<uint16_t>(probs[i].output_bf16);
+    a[i].error_flag = Ptr<uint32_t>(r->error_flag_u32);
+    a[i].stream = AsStream(r->stream);
+    a[i].m = r->m;
+    a[i].n = probs[i].n;
+    a[i].k = r->k;
+    a[i].symmetric = r->format == PIH_AMD_W4A16_SYMMETRIC_V1;
+  }
+  return LaunchW4a16Grouped(a, r->problem_count);
+}
+
 St SiluMul(const pih_amd_silu_mul_launch_v1* r) {
   if (!HeaderOk(r, kAbi)) return Invalid("silu_mul_request_invalid");
   SiluMulArgs a;
@@ -285,11 +309,12 @@ PIH_AMD_CONTAINED(CSiluMul, SiluMul, pih_amd_silu_mul_launch_v1)
 PIH_AMD_CONTAINED(CSwiGlu, SwiGlu, pih_amd_swiglu_launch_v1)
 PIH_AMD_CONTAINED(CMxfp4Decode, Mxfp4Decode, pih_amd_mxfp4_decode_launch_v1)
 PIH_AMD_CONTAINED(CW4a16Dequant, W4a16Dequant, pih_amd_w4a16_dequant_launch_v1)
+PIH_AMD_CONTAINED(CW4a16Grouped, W4a16Grouped, pih_amd_w4a16_grouped_launch_v1)
 
 const pih_amd_linear_kernels_api_v1 kContract = {
     sizeof(pih_amd_linear_kernels_api_v1), kAbi, &kIdentity, &CQueryWorkspace, &CRoutePlan,
     &CFp8Quant, &CFp8Gemm, &CMoeFp8Gemm, &CMoeMxfp4Gemm, &CMoeCombine, &CBf16Gemm, &CW4a16,
-    &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant};
+    &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant, &CW4a16Grouped};
 
 pih_status_v1 BindOrigin(const char* path) noexcept {
   return ToAbi(path && path[0] == '/' ? Ok() : Invalid("bind_origin_path_not_absolute"));

@@ -145,6 +145,68 @@ def test_w4a16_asym(eng, m, n, k):
     assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref), f"w4a16 asym {m}x{n}x{k}")
 
 
+def _w4a16_grouped(xs, weights, fmt, m, k):
+    """weights: list of (q, s, z, n); xs: list of bf16 inputs [m, k]."""
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    keep, outs = [], []
+    probs = (abi.W4A16_PROBLEM * len(weights))()
+    for i, ((q, s, z, n), x) in enumerate(zip(weights, xs)):
+        xd, qd, sd = to_dev(x), to_dev(q), to_dev(s)
+        zd = to_dev(z) if z is not None else None
+        out = torch.full((m, n), 0x7E7E, dtype=torch.int16, device="cuda").view(torch.bfloat16)
+        keep += [xd, qd, sd, zd]
+        outs.append(out)
+        probs[i].input_bf16, probs[i].qweight, probs[i].scales = ptr(xd), ptr(qd), ptr(sd)
+        probs[i].zeros, probs[i].output_bf16, probs[i].n = ptr(zd), ptr(out), n
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    r = abi.request(abi.LN["w4a16_grouped"], problems=abi.C.addressof(probs), error_flag_u32=ptr(flag),
+                    stream=stream_handle(), problem_count=len(weights), m=m, k=k, format=fmt)
+    st = abi.linear_pack().call("launch_w4a16_grouped", r)
+    assert st.code == abi.OK, st
+    _sync()
+    return [to_host(o) for o in outs], _flag(flag)
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_w4a16_grouped_qkv_and_gate_up(eng, m):
+    """q/k/v and gate/up of Qwen3-8B as two grouped launches (one input per
+    problem); each output against the oracle's strict-k sum.  m = 16 takes
+    the per-problem fallback path."""
+    k = 4096
+    for ns in ((4096, 1024, 1024), (12288, 12288)):
+        weights = [synth.int4_asym_weight(synth.config_seed(3, 3000 + i + n), n, k) + (n,) for i, n in enumerate(ns)]
+        xs = [synth.bf16_normal(synth.config_seed(3, 3100 + i + m), (m, k)) for i in range(len(ns))]
+        got, flag = _w4a16_grouped(xs, weights, abi.W4A16_ASYMMETRIC, m, k)
+        assert flag == 0
+        for (q, s, z, n), x, g in zip(weights, xs, got):
+            ref = oracle.w4a16_asym(x, q, s, z)
+            assert_close(oracle.bf16_bits_to_f32(g), oracle.bf16_bits_to_f32(ref), f"grouped w4a16 {m}x{n}x{k}")
+
+
+def test_w4a16_grouped_symmetric_and_errors(eng):
+    """Reference format in a group of three; a bad scale in the last problem
+    raises code 13 while the other problems still match the oracle."""
+    m, k = 1, 2048
+    ns = (1024, 2048, 256)
+    weights = [synth.int4_sym_weight(synth.config_seed(3, 3200 + n), n, k) + (None, n) for n in ns]
+    xs = [synth.bf16_normal(synth.config_seed(3, 3300 + i), (m, k)) for i in range(3)]
+    got, flag = _w4a16_grouped(xs, weights, abi.W4A16_SYMMETRIC, m, k)
+    assert flag == 0
+    for (q, s, _, n), x, g in zip(weights, xs, got):
+        assert_close(oracle.bf16_bits_to_f32(g), oracle.bf16_bits_to_f32(oracle.w4a16_sym(x, q, s)), "grouped sym")
+    q, s, z, n = weights[2]
+    s = s.copy()
+    s[7, 3] = 0xBC00  # -1.0
+    weights[2] = (q, s, z, n)
+    got, flag = _w4a16_grouped(xs, weights, abi.W4A16_SYMMETRIC, m, k)
+    assert flag == 13
+    for (q, s, _, n), x, g in list(zip(weights, xs, got))[:2]:
+        assert_close(oracle.bf16_bits_to_f32(g), oracle.bf16_bits_to_f32(oracle.w4a16_sym(x, q, s)), "grouped sym")
+
+
 @pytest.mark.parametrize("n,k", [(1024, 4096), (256, 1024)])
 def test_w4a16_asym_dequant_bit_exact(eng, n, k):
     q, s, z = synth.int4_asym_weight(synth.config_seed(3, 99 + n), n, k)

@@ -51,6 +51,7 @@ def _layout_program():
     emit("ds_api", "pih_deepseek_kernels_api_v1", [f[0] for f in abi.DS_API._fields_])
     emit("ln_api", "pih_amd_linear_kernels_api_v1", [f[0] for f in abi.LN_API._fields_])
     emit("qwen_api", "pih_qwen_kernels_api_v1", [f[0] for f in abi.QWEN_API._fields_])
+    emit("w4a16_problem", "pih_amd_w4a16_problem_v1", [f[0] for f in abi.W4A16_PROBLEM._fields_])
     lines += ['printf("}\\n");', "return 0; }"]
     return "\n".join(lines)
 
@@ -70,7 +71,8 @@ def test_c_struct_layouts_match_ctypes_mirror():
     want = {"ds." + n: mirror(t) for n, t in abi.DS.items()}
     want.update({"ln." + n: mirror(t) for n, t in abi.LN.items()})
     want.update(status=mirror(abi.Status), identity=mirror(abi.Identity), api=mirror(abi.PackApi),
-                ds_api=mirror(abi.DS_API), ln_api=mirror(abi.LN_API), qwen_api=mirror(abi.QWEN_API))
+                ds_api=mirror(abi.DS_API), ln_api=mirror(abi.LN_API), qwen_api=mirror(abi.QWEN_API),
+                w4a16_problem=mirror(abi.W4A16_PROBLEM))
     assert got == want
     assert got["status"][0] == 268
     assert len(abi.DS_ORDER) == 29
@@ -183,3 +185,30 @@ def test_linear_entries_reject_bad_requests():
     assert ln.call("query_workspace", w).code == abi.OK and out[0] > 0
     w.kind = 77
     assert ln.call("query_workspace", w).code == abi.INVALID_ARGUMENT
+
+
+def test_w4a16_grouped_rejects_bad_groups():
+    """Group validation happens before any device work: count 0 or above 8,
+    a NULL problem array, n not a multiple of 16 or a missing zeros pointer
+    in the asymmetric format are INVALID_ARGUMENT."""
+    ln = abi.linear_pack()
+    probs = (abi.W4A16_PROBLEM * 9)()
+    for p in probs:
+        p.input_bf16 = p.qweight = p.scales = p.zeros = p.output_bf16 = 0x1000
+        p.n = 256
+    r = abi.request(abi.LN["w4a16_grouped"], problems=C.addressof(probs), error_flag_u32=0x1000, stream=0x2000,
+                    problem_count=0, m=1, k=4096, format=abi.W4A16_ASYMMETRIC)
+    assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
+    r.problem_count = 9
+    assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
+    r.problem_count = 3
+    r.problems = 0
+    assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
+    r.problems = C.addressof(probs)
+    probs[1].n = 200
+    assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
+    probs[1].n = 256
+    probs[2].zeros = 0
+    assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
+    r.format = 7
+    assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
