@@ -40,6 +40,11 @@
  *                          (the reference's quantizer format,
  *                          plugins/offline-qwen/
  *                          qwen3_int4_reference_quantizer.cpp:30-108);
+ *   query_moe_layer_workspace, launch_moe_layer
+ *                          DeepSeekExpertCudaBackend::submit's whole
+ *                          per-expert loop (cuda/deepseek_expert_cuda_
+ *                          backend.cpp:23-103) as one host call that
+ *                          enqueues the six grouped stages above;
  *   launch_w4a16_grouped   several launch_w4a16_gemm problems with one m
  *                          and K in one launch (the Qwen decode step's
  *                          q/k/v and gate/up projections each read the
@@ -218,6 +223,36 @@ typedef struct pih_amd_w4a16_grouped_launch_v1 {
   uint32_t problem_count, m, k, format;
 } pih_amd_w4a16_grouped_launch_v1;
 
+/* One MoE expert layer per call, enqueued on `stream` with no host wait:
+ * route plan -> activation quant -> grouped gate/up GEMM with the SwiGLU x
+ * route-weight epilogue -> intermediate quant -> grouped down GEMM ->
+ * ordered combine (+ shared).  The output equals launching those entries
+ * one by one in that order.
+ * FP8 weights: w13 e4m3 [E][2I][H] (gate rows, then up rows), w13_scale
+ *   [E][2I/128][H/128], w2 e4m3 [E][H][I], w2_scale [E][H/128][I/128];
+ *   scale_format applies to weights and activations.
+ * MXFP4 weights: w13 e2m1 [E][2I][H/2], UE8M0 [E][2I][H/32]; w2 e2m1
+ *   [E][H][I/2], UE8M0 [E][H][I/32]; activation_type e4m3 (UE8M0 per 128)
+ *   or bf16 (no quant stages).
+ * Scratch: query_moe_layer_workspace writes the byte count to
+ * *required_bytes_u64 (a host address); launch_moe_layer needs at least
+ * that much in `workspace`.  Error bits are those of the stage entries. */
+#define PIH_AMD_WEIGHT_FP8_V1 1U
+#define PIH_AMD_WEIGHT_MXFP4_V1 2U
+typedef struct pih_amd_moe_layer_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t input_bf16, topk_ids_u32, topk_weights_f32;
+  uintptr_t w13, w13_scale, w2, w2_scale;
+  uintptr_t shared_bf16, output_bf16;
+  uintptr_t workspace;
+  uint64_t workspace_bytes;
+  uintptr_t required_bytes_u64;
+  uintptr_t error_flag_u32, stream;
+  uint32_t token_count, top_k, expert_count, hidden_size, intermediate_size;
+  uint32_t weight_format, scale_format, activation_type;
+  float swiglu_limit;
+} pih_amd_moe_layer_launch_v1;
+
 /* Exact INT4 dequant, the unpack the W4A16 GEMV applies: output fp32
  * [N, K] with w = (q - z) * s (ASYMMETRIC) or q * s (SYMMETRIC); same
  * layouts and error codes as pih_amd_w4a16_launch_v1. */
@@ -265,6 +300,8 @@ typedef struct pih_amd_linear_kernels_api_v1 {
   pih_status_v1 (*launch_mxfp4_decode)(const pih_amd_mxfp4_decode_launch_v1*);
   pih_status_v1 (*launch_w4a16_dequant)(const pih_amd_w4a16_dequant_launch_v1*);
   pih_status_v1 (*launch_w4a16_grouped)(const pih_amd_w4a16_grouped_launch_v1*);
+  pih_status_v1 (*query_moe_layer_workspace)(const pih_amd_moe_layer_launch_v1*);
+  pih_status_v1 (*launch_moe_layer)(const pih_amd_moe_layer_launch_v1*);
 } pih_amd_linear_kernels_api_v1;
 
 #ifdef __cplusplus

@@ -214,6 +214,14 @@ LN["w4a16_dequant"] = _struct("W4a16Dequant", _hdr(*_u("qweight", "scales", "zer
                                                       "stream"), *_i("n", "k", "format")))
 LN["w4a16_grouped"] = _struct("W4a16Grouped", _hdr(*_u("problems", "error_flag_u32", "stream"),
                                                     *_i("problem_count", "m", "k", "format")))
+LN["moe_layer"] = _struct("MoeLayer", _hdr(*_u("input_bf16", "topk_ids_u32", "topk_weights_f32", "w13", "w13_scale",
+                                             "w2", "w2_scale", "shared_bf16", "output_bf16", "workspace"),
+                                          ("workspace_bytes", U64), *_u("required_bytes_u64", "error_flag_u32",
+                                                                        "stream"),
+                                          *_i("token_count", "top_k", "expert_count", "hidden_size",
+                                              "intermediate_size", "weight_format", "scale_format",
+                                              "activation_type"), ("swiglu_limit", F32)))
+WEIGHT_FP8, WEIGHT_MXFP4 = 1, 2
 # pih_amd_w4a16_problem_v1: one entry of the grouped launch's host array
 W4A16_PROBLEM = _struct("W4a16Problem", _u("input_bf16", "qweight", "scales", "zeros", "output_bf16") +
                         _i("n", "reserved"))
@@ -224,7 +232,8 @@ LN_ORDER = [("query_workspace", "workspace_query"), ("launch_route_plan", "route
             ("launch_moe_combine", "moe_combine"), ("launch_bf16_gemm", "bf16_gemm"),
             ("launch_w4a16_gemm", "w4a16"), ("launch_silu_mul", "silu_mul"), ("launch_swiglu", "swiglu"),
             ("launch_mxfp4_decode", "mxfp4_decode"), ("launch_w4a16_dequant", "w4a16_dequant"),
-            ("launch_w4a16_grouped", "w4a16_grouped")]
+            ("launch_w4a16_grouped", "w4a16_grouped"), ("query_moe_layer_workspace", "moe_layer"),
+            ("launch_moe_layer", "moe_layer")]
 LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_version", U32),
                                          ("identity", C.POINTER(Identity))] +
                  [(f, C.CFUNCTYPE(Status, C.POINTER(LN[s]))) for f, s in LN_ORDER])

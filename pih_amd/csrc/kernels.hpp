@@ -185,6 +185,32 @@ struct CombineArgs {
 };
 St LaunchMoeCombine(const CombineArgs& a);
 
+// One MoE expert layer (route plan -> quant -> gate/up -> quant -> down ->
+// combine) on the caller's stream; moe_layer.cpp.
+enum WeightFmt : uint32_t { kWeightFp8 = 1, kWeightMxfp4 = 2 };
+struct MoeLayerArgs {
+  const uint16_t* x = nullptr;          // bf16 [tokens, hidden]
+  const uint32_t* topk_ids = nullptr;   // [tokens, topk]
+  const float* topk_weights = nullptr;  // [tokens, topk]
+  const void* w13 = nullptr;            // fp8 [E][2I][H] or e2m1 [E][2I][H/2]
+  const void* w13_scale = nullptr;      // fp8 [E][2I/128][H/128]; mxfp4 UE8M0 [E][2I][H/32]
+  const void* w2 = nullptr;             // fp8 [E][H][I] or e2m1 [E][H][I/2]
+  const void* w2_scale = nullptr;
+  const uint16_t* shared = nullptr;     // bf16 [tokens, hidden] or null
+  uint16_t* out = nullptr;              // bf16 [tokens, hidden]
+  void* workspace = nullptr;
+  uint64_t workspace_bytes = 0;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t tokens = 0, topk = 0, experts = 0, hidden = 0, inter = 0;
+  WeightFmt weight_format = kWeightFp8;
+  ScaleFmt scale_fmt = kScaleF32;  // FP8 weights and their activations
+  ActKind act = kActE4m3;          // MXFP4 weights: e4m3 (UE8M0) or bf16 activations
+  float swiglu_limit = 0.0f;
+};
+uint64_t MoeLayerWorkspaceBytes(const MoeLayerArgs& a);  // 0 for an invalid shape
+St LaunchMoeLayer(const MoeLayerArgs& a);
+
 struct FinalizeArgs {
   const float* acc = nullptr;
   const uint16_t* shared = nullptr;

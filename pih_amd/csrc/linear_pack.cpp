@@ -241,6 +241,46 @@ St W4a16Grouped(const pih_amd_w4a16_grouped_launch_v1* r) {
   return LaunchW4a16Grouped(a, r->problem_count);
 }
 
+MoeLayerArgs LayerArgs(const pih_amd_moe_layer_launch_v1* r) {
+  MoeLayerArgs a;
+  a.x = Ptr<const uint16_t>(r->input_bf16);
+  a.topk_ids = Ptr<const uint32_t>(r->topk_ids_u32);
+  a.topk_weights = Ptr<const float>(r->topk_weights_f32);
+  a.w13 = Ptr<const void>(r->w13);
+  a.w13_scale = Ptr<const void>(r->w13_scale);
+  a.w2 = Ptr<const void>(r->w2);
+  a.w2_scale = Ptr<const void>(r->w2_scale);
+  a.shared = Ptr<const uint16_t>(r->shared_bf16);
+  a.out = Ptr<uint16_t>(r->output_bf16);
+  a.workspace = Ptr<void>(r->workspace);
+  a.workspace_bytes = r->workspace_bytes;
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.tokens = r->token_count;
+  a.topk = r->top_k;
+  a.experts = r->expert_count;
+  a.hidden = r->hidden_size;
+  a.inter = r->intermediate_size;
+  a.weight_format = (WeightFmt)r->weight_format;
+  a.scale_fmt = (ScaleFmt)r->scale_format;
+  a.act = (ActKind)r->activation_type;
+  a.swiglu_limit = r->swiglu_limit;
+  return a;
+}
+
+St QueryMoeLayer(const pih_amd_moe_layer_launch_v1* r) {
+  if (!HeaderOk(r, kAbi) || !r->required_bytes_u64) return Invalid("moe_layer_query_invalid");
+  const uint64_t bytes = MoeLayerWorkspaceBytes(LayerArgs(r));
+  if (bytes == 0) return Invalid("moe_layer_shape_invalid");
+  *Ptr<uint64_t>(r->required_bytes_u64) = bytes;
+  return Ok();
+}
+
+St MoeLayer(const pih_amd_moe_layer_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("moe_layer_request_invalid");
+  return LaunchMoeLayer(LayerArgs(r));
+}
+
 St SiluMul(const pih_amd_silu_mul_launch_v1* r) {
   if (!HeaderOk(r, kAbi)) return Invalid("silu_mul_request_invalid");
   SiluMulArgs a;
@@ -310,11 +350,13 @@ PIH_AMD_CONTAINED(CSwiGlu, SwiGlu, pih_amd_swiglu_launch_v1)
 PIH_AMD_CONTAINED(CMxfp4Decode, Mxfp4Decode, pih_amd_mxfp4_decode_launch_v1)
 PIH_AMD_CONTAINED(CW4a16Dequant, W4a16Dequant, pih_amd_w4a16_dequant_launch_v1)
 PIH_AMD_CONTAINED(CW4a16Grouped, W4a16Grouped, pih_amd_w4a16_grouped_launch_v1)
+PIH_AMD_CONTAINED(CQueryMoeLayer, QueryMoeLayer, pih_amd_moe_layer_launch_v1)
+PIH_AMD_CONTAINED(CMoeLayer, MoeLayer, pih_amd_moe_layer_launch_v1)
 
 const pih_amd_linear_kernels_api_v1 kContract = {
     sizeof(pih_amd_linear_kernels_api_v1), kAbi, &kIdentity, &CQueryWorkspace, &CRoutePlan,
     &CFp8Quant, &CFp8Gemm, &CMoeFp8Gemm, &CMoeMxfp4Gemm, &CMoeCombine, &CBf16Gemm, &CW4a16,
-    &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant, &CW4a16Grouped};
+    &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant, &CW4a16Grouped, &CQueryMoeLayer, &CMoeLayer};
 
 pih_status_v1 BindOrigin(const char* path) noexcept {
   return ToAbi(path && path[0] == '/' ? Ok() : Invalid("bind_origin_path_not_absolute"));

@@ -240,3 +240,37 @@ class MoeFp8Layer:
         _check(st, "moe_combine")
         mark(6)
         return self.out
+
+
+class MoeLayer:
+    """One MoE expert layer per call through the pack's C++ layer entry
+    (``launch_moe_layer``): the six stages of ``MoeFp8Layer`` enqueued by the
+    native host code, for FP8 or MXFP4 weights.  Scratch is sized once with
+    ``query_moe_layer_workspace`` and allocated at construction."""
+
+    def __init__(self, w13, w13_scale, w2, w2_scale, tokens: int, topk: int, weight_format: int = abi.WEIGHT_FP8,
+                 scale_format: int = abi.SCALE_F32, activation_type: int = abi.ACTIVATION_E4M3,
+                 swiglu_limit: float = 0.0):
+        self.w13, self.w13_scale, self.w2, self.w2_scale = w13, w13_scale, w2, w2_scale
+        self.experts, n13, k13 = w13.shape
+        self.hidden = k13 if weight_format == abi.WEIGHT_FP8 else 2 * k13
+        self.inter = n13 // 2
+        self.tokens, self.topk = tokens, topk
+        self.fields = dict(token_count=tokens, top_k=topk, expert_count=self.experts, hidden_size=self.hidden,
+                           intermediate_size=self.inter, weight_format=weight_format, scale_format=scale_format,
+                           activation_type=activation_type, swiglu_limit=swiglu_limit)
+        need = (abi.C.c_uint64 * 1)()
+        q = abi.request(abi.LN["moe_layer"], required_bytes_u64=abi.C.addressof(need), **self.fields)
+        _check(_ln().call("query_moe_layer_workspace", q), "query_moe_layer_workspace")
+        self.ws = torch.empty(int(need[0]), dtype=torch.uint8, device=w13.device)
+        self.out = torch.empty(tokens, self.hidden, dtype=torch.bfloat16, device=w13.device)
+        self.flag = error_flag()
+
+    def forward(self, x, topk_ids, topk_weights, shared=None):
+        r = abi.request(abi.LN["moe_layer"], input_bf16=ptr(x), topk_ids_u32=ptr(topk_ids),
+                        topk_weights_f32=ptr(topk_weights), w13=ptr(self.w13), w13_scale=ptr(self.w13_scale),
+                        w2=ptr(self.w2), w2_scale=ptr(self.w2_scale), shared_bf16=ptr(shared),
+                        output_bf16=ptr(self.out), workspace=ptr(self.ws), workspace_bytes=self.ws.numel(),
+                        error_flag_u32=ptr(self.flag), stream=stream_handle(), **self.fields)
+        _check(_ln().call("launch_moe_layer", r), "moe_layer")
+        return self.out
