@@ -10,9 +10,15 @@ plan -> activation quant -> grouped gate/up GEMM (+SwiGLU*w epilogue) ->
 quant -> grouped down GEMM -> ordered combine.  Inputs are resident in HBM
 before timing starts.
 
+A timed step is one call of the linear pack's C++ layer entry
+(``launch_moe_layer``), which enqueues the six grouped launches; a staged
+copy of the same layer launched stage by stage gives the per-kernel times.
+
 Prints one JSON line.  ``value`` is the layer's TFLOP/s (2*R*(2I*H + H*I)
 FLOP per step, R = T*top_k).  ``roofline`` covers the dominant kernel (the
-grouped gate/up GEMM), timed with HIP events on its launch stream.
+grouped gate/up GEMM), timed with HIP events on its launch stream.  Side
+measurements: ``moe_mxfp4_decode`` (configs[4], MXFP4 experts at 64 and 512
+tokens) and ``decode_gemv`` (configs[1] and [2] decode, BF16 prefill).
 ``cpu_baseline`` times the C restatement of the reference's CPU oracle
 (oracle/pih_oracle.c, po_expert_fp8: the per-expert chain) on a bounded
 sample of the same routed rows.
@@ -281,6 +287,48 @@ def bench_decode(torch, iters: int):
     return out
 
 
+def bench_mxfp4(torch, iters: int):
+    """the cfg4 MoE shapes (E=256, top-8, H=7168,
+    I=2048) with MXFP4 experts (e2m1 two per byte + UE8M0 per 32 k) at decode
+    batches of 64 and 512 tokens, bf16 and e4m3 (UE8M0 per 128) activations,
+    through the pack's layer entry.  Memory-bound: bytes = touched experts x
+    23,396,352 (weights + scales) + token activations in and out."""
+    from pih_amd import abi, synth
+    from pih_amd.linear import MoeLayer
+
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x50494805)
+    # any byte is two valid e2m1 codes; UE8M0 scales 2^-9 .. 2^-1
+    w13 = torch.randint(0, 256, (E, 2 * I, H // 2), dtype=torch.uint8, device=dev, generator=gen)
+    s13 = torch.randint(118, 127, (E, 2 * I, H // 32), dtype=torch.uint8, device=dev, generator=gen)
+    w2 = torch.randint(0, 256, (E, H, I // 2), dtype=torch.uint8, device=dev, generator=gen)
+    s2 = torch.randint(118, 127, (E, H, I // 32), dtype=torch.uint8, device=dev, generator=gen)
+    per_expert = 2 * I * H // 2 + H * I // 2 + 2 * I * H // 32 + H * I // 32
+    out = {}
+    for tokens in (64, 512):
+        ids, wts = synth.zipf_router(synth.config_seed(5, tokens), tokens, E, TOPK)
+        touched = int((np.bincount(ids.ravel(), minlength=E) > 0).sum())
+        x = torch.from_numpy(synth.bf16_normal(synth.config_seed(5, tokens + 1), (tokens, H)).view(np.int16))
+        x = x.to(dev).view(torch.bfloat16)
+        ids_d = torch.from_numpy(ids.view(np.int32)).to(dev)
+        wts_d = torch.from_numpy(wts).to(dev)
+        for act, name in ((abi.ACTIVATION_BF16, "bf16"), (abi.ACTIVATION_E4M3, "e4m3")):
+            layer = MoeLayer(w13, s13, w2, s2, tokens, TOPK, weight_format=abi.WEIGHT_MXFP4, activation_type=act)
+            ms = _timed(torch, lambda i: layer.forward(x, ids_d, wts_d), iters)
+            if int(layer.flag.item()):
+                raise RuntimeError(f"mxfp4 layer error flag {int(layer.flag.item())}")
+            algo = touched * per_expert + tokens * H * 2 * 2
+            flop = 2.0 * tokens * TOPK * (2 * I * H + H * I)
+            gbs = algo / (ms * 1e-3) / 1e9
+            out[f"t{tokens}_{name}"] = {"us_per_layer": round(ms * 1e3, 1), "gbs": round(gbs, 1),
+                                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                        "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+                                        "touched_experts": touched, "algorithmic_bytes": algo}
+            del layer
+    return out
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_fp8_cfg4_hbm_traffic.md")
 
 
@@ -320,6 +368,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode GEMV / prefill side measurements")
+    ap.add_argument("--no-mxfp4", action="store_true", help="skip the MXFP4 MoE decode side measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 1 GiB device-to-device copies (the reference kernel for scaling the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -335,7 +384,7 @@ def main() -> int:
 
     from pih_amd import abi
     from pih_amd.device import engine_stream, flag_value
-    from pih_amd.linear import MoeFp8Layer
+    from pih_amd.linear import MoeFp8Layer, MoeLayer
 
     log("generating inputs")
     ids, wts, x_bits, ids_d, wts_d, x_d, w13, s13, w2, s2 = build_inputs(torch)
@@ -351,27 +400,34 @@ def main() -> int:
                    + T * H * 2 + T * H * 2)
 
     with engine_stream() as s:
-        layer = MoeFp8Layer(w13, s13, w2, s2, T, TOPK, scale_format=abi.SCALE_F32)
+        # the timed step: one call of the pack's C++ layer entry (six grouped
+        # launches); the staged copy below times each launch on its own
+        layer = MoeLayer(w13, s13, w2, s2, T, TOPK, scale_format=abi.SCALE_F32)
+        staged = MoeFp8Layer(w13, s13, w2, s2, T, TOPK, scale_format=abi.SCALE_F32)
         log("warmup")
         for _ in range(args.warmup):
             layer.forward(x_d, ids_d, wts_d)
+            staged.forward(x_d, ids_d, wts_d)
         s.synchronize()
-        if flag_value(layer.flag):
-            log(f"device error flag {flag_value(layer.flag):#x}")
+        if flag_value(layer.flag) or flag_value(staged.flag):
+            log(f"device error flag {flag_value(layer.flag):#x} {flag_value(staged.flag):#x}")
             return 1
-        n_marks = len(MoeFp8Layer.STAGES) + 1
-        marks = [[torch.cuda.Event(enable_timing=True) for _ in range(n_marks)] for _ in range(args.steps)]
         log(f"timing {args.steps} steps")
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(args.steps):
-            layer.forward(x_d, ids_d, wts_d, marks=marks[i])
+            layer.forward(x_d, ids_d, wts_d)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        n_marks = len(MoeFp8Layer.STAGES) + 1
+        marks = [[torch.cuda.Event(enable_timing=True) for _ in range(n_marks)] for _ in range(args.steps)]
+        for i in range(args.steps):
+            staged.forward(x_d, ids_d, wts_d, marks=marks[i])
+        torch.cuda.synchronize()
         stage_ms = {name: float(np.median([m[j].elapsed_time(m[j + 1]) for m in marks]))
                     for j, name in enumerate(MoeFp8Layer.STAGES)}
-        if flag_value(layer.flag):
-            log(f"device error flag {flag_value(layer.flag):#x}")
+        if flag_value(layer.flag) or flag_value(staged.flag):
+            log(f"device error flag {flag_value(layer.flag):#x} {flag_value(staged.flag):#x}")
             return 1
     ms = wall * 1000.0 / args.steps
     tflops = flop / (ms * 1e-3) / 1e12
@@ -379,11 +435,19 @@ def main() -> int:
     gu_gbs = bytes_gu / (gu_ms * 1e-3) / 1e9
     log("stage ms: " + ", ".join(f"{k}={v:.3f}" for k, v in stage_ms.items()))
 
+    del layer, staged, w13, w2
+    torch.cuda.empty_cache()
+    mxfp4 = None
+    if not args.no_mxfp4:
+        log("MXFP4 MoE decode (configs[4])")
+        with engine_stream():
+            mxfp4 = bench_mxfp4(torch, iters=max(10, args.steps))
+        torch.cuda.empty_cache()
+        log("mxfp4: " + json.dumps(mxfp4))
+
     decode = None
     if not args.no_decode:
         log("decode GEMV / prefill side measurements")
-        del layer, w13, w2
-        torch.cuda.empty_cache()
         with engine_stream():
             decode = bench_decode(torch, iters=max(10, args.steps))
         log("decode: " + json.dumps(decode))
@@ -418,6 +482,7 @@ def main() -> int:
                      "algorithmic_bytes": int(bytes_gu), "flop": flop_gu, "ms": round(gu_ms, 4),
                      "mfma_tflops": round(flop_gu / (gu_ms * 1e-3) / 1e12, 1),
                      "mfma_frac": round(flop_gu / (gu_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)},
+        "moe_mxfp4_decode": mxfp4,
         "decode_gemv": decode,
         "cpu_baseline": cpu,
     }
