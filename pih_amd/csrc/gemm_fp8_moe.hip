@@ -13,9 +13,11 @@
 // SIMD):
 //   * one block of 512 threads (8 waves, two per SIMD) per CU owns a tile of
 //     128 A rows x 256 W rows; each 128-deep K step loads 48 KB with full
-//     128-byte lines (8 lanes per row) and stages both operands in LDS (rows
-//     padded to 144 B: the 16 rows one ds_read_b128 touches hit distinct
-//     banks);
+//     128-byte lines (8 lanes per row) and stages both operands in LDS as
+//     dense 128-byte rows whose 16-byte chunk c sits in slot
+//     c ^ ((row >> 1) & 7): a ds_write_b128 of 16 lanes (two rows) and a
+//     ds_read_b128 of 16 lanes (16 rows, one chunk) each cover 64 distinct
+//     4-byte banks;
 //   * the output is computed transposed, C^T = W . A^T: the MFMA's first
 //     operand is a 16-row W block and its second a 16-row A block, so a lane
 //     owns four consecutive output columns of one row.  That makes the fp32
@@ -34,13 +36,17 @@
 // Tiles are numbered expert-major and, inside an expert, in groups of up to
 // 32 M-tiles walked M-fastest; each XCD (blocks b % 8) walks one contiguous
 // range of that order so concurrently running tiles share W and A in its L2.
+// (An 8 M x 4 N grouping cut the L2-miss bytes by 9 % but ran 3 % slower.)
 #include "device_common.hpp"
 #include "kernels.hpp"
 
 namespace pih_amd {
 namespace {
 
-constexpr int BM = 128, BN = 256, NTH = 512, LDS_ROW = 144, GROUP_M = 32;
+constexpr int BM = 128, BN = 256, NTH = 512, LDS_ROW = 128, GROUP_M = 32;
+
+// byte offset of 16-byte chunk c of tile row r (XOR-swizzled slots)
+__device__ __forceinline__ uint32_t lds_at(uint32_t r, uint32_t c) { return r * LDS_ROW + ((c ^ ((r >> 1) & 7u)) << 4); }
 
 struct MoeParams {
   const uint8_t* a;
@@ -178,6 +184,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   };
   // staging: chunk c = tid + 512 i -> tile row c >> 3, 16-byte column c & 7
   const uint32_t ccol = (tid & 7) * 16;
+  const uint32_t cst = lds_at(tid >> 3, tid & 7);  // + 64 rows per i: same slot
   const uint8_t* a_ptr[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) a_ptr[i] = p.a + a_source((tid >> 3) + 64 * i) * K + ccol;
@@ -235,10 +242,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   auto lstore = [&](int set, int stage) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      *reinterpret_cast<v4i*>(&sA[stage][((tid >> 3) + 64 * i) * LDS_ROW + ccol]) = ra[set][i];
+      *reinterpret_cast<v4i*>(&sA[stage][cst + 64 * i * LDS_ROW]) = ra[set][i];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<v4i*>(&sB[stage][((tid >> 3) + 64 * i) * LDS_ROW + ccol]) = rw[set][i];
+      *reinterpret_cast<v4i*>(&sB[stage][cst + 64 * i * LDS_ROW]) = rw[set][i];
     if (tid < BM) {
       sSa[stage][(tid >> 6) * 64 + (tid & 15) * 4 + ((tid >> 4) & 3)] = sar[set];
       if constexpr (SCALE == kScaleUe8m0)
@@ -256,19 +263,22 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   auto compute = [&](int stage) {
     if (rb_live == 0) return;
     // operand fragments: lane (lr, lg) holds row lr, bytes [16lg, 16lg+16)
-    // and [64+16lg, 64+16lg+16) of the step (the same map for both)
+    // and [64+16lg, 64+16lg+16) of the step (the same map for both); the
+    // fragment rows start at multiples of 16, so the slot of chunk lg is
+    // lg ^ (lr >> 1) and that of chunk lg + 4 is the same slot ^ 4
+    const uint32_t rd0 = (lg ^ (lr >> 1)) << 4;
     v8i wf[4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const uint8_t* pb = &sB[stage][(wn * 64 + nb * 16 + lr) * LDS_ROW + lg * 16];
-      wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb), *reinterpret_cast<const v4i*>(pb + 64));
+      const uint8_t* pb = &sB[stage][(wn * 64 + nb * 16 + lr) * LDS_ROW];
+      wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb + rd0), *reinterpret_cast<const v4i*>(pb + (rd0 ^ 64)));
     }
     const v4i sa4 = *reinterpret_cast<const v4i*>(&sSa[stage][wm * 64 + lr * 4]);
     const uint32_t sw0 = sSw[stage][OUT == kOutSwiGlu ? 0 : (wn >> 1)];
     const uint32_t sw1 = sSw[stage][OUT == kOutSwiGlu ? 1 : (wn >> 1)];
     auto a_frag = [&](int r) -> v8i {
-      const uint8_t* pa = &sA[stage][(wm * 64 + r * 16 + lr) * LDS_ROW + lg * 16];
-      return cat8(*reinterpret_cast<const v4i*>(pa), *reinterpret_cast<const v4i*>(pa + 64));
+      const uint8_t* pa = &sA[stage][(wm * 64 + r * 16 + lr) * LDS_ROW];
+      return cat8(*reinterpret_cast<const v4i*>(pa + rd0), *reinterpret_cast<const v4i*>(pa + (rd0 ^ 64)));
     };
     auto mma = [&](int r, const v8i& af) {
       if constexpr (SCALE == kScaleF32) {

@@ -21,14 +21,17 @@
 //   kBf16    A, W bf16; two v_mfma_f32_16x16x32_bf16 per 64-deep step
 //            (the GemmPlan C = A.W^T of src/backend/cuda/gemm_plan.cpp).
 //   kBf16Fp4 A bf16; W MXFP4 dequantised exactly into bf16 in registers
-//            (every e2m1 value times 2^(s-127) is a bf16 number), then bf16
-//            MFMAs.
+//            (every e2m1 value times 2^(s-127) is a bf16 number; one
+//            v_cvt_scalef32_pk_bf16_fp4 per byte), then bf16 MFMAs.
 //
 // Tiling: 256 threads = 4 waves, block tile 128 A rows x 128 W rows, each
 // wave 64x64 = 4x4 MFMA 16x16 tiles.  Per K step A and W tiles go through
-// LDS (rows padded by 16 B: the 16 rows one ds_read touches land on distinct
-// banks), double-buffered with one barrier per step, next step prefetched
-// into registers.  Every global load is unconditional and in bounds (rows
+// LDS, double-buffered with one barrier per step, next step prefetched into
+// registers.  128-byte and 64-byte tile rows are dense with XOR-swizzled
+// 16-byte slots (chunk c of row r in slot c ^ ((r >> 1) & 7), resp.
+// c ^ ((r >> 2) & 3)), so that the 16 lanes of one ds_write_b128 or
+// ds_read_b128 cycle touch 64 distinct 4-byte banks; 32-byte rows are padded
+// to 48 B.  Every global load is unconditional and in bounds (rows
 // past a tile's end read row 0 and are never stored).
 //
 // Problems: strided (dense GEMM; the reference's grouped projection whose A
@@ -50,7 +53,17 @@ namespace {
 enum Kind : int { kFp8 = 0, kFp4 = 1, kBf16 = 2, kBf16Fp4 = 3 };
 
 constexpr int BM = 128, BN = 128, THREADS = 256, A_STEP_BYTES = 128;
-constexpr int LDS_A = A_STEP_BYTES + 16;
+constexpr int LDS_A = A_STEP_BYTES;
+
+// Byte offset of 16-byte chunk c of tile row r in a tile of ROW-byte rows.
+template <int ROW>
+__device__ __forceinline__ uint32_t lds_at(uint32_t r, uint32_t c) {
+  if constexpr (ROW == 128) return r * 128 + ((c ^ ((r >> 1) & 7u)) << 4);
+  else if constexpr (ROW == 64) return r * 64 + ((c ^ ((r >> 2) & 3u)) << 4);
+  else return r * (ROW + 16) + (c << 4);
+}
+template <int ROW>
+constexpr int lds_row_bytes() { return ROW == 128 || ROW == 64 ? ROW : ROW + 16; }
 
 template <int KIND>
 struct Traits;
@@ -154,22 +167,27 @@ __device__ __forceinline__ uint32_t ff_bytes(uint32_t w) {
   return (n - 0x01010101u) & ~n & 0x80808080u;
 }
 
-// 8 e2m1 nibbles of `w` times 2^(s-127) as 8 bf16 values (exact).
+// 8 e2m1 nibbles of `w` (low nibble first) times the power of two `scale`
+// as 8 bf16 values.  v_cvt_scalef32_pk_bf16_fp4 converts one byte (two
+// nibbles, low first) per instruction; the product is exact for every UE8M0
+// scale 0..254 (checked against decode-multiply-truncate over all 256 bytes
+// and all 255 scales on gfx950, overflow to inf included).
 __device__ __forceinline__ v8s dequant8_fp4(uint32_t w, float scale) {
-  v8s o;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float v = e2m1_decode((w >> (4 * j)) & 0xfu) * scale;
-    o[j] = (short)(__float_as_uint(v) >> 16);
-  }
-  return o;
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  const v2bf b0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  const v2bf b1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  const v2bf b2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  const v2bf b3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  const v4i o{__builtin_bit_cast(int, b0), __builtin_bit_cast(int, b1), __builtin_bit_cast(int, b2),
+              __builtin_bit_cast(int, b3)};
+  return __builtin_bit_cast(v8s, o);
 }
 
 template <int KIND, int SCALE, int OUT, bool MOE, bool CHECK>
 __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
   using T = Traits<KIND>;
   constexpr int B_STEP = T::B_STEP_BYTES;
-  constexpr int LDS_B = B_STEP + 16;
+  constexpr int LDS_B = lds_row_bytes<B_STEP>();
   constexpr int B_CPR = B_STEP / 16;             // 16-byte chunks per W row per step
   constexpr int B_LOADS = BN * B_CPR / THREADS;  // per thread
   constexpr bool FP8A = KIND == kFp8 || KIND == kFp4;
@@ -302,11 +320,11 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<v4i*>(&sA[buf][((tid >> 3) + 32 * i) * LDS_A + a_col * 16]) = ra[i];
+      *reinterpret_cast<v4i*>(&sA[buf][lds_at<A_STEP_BYTES>((tid >> 3) + 32 * i, a_col)]) = ra[i];
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
       const uint32_t c = tid + THREADS * i;
-      *reinterpret_cast<v4i*>(&sB[buf][(c / B_CPR) * LDS_B + (c % B_CPR) * 16]) = rb[i];
+      *reinterpret_cast<v4i*>(&sB[buf][lds_at<B_STEP>(c / B_CPR, c % B_CPR)]) = rb[i];
     }
     if constexpr (ASCALE)
       if (tid < BM) sAs[buf][tid] = rsa;
@@ -356,11 +374,11 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
       for (int ns = 0; ns < 4; ++ns) {
         const uint32_t brow = wn * 64 + ns * 16 + lr;
         const uint8_t* pb = &sB[buf][brow * LDS_B];
-        if constexpr (KIND == kFp8 || KIND == kBf16) {
-          bv[ns] = cat8(*reinterpret_cast<const v4i*>(pb + lg * 32),
-                        *reinterpret_cast<const v4i*>(pb + lg * 32 + 16));
+        if constexpr (KIND == kFp8 || KIND == kBf16) {  // chunks 2lg, 2lg + 1
+          const uint32_t o = lds_at<128>(brow, 2 * lg);
+          bv[ns] = cat8(*reinterpret_cast<const v4i*>(&sB[buf][o]), *reinterpret_cast<const v4i*>(&sB[buf][o ^ 16]));
         } else if constexpr (KIND == kFp4) {
-          bv[ns] = cat8(*reinterpret_cast<const v4i*>(pb + lg * 16), v4i{0, 0, 0, 0});
+          bv[ns] = cat8(*reinterpret_cast<const v4i*>(&sB[buf][lds_at<64>(brow, lg)]), v4i{0, 0, 0, 0});
           bsc[ns] = (sBs[buf][brow] >> (8 * lg)) & 0xffu;
         } else {  // kBf16Fp4: 16 nibbles = k 16*lg .. 16*lg+15 of the step
           const uint2 w2 = *reinterpret_cast<const uint2*>(pb + lg * 8);
@@ -377,9 +395,10 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
         // two 16-byte halves with k [16g, 16g+16) and [64+16g, 64+16g+16),
         // while an FP4 lane group g holds k [32g, 32g+32) contiguously
         // (measured on gfx950); same-format operands just use the same map.
-        const uint8_t* pa = &sA[buf][arow * LDS_A + (KIND == kFp4 ? lg * 16 : lg * 32)];
-        const v4i a0 = *reinterpret_cast<const v4i*>(pa);
-        const v4i a1 = *reinterpret_cast<const v4i*>(pa + (KIND == kFp4 ? 64 : 16));
+        // chunks lg and lg + 4 (kFp4) or 2lg and 2lg + 1 of the 128-byte row
+        const uint32_t ao = lds_at<A_STEP_BYTES>(arow, KIND == kFp4 ? lg : 2 * lg);
+        const v4i a0 = *reinterpret_cast<const v4i*>(&sA[buf][ao]);
+        const v4i a1 = *reinterpret_cast<const v4i*>(&sA[buf][ao ^ (KIND == kFp4 ? 64u : 16u)]);
         if constexpr (KIND == kFp8 && SCALE == kScaleF32) {
           const v4i s4 = *reinterpret_cast<const v4i*>(&sAs[buf][wm * 64 + ms * 16 + 4 * lg]);
           const v8i av = cat8(a0, a1);
