@@ -8,16 +8,18 @@
 // expert segments are the device offsets of the route plan, the reference's
 // host plan deepseek_expert_subwave_plan.cpp:32-101).
 //
-// Design (measured on MI355X; the per-CU limits are 128 B/clk of LDS, about
-// 64 B/clk of vector-memory loads and one 16x16x128 FP8 MFMA per 32 clk per
-// SIMD):
+// Design (measured on MI355X; one 16x16x128 FP8 MFMA per 32 clk per SIMD;
+// LDS has 64 four-byte banks and serves 16 lanes of a 16-byte access per
+// cycle):
 //   * one block of 512 threads (8 waves, two per SIMD) per CU owns a tile of
-//     128 A rows x 256 W rows; each 128-deep K step loads 48 KB with full
-//     128-byte lines (8 lanes per row) and stages both operands in LDS as
-//     dense 128-byte rows whose 16-byte chunk c sits in slot
-//     c ^ ((row >> 1) & 7): a ds_write_b128 of 16 lanes (two rows) and a
-//     ds_read_b128 of 16 lanes (16 rows, one chunk) each cover 64 distinct
-//     4-byte banks;
+//     128 A rows x 256 W rows; each 128-deep K step moves 48 KB with full
+//     128-byte lines (8 lanes per row) straight into LDS by DMA
+//     (global_load_lds_dwordx4: no staging registers, no ds_write), as dense
+//     128-byte rows whose 16-byte chunk c sits in slot c ^ ((row >> 1) & 7):
+//     the 16 rows of one operand-fragment read hit 64 distinct banks;
+//   * three LDS stages (144 KB), loads issued two steps ahead, one barrier
+//     per step; the waits are explicit vmcnt counts (seven loads per thread
+//     and step), because the compiler does not order LDS reads after DMA;
 //   * the output is computed transposed, C^T = W . A^T: the MFMA's first
 //     operand is a 16-row W block and its second a 16-row A block, so a lane
 //     owns four consecutive output columns of one row.  That makes the fp32
@@ -25,10 +27,6 @@
 //     epilogue stores 8 or 16 contiguous bytes per lane;
 //   * wave (wm, wn) computes A rows wm*64 + [0,64) against W rows
 //     wn*64 + [0,64): 4 x 4 MFMAs of 16x16x128 per K step;
-//   * global loads run three steps ahead in three register sets; the main
-//     loop is six whole steps with no branch around a memory operation, so
-//     the compiler's in-order vmcnt waits stay exact and every load has two
-//     whole steps to land;
 //   * fp32 scales: each MFMA starts from zero and the lane adds
 //     t * (a_scale[row] * w_scale[block]) in fp32 (DeepSeek-V3 promotion,
 //     bit-identical to the 128x128-tile kernel); UE8M0 scales ride in the
@@ -43,7 +41,19 @@
 namespace pih_amd {
 namespace {
 
-constexpr int BM = 128, BN = 256, NTH = 512, LDS_ROW = 128, GROUP_M = 32;
+constexpr int BM = 128, BN = 256, NTH = 512, LDS_ROW = 128, GROUP_M = 32, STAGES = 3;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
+// [6:4], lgkmcnt [11:8]; an all-ones field does not wait)
+constexpr int kWaitVm7 = 0x0F77;     // vmcnt(7)
+constexpr int kWaitVm0 = 0x0F70;     // vmcnt(0)
+constexpr int kWaitLgkm0 = 0xC07F;   // lgkmcnt(0)
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes
+// land at lds + 16 l (lds is wave-uniform; it goes to M0)
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
 
 // byte offset of 16-byte chunk c of tile row r (XOR-swizzled slots)
 __device__ __forceinline__ uint32_t lds_at(uint32_t r, uint32_t c) { return r * LDS_ROW + ((c ^ ((r >> 1) & 7u)) << 4); }
@@ -149,11 +159,19 @@ __device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, u
 
 template <int SCALE, int OUT>
 __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
-  __shared__ __align__(16) uint8_t sA[2][BM * LDS_ROW];
-  __shared__ __align__(16) uint8_t sB[2][BN * LDS_ROW];
+  // One LDS variable per stage and operand: the compiler's wait insertion
+  // tells DMA into one stage from reads of another only across distinct
+  // variables (otherwise it waits for every load in flight before any LDS
+  // access).
+  __shared__ __align__(16) uint8_t sA0[BM * LDS_ROW], sA1[BM * LDS_ROW], sA2[BM * LDS_ROW];
+  __shared__ __align__(16) uint8_t sB0[BN * LDS_ROW], sB1[BN * LDS_ROW], sB2[BN * LDS_ROW];
   // A-row scales of a stage: row wm*64 + rb*16 + l at [wm*64 + l*4 + rb]
-  __shared__ __align__(16) uint32_t sSa[2][BM];
-  __shared__ __align__(16) uint32_t sSw[2][2];
+  __shared__ __align__(16) uint32_t sSa0[BM], sSa1[BM], sSa2[BM];
+  __shared__ __align__(16) uint32_t sSw0[2], sSw1[2], sSw2[2];
+  auto sA = [&](int st) -> uint8_t* { return st == 0 ? sA0 : st == 1 ? sA1 : sA2; };
+  auto sB = [&](int st) -> uint8_t* { return st == 0 ? sB0 : st == 1 ? sB1 : sB2; };
+  auto sSa = [&](int st) -> uint32_t* { return st == 0 ? sSa0 : st == 1 ? sSa1 : sSa2; };
+  auto sSw = [&](int st) -> uint32_t* { return st == 0 ? sSw0 : st == 1 ? sSw1 : sSw2; };
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
@@ -182,12 +200,6 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
     return src;
   };
-  // staging: chunk c = tid + 512 i -> tile row c >> 3, 16-byte column c & 7
-  const uint32_t ccol = (tid & 7) * 16;
-  const uint32_t cst = lds_at(tid >> 3, tid & 7);  // + 64 rows per i: same slot
-  const uint8_t* a_ptr[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) a_ptr[i] = p.a + a_source((tid >> 3) + 64 * i) * K + ccol;
   const uint64_t sa_off = a_source(tid & (BM - 1)) * KB;
 
   // W tile row R: for SwiGLU, wave block R >> 6 holds 32 gate rows (R & 63
@@ -203,9 +215,6 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
   };
   const uint8_t* w_base = p.w + (uint64_t)expert * p.n * K;
-  const uint8_t* w_ptr[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) w_ptr[i] = w_base + (uint64_t)w_row((tid >> 3) + 64 * i) * K + ccol;
   // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
   uint32_t wblk0, wblk1;
   if constexpr (OUT == kOutSwiGlu) {
@@ -221,36 +230,55 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   const uint32_t rb_live =
       __builtin_amdgcn_readfirstlane(rows > wm * 64 ? min(4u, (rows - wm * 64 + 15) / 16) : 0u);
 
-  v4i ra[3][2], rw[3][4];
-  uint32_t sar[3], swr0[3], swr1[3];
-  auto gload = [&](int set, uint32_t kb) {
+  // Operand tiles move global -> LDS by DMA (global_load_lds_dwordx4): an
+  // instruction lands lane l's 16 bytes at byte 16 l of a wave-uniform 1 KB
+  // window, i.e. tile row 8q + (l >> 3), slot l & 7 of window q, so lane l
+  // fetches chunk (l & 7) ^ ((row >> 1) & 7) of that row (full 128-byte lines
+  // per 8 lanes).  Wave w fills A rows [16w, 16w + 16) and W rows
+  // [32w, 32w + 32) of a stage.
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lrow = lane >> 3, lslot = lane & 7;
+  const uint8_t* a_src[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t R = 16 * wave + 8 * i + lrow;
+    a_src[i] = p.a + a_source(R) * K + ((lslot ^ ((R >> 1) & 7u)) << 4);
+  }
+  const uint8_t* w_src[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t R = 32 * wave + 8 * i + lrow;
+    w_src[i] = w_base + (uint64_t)w_row(R) * K + ((lslot ^ ((R >> 1) & 7u)) << 4);
+  }
+  // Scales ride in registers: thread t < 128 loads the A scale of tile row
+  // t, threads 128 and 129 the two W block scales, every other thread the
+  // A scale of row t & 127 again, so each thread issues exactly seven
+  // vector loads per step (the wait counts below rely on it).
+  constexpr uint32_t ESZ = SCALE == kScaleUe8m0 ? 1 : 4;
+  const uint8_t* s_src = static_cast<const uint8_t*>(p.a_scale) + sa_off * ESZ;
+  if (tid == BM) s_src = static_cast<const uint8_t*>(p.w_scale) + ws0_off * ESZ;
+  if (tid == BM + 1) s_src = static_cast<const uint8_t*>(p.w_scale) + ws1_off * ESZ;
+  uint32_t sreg[STAGES];
+  auto issue = [&](int stage, uint32_t kb) {
     const uint64_t o = (uint64_t)kb * 128;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) ra[set][i] = *reinterpret_cast<const v4i*>(a_ptr[i] + o);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) rw[set][i] = *reinterpret_cast<const v4i*>(w_ptr[i] + o);
-    if constexpr (SCALE == kScaleUe8m0) {
-      sar[set] = static_cast<const uint8_t*>(p.a_scale)[sa_off + kb];
-      swr0[set] = static_cast<const uint8_t*>(p.w_scale)[ws0_off + kb];
-      swr1[set] = static_cast<const uint8_t*>(p.w_scale)[ws1_off + kb];
-    } else {
-      sar[set] = static_cast<const uint32_t*>(p.a_scale)[sa_off + kb];
-      swr0[set] = static_cast<const uint32_t*>(p.w_scale)[ws0_off + kb];
-      swr1[set] = static_cast<const uint32_t*>(p.w_scale)[ws1_off + kb];
-    }
-  };
-  auto lstore = [&](int set, int stage) {
-#pragma unroll
     for (int i = 0; i < 2; ++i)
-      *reinterpret_cast<v4i*>(&sA[stage][cst + 64 * i * LDS_ROW]) = ra[set][i];
+      dma16(a_src[i] + o, sA(stage) + wv * 2048 + i * 1024);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<v4i*>(&sB[stage][cst + 64 * i * LDS_ROW]) = rw[set][i];
+      dma16(w_src[i] + o, sB(stage) + wv * 4096 + i * 1024);
+    if constexpr (SCALE == kScaleUe8m0) sreg[stage] = s_src[kb];
+    else sreg[stage] = reinterpret_cast<const uint32_t*>(s_src)[kb];
+  };
+  auto sstore = [&](int stage) {
     if (tid < BM) {
-      sSa[stage][(tid >> 6) * 64 + (tid & 15) * 4 + ((tid >> 4) & 3)] = sar[set];
+      sSa(stage)[(tid >> 6) * 64 + (tid & 15) * 4 + ((tid >> 4) & 3)] = sreg[stage];
       if constexpr (SCALE == kScaleUe8m0)
-        bad |= ((sar[set] == 0xffu && tid < rows) || swr0[set] == 0xffu || swr1[set] == 0xffu) ? kErrScale : 0u;
-      if (tid < 2) sSw[stage][tid] = tid ? swr1[set] : swr0[set];
+        if (sreg[stage] == 0xffu && tid < rows) bad |= kErrScale;
+    } else if (tid < BM + 2) {
+      sSw(stage)[tid - BM] = sreg[stage];
+      if constexpr (SCALE == kScaleUe8m0)
+        if (sreg[stage] == 0xffu) bad |= kErrScale;
     }
   };
 
@@ -270,14 +298,14 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     v8i wf[4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const uint8_t* pb = &sB[stage][(wn * 64 + nb * 16 + lr) * LDS_ROW];
+      const uint8_t* pb = sB(stage) + (wn * 64 + nb * 16 + lr) * LDS_ROW;
       wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb + rd0), *reinterpret_cast<const v4i*>(pb + (rd0 ^ 64)));
     }
-    const v4i sa4 = *reinterpret_cast<const v4i*>(&sSa[stage][wm * 64 + lr * 4]);
-    const uint32_t sw0 = sSw[stage][OUT == kOutSwiGlu ? 0 : (wn >> 1)];
-    const uint32_t sw1 = sSw[stage][OUT == kOutSwiGlu ? 1 : (wn >> 1)];
+    const v4i sa4 = *reinterpret_cast<const v4i*>(sSa(stage) + wm * 64 + lr * 4);
+    const uint32_t sw0 = sSw(stage)[OUT == kOutSwiGlu ? 0 : (wn >> 1)];
+    const uint32_t sw1 = sSw(stage)[OUT == kOutSwiGlu ? 1 : (wn >> 1)];
     auto a_frag = [&](int r) -> v8i {
-      const uint8_t* pa = &sA[stage][(wm * 64 + r * 16 + lr) * LDS_ROW];
+      const uint8_t* pa = sA(stage) + (wm * 64 + r * 16 + lr) * LDS_ROW;
       return cat8(*reinterpret_cast<const v4i*>(pa + rd0), *reinterpret_cast<const v4i*>(pa + (rd0 ^ 64)));
     };
     auto mma = [&](int r, const v8i& af) {
@@ -316,27 +344,29 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
   };
 
-  // prologue: steps 0, 1, 2 into sets 0, 1, 2; stage 0 <- step 0
+  // Three LDS stages, loads two steps ahead.  Step j: wait until at most
+  // the seven loads of step j + 1 are in flight (step j's tiles and scale
+  // registers have landed), publish step j's scales, barrier (every wave's
+  // DMA for step j is visible and step j - 1's compute is done, so its stage
+  // may be refilled), issue step j + 2 into that stage, compute step j.
+  // Loads past the last step re-read it into a stage that is never used.
   const uint32_t last = KB - 1;
-  gload(0, 0);
-  gload(1, min(1u, last));
-  gload(2, min(2u, last));
-  lstore(0, 0);
-  __syncthreads();
-
-  // Step j: compute stage j&1; store step j+1 (set (j+1)%3) into stage
-  // (j+1)&1; barrier; load step j+3 into set j%3.  Loads past the last step
-  // re-read it (in bounds, never stored).
+  issue(0, 0);
+  issue(1, min(1u, last));
 #define PIH_MOE_STEP(J, TAIL)                                           \
   {                                                                     \
     const uint32_t j = kb + (J);                                        \
-    compute((J) & 1);                                                   \
-    if (!(TAIL) || j + 1 < KB) lstore(((J) + 1) % 3, ((J) + 1) & 1);    \
-    __syncthreads();                                                    \
-    if ((TAIL) && j + 1 >= KB) goto done;                               \
-    gload((J) % 3, min(j + 3, last));                                   \
+    if ((TAIL) && j >= KB) goto done;                                   \
+    __builtin_amdgcn_s_waitcnt(kWaitVm7);                               \
+    sstore((J) % 3);                                                    \
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);                             \
+    __builtin_amdgcn_s_barrier();                                       \
+    issue(((J) + 2) % 3, min(j + 2, last));                             \
+    compute((J) % 3);                                                   \
   }
   {
+    // six steps per trip: only the first LDS accesses after the loop
+    // header get a conservative full wait from the compiler
     uint32_t kb = 0;
     for (; kb + 6 < KB; kb += 6) {
       PIH_MOE_STEP(0, false)
@@ -355,6 +385,8 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   }
 #undef PIH_MOE_STEP
 done:
+  // no DMA may still target this block's LDS when its waves end
+  __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
   // ---- epilogue: lane holds out[row wm*64 + r*16 + lr][4*lg + i] of block nb
 #pragma unroll
