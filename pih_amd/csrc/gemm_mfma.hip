@@ -99,13 +99,14 @@ struct GemmParams {
   uint64_t out_row_stride;
   uint32_t out_prob_col;
   uint32_t n_tiles, m_tiles_per, tiles_total;
+  uint32_t light_rows;  // MoE: experts with at most this many rows are skipped
   float limit;
   uint32_t err_code, err_scale, err_nonfinite;
 };
 
 // Expert lookup for MoE tile g: returns false when g is past the last tile.
-__device__ bool moe_find_tile(const uint32_t* offsets, uint32_t experts, uint32_t m_bound, uint32_t g,
-                              uint32_t* err, uint32_t err_code, uint32_t& expert, uint32_t& row0,
+__device__ bool moe_find_tile(const uint32_t* offsets, uint32_t experts, uint32_t m_bound, uint32_t light_rows,
+                              uint32_t g, uint32_t* err, uint32_t err_code, uint32_t& expert, uint32_t& row0,
                               uint32_t& rows) {
   __shared__ uint32_t s_scan[THREADS];
   __shared__ uint32_t s_res[2];
@@ -116,7 +117,7 @@ __device__ bool moe_find_tile(const uint32_t* offsets, uint32_t experts, uint32_
     const uint32_t e = tid * per + j;
     if (e < experts) {
       const uint32_t lo = offsets[e], hi = offsets[e + 1];
-      cnt += hi > lo ? (hi - lo + BM - 1) / BM : 0;
+      cnt += hi > lo + light_rows ? (hi - lo + BM - 1) / BM : 0;
     }
   }
   if (tid == 0) s_res[0] = 0xffffffffu;
@@ -135,7 +136,7 @@ __device__ bool moe_find_tile(const uint32_t* offsets, uint32_t experts, uint32_
       const uint32_t e = tid * per + j;
       if (e >= experts) break;
       const uint32_t lo = offsets[e], hi = offsets[e + 1];
-      const uint32_t t = hi > lo ? (hi - lo + BM - 1) / BM : 0;
+      const uint32_t t = hi > lo + light_rows ? (hi - lo + BM - 1) / BM : 0;
       if (g < acc + t) {
         s_res[0] = e;
         s_res[1] = g - acc;
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
 
   uint32_t prob, row0, rows;
   if constexpr (MOE) {
-    if (!moe_find_tile(p.offsets, p.problems, p.m, g, p.err, p.err_code, prob, row0, rows)) return;
+    if (!moe_find_tile(p.offsets, p.problems, p.m, p.light_rows, g, p.err, p.err_code, prob, row0, rows)) return;
   } else {
     prob = g / p.m_tiles_per;
     row0 = (g % p.m_tiles_per) * BM;
@@ -530,7 +531,7 @@ void dispatch_out(const GemmParams& gp, uint32_t grid, hipStream_t s, OutKind ou
 
 // Shared host setup: tile counts, grid, common fields.
 St prepare(GemmParams& gp, uint32_t& grid, uint32_t m, uint32_t n, uint32_t k, uint32_t problems, bool moe,
-           OutKind out, uint64_t out_row_stride) {
+           OutKind out, uint64_t out_row_stride, uint32_t light_rows = 0) {
   gp.m = m;
   gp.n = n;
   gp.k = k;
@@ -538,18 +539,21 @@ St prepare(GemmParams& gp, uint32_t& grid, uint32_t m, uint32_t n, uint32_t k, u
   gp.n_tiles = n / BN;
   gp.out_row_stride = out_row_stride ? out_row_stride : (out == kOutSwiGlu ? n / 2 : n);
   uint64_t mt;
+  gp.light_rows = moe ? light_rows : 0;
   if (moe) {
-    // sum_e ceil(rows_e/BM) <= rows/BM + (number of non-empty experts)
-    mt = (uint64_t)m / BM + (problems < m ? problems : m);
+    // sum_e ceil(rows_e/BM) <= rows/BM + (number of tiled experts), and a
+    // tiled expert has more than light_rows rows
+    const uint64_t tiled = m / ((uint64_t)light_rows + 1);
+    mt = (uint64_t)m / BM + (problems < tiled ? problems : tiled);
     gp.m_tiles_per = 0;
   } else {
     gp.m_tiles_per = (m + BM - 1) / BM;
     mt = (uint64_t)gp.m_tiles_per * problems;
   }
   const uint64_t total = mt * gp.n_tiles;
-  if (total == 0 || total > 0x7fffffffull - 8) return Invalid("gemm_grid_too_large");
+  if (total > 0x7fffffffull - 8 || (total == 0 && gp.light_rows == 0)) return Invalid("gemm_grid_too_large");
   gp.tiles_total = (uint32_t)total;
-  grid = (uint32_t)((total + 7) / 8 * 8);
+  grid = (uint32_t)((total + 7) / 8 * 8);  // 0: every expert is light, nothing to tile
   return RequireCleanLastError();
 }
 
@@ -620,12 +624,18 @@ St LaunchFp4Gemm(const Fp4GemmArgs& a) {
   gp.err_code = 1u;
   gp.err_scale = 2u;
   gp.err_nonfinite = 4u;
+  // MoE: the light experts go to the weight-streaming kernel, the tiles
+  // here cover the others
   uint32_t grid;
-  St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, 0);
+  St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, 0, a.moe ? Fp4MoeLightRows(a) : 0);
   if (!s.ok()) return s;
-  if (a.act == kActE4m3) dispatch_out<kFp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, !a.moe);
-  else dispatch_out<kBf16Fp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, false);
-  return AfterLaunch("fp4_gemm_launch_failed");
+  if (grid) {
+    if (a.act == kActE4m3) dispatch_out<kFp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, !a.moe);
+    else dispatch_out<kBf16Fp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, false);
+    s = AfterLaunch("fp4_gemm_launch_failed");
+  }
+  if (!s.ok() || gp.light_rows == 0) return s;
+  return LaunchFp4MoeStream(a);
 }
 
 St LaunchBf16Gemm(const Bf16GemmArgs& a) {

@@ -286,8 +286,11 @@ def _mx_moe_weights(experts, n, k, seed):
 
 
 @pytest.mark.parametrize("act", [abi.ACTIVATION_E4M3, abi.ACTIVATION_BF16])
-@pytest.mark.parametrize("tokens,experts,topk", [(64, 8, 2), (5, 16, 4)])
+@pytest.mark.parametrize("tokens,experts,topk", [(64, 8, 2), (5, 16, 4), (200, 8, 2)])
 def test_moe_mxfp4_gemm_swiglu(eng, act, tokens, experts, topk):
+    """Light experts (<= 64 rows with e4m3, <= 32 with bf16 activations) go
+    to the weight-streaming kernel, the others to the 128-row tiles; the
+    200-token case has experts on both sides of both limits."""
     from pih_amd import linear
 
     hidden, inter = 512, 256
