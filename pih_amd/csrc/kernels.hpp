@@ -94,11 +94,11 @@ struct Fp4GemmArgs {
   float swiglu_limit = 0.0f;
 };
 St LaunchFp4Gemm(const Fp4GemmArgs& a);
-// MoE problems: experts with at most Fp4MoeLightRows(a) rows (64 with e4m3,
-// 32 with bf16 activations; 0 when the shape does not fit the streaming
-// kernel) go to the weight-streaming kernel of moe_stream.hip, the others to
-// the tiled kernel; LaunchFp4Gemm enqueues both on a.stream.
-constexpr uint32_t kMoeLightRows = 64, kMoeLightRowsBf16 = 32;
+// MoE problems: experts with at most Fp4MoeLightRows(a) rows (64; 0 when
+// the shape does not fit the streaming kernel) go to the weight-streaming
+// kernel of moe_stream.hip, the others to the tiled kernel; LaunchFp4Gemm
+// enqueues both on a.stream.
+constexpr uint32_t kMoeLightRows = 64;
 uint32_t Fp4MoeLightRows(const Fp4GemmArgs& a);
 St LaunchFp4MoeStream(const Fp4GemmArgs& a);
 

@@ -16,14 +16,16 @@
 // A light expert's work is weight streaming, and the kernel is built for
 // that (the 128-row tiles of gemm_mfma.hip spend most of their loads on
 // dead activation rows when an expert has a few rows):
-//   * a block of 4 waves owns 128 W rows of one light expert and all of its
-//     rows (<= 64 with e4m3, <= 32 with bf16 activations); each wave owns 32
+//   * a block of 4 waves owns 128 W rows of one light expert (<= 64 rows)
+//     and up to 64 (e4m3) or 32 (bf16) of its rows; each wave owns 32
 //     W rows (two 16-row MFMA fragments) and loads them straight into
 //     registers in the MFMA operand layout, non-temporal, 3-4 steps of
 //     256 k ahead (lane (lr, lg): row lr, bytes [16lg, +16) and
 //     [64 + 16lg, +16) of the row's 128-byte step: the 32 k of sub-step 0
 //     and of sub-step 1 that the lane's group multiplies);
-//   * the expert's activation rows go through a double-buffered LDS tile
+//   * the expert's activation rows (only the 16-row groups it has: staging
+//     loads cost as much as the weight stream when a tile is mostly dead
+//     rows) go through a double-buffered LDS tile
 //     with XOR-swizzled 16-byte slots (chunk c of row r in slot c ^ (r & 15):
 //     16 rows read at one chunk hit 64 distinct banks), loaded kDepth steps
 //     ahead together with the weights -- every vector load shares one
@@ -49,9 +51,11 @@ constexpr int KSTEP = 256;  // k per step: 128 weight bytes per row
 
 template <int ACT>
 struct Act {
-  static constexpr uint32_t MAXR = ACT == kActBf16 ? kMoeLightRowsBf16 : kMoeLightRows;
+  // rows per pass (a light expert with more rows is done in row chunks)
+  static constexpr uint32_t MAXR = ACT == kActBf16 ? 32 : kMoeLightRows;
   static constexpr uint32_t ROW = ACT == kActBf16 ? 512 : 256;  // activation bytes per row and step
   static constexpr uint32_t CHUNKS = MAXR * ROW / 16 / NTH;     // 16-byte chunks per thread and step
+  static constexpr uint32_t RPI = NTH * 16 / ROW;               // rows per staging instruction
 };
 
 struct StreamParams {
@@ -81,25 +85,27 @@ __device__ __forceinline__ uint32_t ff_bytes(uint32_t w) {
 }
 
 // Block -> (expert, first row, rows, W block) over the light experts only
-// (1 <= rows <= max_rows).  The light experts are counted by a block-wide
-// scan; items are numbered expert-major (neighbouring W blocks of one
-// expert share its activation rows in L2) and split into 8 equal
-// contiguous ranges, one per XCD (blocks b % 8).  Needs
-// gridDim.x >= 8 * ceil(items / 8).
+// (1 <= rows <= kMoeLightRows).  An expert with more than max_rows rows is
+// done in ceil(rows / max_rows) row chunks; items are numbered expert-major,
+// then W block, then row chunk, so that the chunks of one W block (which
+// stream the same weights) run next to each other, and neighbouring W
+// blocks of one expert share its activation rows in L2.  The items are
+// split into 8 equal contiguous ranges, one per XCD (blocks b % 8).
+// Needs gridDim.x >= 8 * ceil(items / 8).
 __device__ bool light_item(const StreamParams& p, uint32_t max_rows, uint32_t& expert, uint32_t& row0,
                            uint32_t& rows, uint32_t& wb) {
   __shared__ uint32_t s_wave[NTH / 64];
-  __shared__ uint32_t s_res;
+  __shared__ uint32_t s_res[2];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t E = p.experts;
   const uint32_t per_t = (E + NTH - 1) / NTH;
+  auto chunks = [&](uint32_t lo, uint32_t hi) -> uint32_t {
+    return (hi > lo && hi - lo <= kMoeLightRows) ? (hi - lo + max_rows - 1) / max_rows : 0u;
+  };
   uint32_t cnt = 0;
   for (uint32_t j = 0; j < per_t; ++j) {
     const uint32_t e = tid * per_t + j;
-    if (e < E) {
-      const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
-      cnt += (hi > lo && hi - lo <= max_rows) ? 1u : 0u;
-    }
+    if (e < E) cnt += chunks(p.offsets[e], p.offsets[e + 1]);
   }
   uint32_t incl = cnt;
 #pragma unroll
@@ -108,7 +114,7 @@ __device__ bool light_item(const StreamParams& p, uint32_t max_rows, uint32_t& e
     if ((int)lane >= off) incl += v;
   }
   if (lane == 63) s_wave[wave] = incl;
-  if (tid == 0) s_res = 0xffffffffu;
+  if (tid == 0) s_res[0] = 0xffffffffu;
   __syncthreads();
   uint32_t before = 0, light = 0;
 #pragma unroll
@@ -118,40 +124,42 @@ __device__ bool light_item(const StreamParams& p, uint32_t max_rows, uint32_t& e
     light += v;
   }
   incl += before;
-  const uint32_t excl = incl - cnt;
+  const uint32_t excl = incl - cnt;  // in row chunks
   const uint32_t total = light * p.nblk;
   const uint32_t per = (total + 7) / 8;
   const uint32_t xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
   const uint32_t t = xcd * per + jj;
   if (jj >= per || t >= total) return false;  // same for every thread
-  const uint32_t q = t / p.nblk;              // ordinal of the light expert
-  if (q >= excl && q < incl) {
-    uint32_t seen = excl;
+  // the expert whose items [nblk * c0, nblk * (c0 + c)) contain t, where c0
+  // is its first chunk ordinal and c its chunk count
+  if (t >= excl * p.nblk && t < incl * p.nblk) {
+    uint32_t c0 = excl;
     for (uint32_t j = 0; j < per_t; ++j) {
       const uint32_t e = tid * per_t + j;
       if (e >= E) break;
-      const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
-      if (hi > lo && hi - lo <= max_rows) {
-        if (seen == q) {
-          s_res = e;
-          break;
-        }
-        ++seen;
+      const uint32_t c = chunks(p.offsets[e], p.offsets[e + 1]);
+      if (t < (c0 + c) * p.nblk) {
+        s_res[0] = e;
+        s_res[1] = c0;
+        break;
       }
+      c0 += c;
     }
   }
   __syncthreads();
-  const uint32_t e = s_res;
+  const uint32_t e = s_res[0];
   if (e == 0xffffffffu) return false;
   const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
   if (hi > p.m || lo > hi) {
     if (tid == 0) atomicOr(p.err, kErrCode);
     return false;
   }
+  const uint32_t c = (hi - lo + max_rows - 1) / max_rows;
+  const uint32_t local = t - s_res[1] * p.nblk;
   expert = e;
-  row0 = lo;
-  rows = hi - lo;
-  wb = t - q * p.nblk;
+  wb = local / c;
+  row0 = lo + (local % c) * max_rows;
+  rows = min(max_rows, hi - row0);
   return true;
 }
 
@@ -162,10 +170,12 @@ template <int ACT, int OUT, int KBT>
 __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) {
   using C = Act<ACT>;
   constexpr uint32_t MAXR = C::MAXR, ROW = C::ROW, CH = C::CHUNKS, NA = MAXR / 16;
-  // steps in flight per wave (bf16 with an unrolled K loop: 3, so that its
-  // conversion temporaries fit the 256 registers of two waves per SIMD)
-  constexpr int kDepth = (ACT == kActBf16 && KBT > 0) ? 3 : 4;
+  // steps in flight per wave: 3 with an unrolled K loop (the ring then fits
+  // the 256 registers of two waves per SIMD), 4 in the generic loop (whose
+  // 8-step body needs a depth dividing 8)
+  constexpr int kDepth = KBT > 0 ? 3 : 4;
   constexpr uint32_t CPR = ROW / 16;  // chunks per activation row
+  constexpr uint32_t RPI = C::RPI;    // staging instruction i covers rows [i RPI, (i + 1) RPI)
   __shared__ __align__(16) uint8_t sA[2][MAXR * ROW];
   __shared__ __align__(16) uint32_t sSa[2][MAXR];  // e4m3: the row's 2 scale bytes of the step
 
@@ -238,9 +248,15 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
     const uint8_t* sb8 = ws_base + (uint64_t)kc * 8;
 #pragma unroll
     for (int f = 0; f < 2; ++f) rws[slot][f] = *reinterpret_cast<const uint2*>(sb8 + ws_off[f]);
+    // only the staging instructions that cover live rows (the tile rows past
+    // the expert's are never stored; their LDS contents are left stale)
     const uint8_t* ab = static_cast<const uint8_t*>(p.a) + (uint64_t)kc * ROW;
 #pragma unroll
-    for (uint32_t i = 0; i < CH; ++i) ra[slot][i] = *reinterpret_cast<const v4i*>(ab + a_off[i]);
+    for (uint32_t i = 0; i < CH; ++i) {
+      v4i v = v4i{0, 0, 0, 0};  // defined on both paths: the old ring value dies here
+      if (i == 0 || i * RPI < rows) v = *reinterpret_cast<const v4i*>(ab + a_off[i]);
+      ra[slot][i] = v;
+    }
     if constexpr (ACT == kActE4m3) {
       // the 2 scale bytes of the step, from the aligned 32-bit word that
       // holds them (s_off + 2 kc is even): a full-register load, so the
@@ -252,7 +268,8 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   };
   auto stage = [&](int slot, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (uint32_t i = 0; i < CH; ++i) *reinterpret_cast<v4i*>(&sA[buf][a_st[i]]) = ra[slot][i];
+    for (uint32_t i = 0; i < CH; ++i)
+      if (i == 0 || i * RPI < rows) *reinterpret_cast<v4i*>(&sA[buf][a_st[i]]) = ra[slot][i];
     if constexpr (ACT == kActE4m3) {
       if (tid < MAXR) {
         const uint32_t v = rsa[slot] & 0xffffu;
@@ -272,13 +289,13 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
 #pragma unroll
     for (int f = 0; f < 2; ++f)
       if (ff_bytes(rws[slot][f].x) | ff_bytes(rws[slot][f].y)) bad |= kErrScale;
-    auto frag = [&](auto R) __attribute__((always_inline)) {
-      constexpr int r = decltype(R)::value;
-      const uint32_t row = r * 16 + lr;
-      const uint8_t* pa = &sA[buf][row * ROW];
+    if constexpr (ACT == kActE4m3) {
+      auto frag = [&](auto R) __attribute__((always_inline)) {
+        constexpr int r = decltype(R)::value;
+        const uint32_t row = r * 16 + lr;
+        const uint8_t* pa = &sA[buf][row * ROW];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if constexpr (ACT == kActE4m3) {
+        for (int s = 0; s < 2; ++s) {
           // FP8 operand: chunks 8s + lg and 8s + 4 + lg of the row
           const uint32_t c0 = 8 * s + lg, c1 = c0 + 4;
           const v8i af = cat8(*reinterpret_cast<const v4i*>(pa + ((c0 ^ lr) << 4)),
@@ -292,36 +309,44 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
             acc[f][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cat8(w4, v4i{0, 0, 0, 0}), af, acc[f][r],
                                                                          4, 0, 0, sw, 0, sa);
           }
-        } else {
-          // bf16 operand of MFMA j: k 32lg + 8j .. +7 of the sub-step, i.e.
-          // chunk 16s + 4lg + j of the row; the weight dword 4s + j holds the
-          // same k (8 nibbles, low first)
+        }
+      };
+      // every activation fragment is computed (rows past the expert's hold
+      // stale data and are never stored): MFMA time stays below the stream
+      frag(std::integral_constant<int, 0>{});
+      frag(std::integral_constant<int, 1>{});
+      frag(std::integral_constant<int, 2>{});
+      frag(std::integral_constant<int, 3>{});
+    } else {
+      // bf16: MFMA j of sub-step s multiplies k 32lg + 8j .. +7 of the
+      // sub-step: weight dword 4s + j (8 nibbles, low first), converted once
+      // per fragment, against chunk 16s + 4lg + j of each activation row
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float sc[2];
+#pragma unroll
+        for (int f = 0; f < 2; ++f) sc[f] = ue8m0_value(((s ? rws[slot][f].y : rws[slot][f].x) >> (8 * lg)) & 0xffu);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t c = 16 * s + 4 * lg + j;
+          v4i av[NA];
+#pragma unroll
+          for (uint32_t r = 0; r < NA; ++r)
+            av[r] = *reinterpret_cast<const v4i*>(&sA[buf][(r * 16 + lr) * ROW + ((c ^ lr) << 4)]);
 #pragma unroll
           for (int f = 0; f < 2; ++f) {
-            const float sc = ue8m0_value(((s ? rws[slot][f].y : rws[slot][f].x) >> (8 * lg)) & 0xffu);
+            const uint32_t wd = (uint32_t)rw[slot][f][4 * s + j];
+            const v4i wv{__builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 0)),
+                         __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 1)),
+                         __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 2)),
+                         __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 3))};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint32_t wd = (uint32_t)rw[slot][f][4 * s + j];
-              const v4i wv{__builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 0)),
-                           __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 1)),
-                           __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 2)),
-                           __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc, 3))};
-              const uint32_t c = 16 * s + 4 * lg + j;
-              const v4i av = *reinterpret_cast<const v4i*>(pa + ((c ^ lr) << 4));
+            for (uint32_t r = 0; r < NA; ++r)
               acc[f][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, wv),
-                                                                  __builtin_bit_cast(v8bf, av), acc[f][r], 0, 0, 0);
-            }
+                                                                  __builtin_bit_cast(v8bf, av[r]), acc[f][r], 0, 0, 0);
           }
         }
       }
-    };
-    // every activation fragment is computed (rows past the expert read its
-    // first row and are never stored): MFMA time stays below the stream time
-    frag(std::integral_constant<int, 0>{});
-    frag(std::integral_constant<int, 1>{});
-    if constexpr (NA > 2) {
-      frag(std::integral_constant<int, 2>{});
-      frag(std::integral_constant<int, 3>{});
     }
     // Pin this step's results here: the MFMAs read only registers, and the
     // optimiser would otherwise sink them past later barriers, keeping every
@@ -345,6 +370,9 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
       stage(j % kDepth, j & 1);
       __syncthreads();
       compute(j % kDepth, j & 1);
+      // keep the next loads after this step's compute (hoisting them would
+      // keep two steps' operands live)
+      __builtin_amdgcn_sched_barrier(0);
       if (j + kDepth < KBT) load(j % kDepth, j + kDepth);
     }
   } else {
@@ -479,7 +507,7 @@ uint32_t Fp4MoeLightRows(const Fp4GemmArgs& a) {
                     (uint64_t)a.a_rows_total * a_row < (1ull << 32) && (uint64_t)a.n * (a.k / 2) < (1ull << 32) &&
                     (uint64_t)a.n * (a.k / 32) < (1ull << 32);
   if (!fits) return 0;
-  return a.act == kActBf16 ? kMoeLightRowsBf16 : kMoeLightRows;
+  return kMoeLightRows;
 }
 
 // Called by LaunchFp4Gemm after its checks, for the light experts of a MoE
@@ -503,8 +531,9 @@ St LaunchFp4MoeStream(const Fp4GemmArgs& a) {
   sp.out_row_stride = a.out_kind == kOutSwiGlu ? a.n / 2 : a.n;
   sp.nblk = a.n / BNW;
   sp.limit = a.swiglu_limit;
-  // at most min(experts, rows) light experts, nblk items each
-  const uint64_t light = a.problems < a.m ? a.problems : a.m;
+  // row chunks: at most one per non-empty expert plus rows / (rows per pass)
+  const uint64_t per_pass = a.act == kActBf16 ? Act<kActBf16>::MAXR : Act<kActE4m3>::MAXR;
+  const uint64_t light = (a.problems < a.m ? a.problems : a.m) + a.m / per_pass;
   const uint64_t total = light * sp.nblk;
   if (total == 0 || total > 0x7fffffffull - 8) return Invalid("fp4_moe_stream_grid_too_large");
   const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
