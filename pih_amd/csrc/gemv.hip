@@ -2,6 +2,11 @@
 // (1..64), with W in bf16 or INT4 (W4A16, symmetric reference format or
 // asymmetric u32-packed format).  Memory-bound: the kernel streams W once.
 //
+// Three kernels: gemv_lds_kernel for M <= 4 (x staged in LDS per wave),
+// gemv_mid_kernel for 4 < M <= 64 (W and x read as whole 128-byte lines and
+// turned into the MFMA layout in LDS), and gemv_kernel, described here, for
+// the shapes whose K does not split evenly over the others' waves.
+//
 // Layout of the work: a block owns 16 W rows (one MFMA column block) and
 // its 4, 8 or 16 waves split K into contiguous runs (more waves for small N,
 // so every shape keeps ~2048 waves streaming).  Each lane loads 16
@@ -561,6 +566,257 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
     if (nonfinite) publish(p.err, kQwenNonFinite);
 }
 
+// ---------------------------------------------------------------------------
+// Mid-M decode GEMV (4 < M <= 64).
+//
+// x is too large to stage per block (M x K bf16 is 128 KB at M = 16,
+// K = 4096) and every block reads it from L2 again, so x traffic is
+// 2M / w_bytes times the W traffic per W row block (4x for INT4 at M = 16,
+// 4x for bf16 at M = 64).  What bounds the kernel is therefore how fast a
+// CU reads L2-resident data, and that depends on the access pattern of one
+// instruction (measured on MI355X, all CUs reading a 512 KB array):
+// 16 rows x 64 B per instruction (the MFMA operand layout) ~9 TB/s in
+// total, 8 rows x 128 B ~25 TB/s, 1 KB contiguous ~32 TB/s.  So W and x are
+// both loaded as whole 128-byte lines, 8 rows per instruction, two MFMA
+// steps per line (a W step is 64 bytes of a row in both formats; an x step
+// is 64 (bf16) or 256 (INT4) bytes of a row), and each wave turns them into
+// the MFMA layout through its own LDS tiles.
+//
+// A block owns NW 16-row W blocks and its waves split K into equal runs of
+// spw steps (WAVES * spw = K / SK, U even and U | spw); a batch of U steps
+// issues every W line, the U group scales of each W row in one vector load,
+// the zero points in one u32, and every x line before any math, so each
+// x fragment feeds NW MFMA column blocks.
+//   INT4: nibbles become bf16 (128 + u) by two masks and four v_perm per
+//   word (nibbles_to_bf16, x permuted to the same k order in registers), and
+//   sum_k x per group comes from one MFMA of x against ones per x fragment,
+//   shared by the NW W blocks.
+// Rows m >= M of an MFMA tile read row M - 1 of x; their sums are never
+// stored.  The waves' partial sums meet in LDS in fixed wave order, one W
+// block at a time.
+template <int FMT>
+constexpr uint32_t mid_x_pitch() {  // bytes per row of an x tile (two steps + pad)
+  return FMT == kWBf16 ? 2 * 64 + 16 : 2 * 256 + 16;
+}
+constexpr uint32_t kMidWPitch = 2 * 64 + 16;
+
+template <int FMT, int MT, int NW, int WAVES, int U>
+constexpr uint32_t mid_lds_bytes() {
+  return WAVES * (U / 2) * 16 * (NW * kMidWPitch + MT * mid_x_pitch<FMT>()) + WAVES * MT * 4 * 64 * 4;
+}
+
+template <int FMT, int MT, int NW, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void gemv_mid_kernel(GemvGroup grp, uint32_t spw) {
+  static_assert(U % 2 == 0, "a batch is whole step pairs");
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint32_t pi = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxGroup; ++i)
+    if ((uint32_t)i < grp.count && blockIdx.x >= grp.block_start[i]) pi = i;
+  GemvParams p = grp.prob[0];
+#pragma unroll
+  for (int i = 1; i < kMaxGroup; ++i)
+    if (pi == (uint32_t)i) p = grp.prob[i];
+  const uint32_t block = blockIdx.x - grp.block_start[pi];
+  constexpr bool kInt4 = FMT != kWBf16;
+  constexpr int P = U / 2;                           // step pairs per batch
+  constexpr uint32_t XP = mid_x_pitch<FMT>();        // x tile row pitch
+  constexpr int XC = kInt4 ? 4 : 1;                  // 128-byte x lines per row and pair
+  constexpr int XL = kInt4 ? 4 : 1;                  // 16-byte x fragments per lane, step and M tile
+  constexpr uint32_t kWaveTiles = P * 16 * (NW * kMidWPitch + MT * XP);
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t lr = lane & 15, lg = lane >> 4;
+  const uint32_t lrow = lane >> 3, lcol = (lane & 7) * 16;  // line-load position
+  const uint32_t n0 = block * 16 * NW;
+  const uint32_t K = p.k, M = p.m, G = K / 128;
+  const uint32_t s0 = wave * spw, s1 = s0 + spw;
+  const uint32_t zwords = (G + 7) / 8;
+  const uint64_t w_row_bytes = kInt4 ? K / 2 : (uint64_t)K * 2;
+  uint8_t* wtile = smem + wave * kWaveTiles;                 // [P][NW][16][kMidWPitch]
+  uint8_t* xtile = wtile + P * NW * 16 * kMidWPitch;         // [P][MT][16][XP]
+  float* red = reinterpret_cast<float*>(smem + WAVES * kWaveTiles);  // [WAVES][MT][4][64]
+
+  const uint8_t* wsrc[NW][2];
+#pragma unroll
+  for (int b = 0; b < NW; ++b)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      wsrc[b][h] = static_cast<const uint8_t*>(p.w) + (uint64_t)(n0 + b * 16 + 8 * h + lrow) * w_row_bytes + lcol;
+  const uint8_t* xsrc[MT][2];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      xsrc[t][h] = reinterpret_cast<const uint8_t*>(p.x + (uint64_t)min(t * 16 + 8 * h + lrow, M - 1) * K) + lcol;
+
+  v4i wl[P][NW][2];
+  v4i xl[P][MT][2][XC];
+  ScaleVec<U> sv[NW];
+  uint32_t zw[NW];
+  auto issue = [&](uint32_t sb) {
+#pragma unroll
+    for (int b = 0; b < NW; ++b) {
+      const uint32_t row = n0 + b * 16 + lr;
+      if constexpr (kInt4) sv[b].load(p.scales + (uint64_t)row * G + sb);
+      if constexpr (FMT == kWAsym) zw[b] = p.zeros[(uint64_t)row * zwords + sb / 8];
+    }
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      const uint64_t st = sb + 2 * q;  // first step of the pair
+#pragma unroll
+      for (int b = 0; b < NW; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          wl[q][b][h] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wsrc[b][h] + st * 64));
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int c = 0; c < XC; ++c)
+            xl[q][t][h][c] = *reinterpret_cast<const v4i*>(xsrc[t][h] + st * (kInt4 ? 256 : 64) + c * 128);
+    }
+  };
+
+  v4f acc[NW][MT];
+#pragma unroll
+  for (int b = 0; b < NW; ++b)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[b][t] = v4f{0.f, 0.f, 0.f, 0.f};
+  uint32_t bad = 0;
+  const v8bf ones = __builtin_bit_cast(v8bf, v4i{0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80});
+
+  auto compute = [&](uint32_t sb) {
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      // lines -> tiles (row 8h + lrow, bytes c*128 + lcol of the pair)
+      uint8_t* wt = wtile + q * NW * 16 * kMidWPitch;
+      uint8_t* xt = xtile + q * MT * 16 * XP;
+#pragma unroll
+      for (int b = 0; b < NW; ++b)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          *reinterpret_cast<v4i*>(wt + (b * 16 + 8 * h + lrow) * kMidWPitch + lcol) = wl[q][b][h];
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int c = 0; c < XC; ++c)
+            *reinterpret_cast<v4i*>(xt + (t * 16 + 8 * h + lrow) * XP + c * 128 + lcol) = xl[q][t][h][c];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        // MFMA layout of step s: lane (lr, lg) takes row lr, 16 bytes lg of
+        // the step (W and bf16 x) or 64 bytes lg of the step (INT4 x)
+        v4i wf[NW], xf[MT][XL];
+#pragma unroll
+        for (int b = 0; b < NW; ++b)
+          wf[b] = *reinterpret_cast<const v4i*>(wt + (b * 16 + lr) * kMidWPitch + s * 64 + lg * 16);
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < XL; ++i)
+            xf[t][i] = *reinterpret_cast<const v4i*>(xt + (t * 16 + lr) * XP +
+                                                     (kInt4 ? s * 256 + lg * 64 + i * 16 : s * 64 + lg * 16));
+        if constexpr (FMT == kWBf16) {
+#pragma unroll
+          for (int b = 0; b < NW; ++b)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+              acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xf[t][0]),
+                                                                  __builtin_bit_cast(v8bf, wf[b]), acc[b][t], 0, 0, 0);
+        } else {
+          const int u = 2 * q + s;  // step inside the batch
+          const uint32_t st = sb + u;
+          v4f xs[MT];
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xf[t][i] = x_in_nibble_order(xf[t][i]);
+            xs[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              xs[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xf[t][i]), ones, xs[t], 0, 0,
+                                                              0);
+          }
+#pragma unroll
+          for (int b = 0; b < NW; ++b) {
+            float sc;
+            int zero;
+            if constexpr (FMT == kWSym) {
+              sc = (float)__builtin_bit_cast(_Float16, (uint16_t)sv[b].bits(u));
+              zero = 8;
+            } else {
+              sc = bf16_bits_to_f32(sv[b].bits(u));
+              zero = (int)((zw[b] >> (4 * (st % 8))) & 0xfu);
+            }
+            if (!(sc > 0.0f) || !__builtin_isfinite(sc)) bad = bad ? bad : kQwenBadScale;
+            uint32_t wd[4] = {(uint32_t)wf[b][0], (uint32_t)wf[b][1], (uint32_t)wf[b][2], (uint32_t)wf[b][3]};
+            if constexpr (FMT == kWSym) {
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const uint32_t v = wd[i] ^ 0x88888888u;  // two's complement nibble -> u = q + 8; reserved 8 -> 0
+                if ((v - 0x11111111u) & ~v & 0x88888888u) bad = kQwenReservedNibble;
+                wd[i] = v;
+              }
+            }
+            v4i qb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nibbles_to_bf16(wd[i], qb[i]);
+            const float zc = 128.0f + (float)zero;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+              v4f pq = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                pq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, xf[t][i]),
+                                                             __builtin_bit_cast(v8bf, qb[i]), pq, 0, 0, 0);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                acc[b][t][i] = __builtin_fmaf(__builtin_fmaf(-zc, xs[t][i], pq[i]), sc, acc[b][t][i]);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  for (uint32_t sb = s0; sb < s1; sb += U) {
+    issue(sb);
+    // every load of the batch is in flight before the first one is used
+    __builtin_amdgcn_sched_barrier(0);
+    compute(sb);
+  }
+  if constexpr (kInt4)
+    if (bad) publish(p.err, bad);
+
+  // ---- reduce the block's waves in wave order, one W block at a time;
+  // lane (lr, lg) of tile t holds rows t*16 + 4*lg + i of column lr
+  uint32_t nonfinite = 0;
+#pragma unroll
+  for (int b = 0; b < NW; ++b) {
+    if (b) __syncthreads();  // the previous block's sums have been read
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[((wave * MT + t) * 4 + i) * 64 + lane] = acc[b][t][i];
+    __syncthreads();
+    for (uint32_t slot = tid; slot < (uint32_t)MT * 256; slot += WAVES * 64) {
+      const uint32_t t = slot / 256, i = (slot / 64) % 4, l = slot % 64;
+      const uint32_t mrow = t * 16 + 4 * (l >> 4) + i, col = n0 + b * 16 + (l & 15);
+      if (mrow >= M) continue;
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) v += red[((w * MT + t) * 4 + i) * 64 + l];
+      if (!__builtin_isfinite(v)) nonfinite = 1;
+      if (p.out_f32) static_cast<float*>(p.out)[(uint64_t)mrow * p.n + col] = v;
+      else static_cast<uint16_t*>(p.out)[(uint64_t)mrow * p.n + col] = (uint16_t)f32_to_bf16_bits(v);
+    }
+  }
+  if constexpr (kInt4)
+    if (nonfinite) publish(p.err, kQwenNonFinite);
+}
+
 // Exact dequant of an INT4 weight to fp32: w[n, k] = (q - z) * s (asym) or
 // q * s (sym), the values the GEMV multiplies (as integers times the
 // group scale).
@@ -678,6 +934,65 @@ St launch_group_lds(const GemvGroup& g, hipStream_t s, bool& taken) {
   }
 }
 
+template <int FMT, int MT, int NW, int WAVES, int U>
+St launch_mid(const GemvGroup& g, uint32_t spw, hipStream_t s) {
+  constexpr uint32_t lds = mid_lds_bytes<FMT, MT, NW, WAVES, U>();
+  static_assert(lds <= 160 * 1024, "mid GEMV tiles exceed the LDS");
+  if constexpr (lds > 65536) {
+    static bool raised = false;  // LDS above 64 KB must be allowed once per kernel
+    if (!raised) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_mid_kernel<FMT, MT, NW, WAVES, U>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+        return Internal("gemv_mid_attribute_failed");
+      raised = true;
+    }
+  }
+  hipLaunchKernelGGL((gemv_mid_kernel<FMT, MT, NW, WAVES, U>), dim3(g.block_start[g.count]), dim3(WAVES * 64), lds,
+                     s, g, spw);
+  return AfterLaunch("gemv_launch_failed");
+}
+
+// The mid-M path for a group (same m and k; block_start counts 16-row
+// blocks).  Configurations measured fastest on MI355X for the Qwen3-8B
+// shapes (per 16-row block count: >= 512 is gate/up):
+//   bf16, M <= 16 : one W block per wave, 8 waves (4 at >= 512 blocks), U 4
+//   bf16, M 49..64: 4 W blocks per wave and 4 waves at >= 512 blocks (x is
+//                   4x the W bytes there), else one W block, 8 waves, U 2
+//   bf16, M 17..48: one W block, 8 waves, U 2
+//   INT4, M <= 32 : one W block, 8 waves (4 at >= 512 blocks or M > 16), U 2
+// Returns with `taken` false when the shape does not split evenly (or INT4
+// with M > 32); the caller then uses gemv_kernel.
+template <int FMT>
+St launch_group_mid(GemvGroup g, hipStream_t s, bool& taken) {
+  taken = false;
+  const GemvParams& p = g.prob[0];
+  const uint32_t mt = (p.m + 15) / 16, rows16 = g.block_start[g.count];
+  const uint32_t steps = p.k / step_k<FMT>();
+  int nw = 1, waves = 8, u = 2;
+  if constexpr (FMT == kWBf16) {
+    if (mt == 1) waves = rows16 >= 512 ? 4 : 8, u = 4;
+    else if (mt == 4 && rows16 >= 512) nw = 4, waves = 4;
+  } else {
+    if (mt > 2) return Ok();
+    if (mt == 2 || rows16 >= 512) waves = 4;
+  }
+  if (steps % (uint32_t)waves || (steps / waves) % (uint32_t)u) return Ok();
+  for (uint32_t i = 0; i < g.count; ++i)
+    if (g.prob[i].n % (16u * nw)) return Ok();
+  for (uint32_t i = 0; i < g.count; ++i) g.block_start[i + 1] = g.block_start[i] + g.prob[i].n / (16u * nw);
+  const uint32_t spw = steps / waves;
+  taken = true;
+  if constexpr (FMT == kWBf16) {
+    if (mt == 1) return waves == 4 ? launch_mid<FMT, 1, 1, 4, 4>(g, spw, s) : launch_mid<FMT, 1, 1, 8, 4>(g, spw, s);
+    if (mt == 2) return launch_mid<FMT, 2, 1, 8, 2>(g, spw, s);
+    if (mt == 3) return launch_mid<FMT, 3, 1, 8, 2>(g, spw, s);
+    return nw == 4 ? launch_mid<FMT, 4, 4, 4, 2>(g, spw, s) : launch_mid<FMT, 4, 1, 8, 2>(g, spw, s);
+  } else {
+    if (mt == 2) return launch_mid<FMT, 2, 1, 4, 2>(g, spw, s);
+    return waves == 4 ? launch_mid<FMT, 1, 1, 4, 2>(g, spw, s) : launch_mid<FMT, 1, 1, 8, 2>(g, spw, s);
+  }
+}
+
 GemvGroup single(const GemvParams& p) {
   GemvGroup g{};
   g.prob[0] = p;
@@ -689,7 +1004,7 @@ GemvGroup single(const GemvParams& p) {
 template <int FMT>
 St launch_gemv(const GemvParams& p, hipStream_t s) {
   bool taken;
-  const St st = launch_group_lds<FMT>(single(p), s, taken);
+  const St st = p.m <= kSmallM ? launch_group_lds<FMT>(single(p), s, taken) : launch_group_mid<FMT>(single(p), s, taken);
   if (taken) return st;
   const int waves = waves_for<FMT>(p.n);
   switch ((p.m + 15) / 16) {
@@ -787,8 +1102,11 @@ St LaunchW4a16Grouped(const W4a16Args* probs, uint32_t count) {
   St clean = RequireCleanLastError();
   if (!clean.ok()) return clean;
   bool taken;
-  const St st = a0.symmetric ? launch_group_lds<kWSym>(g, a0.stream, taken)
-                             : launch_group_lds<kWAsym>(g, a0.stream, taken);
+  St st;
+  if (a0.m <= kSmallM)
+    st = a0.symmetric ? launch_group_lds<kWSym>(g, a0.stream, taken) : launch_group_lds<kWAsym>(g, a0.stream, taken);
+  else
+    st = a0.symmetric ? launch_group_mid<kWSym>(g, a0.stream, taken) : launch_group_mid<kWAsym>(g, a0.stream, taken);
   if (taken) return st;
   for (uint32_t i = 0; i < count; ++i) {  // shapes without the small-M path: one launch each
     const St one = a0.symmetric ? launch_gemv<kWSym>(g.prob[i], a0.stream) : launch_gemv<kWAsym>(g.prob[i], a0.stream);

@@ -93,6 +93,20 @@ def test_bf16_gemv_decode(eng, m, n, k):
     assert_close(_bf16_gemm(a, w, abi.OUTPUT_F32, use_ws=False), ref, f"bf16 gemv no-ws {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(5, 1024, 4096), (20, 1024, 4096), (40, 256, 1024), (64, 8192, 1024),
+                                   (16, 8192, 1024), (64, 1024, 4096), (24, 256, 1152)])
+def test_bf16_gemv_mid_m(eng, m, n, k):
+    """4 < M <= 64: every configuration of the line-loading mid-M kernel
+    (M tiles 1-4; 8192 rows take the 4-W-block and 4-wave variants) and, at
+    K = 1152 (36 steps, no even split over 8 waves with 4-step batches),
+    the gemv_kernel fallback."""
+    a = synth.bf16_normal(synth.config_seed(2, 60 + m), (m, k))
+    w = synth.bf16_normal(synth.config_seed(2, 70 + n), (n, k), std=0.02)
+    ref = oracle.bf16_gemm(a, w)
+    assert_close(_bf16_gemm(a, w, abi.OUTPUT_BF16), ref, f"bf16 gemv {m}x{n}x{k}")
+    assert_close(_bf16_gemm(a, w, abi.OUTPUT_F32, use_ws=False), ref, f"bf16 gemv no-ws {m}x{n}x{k}")
+
+
 # ----------------------------------------------------------------- W4A16
 def _w4a16(x, q, s, z, fmt, m, n, k):
     import torch
@@ -145,6 +159,40 @@ def test_w4a16_asym(eng, m, n, k):
     assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref), f"w4a16 asym {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(5, 1024, 4096), (20, 1024, 4096), (32, 8192, 1024), (9, 8192, 1024),
+                                   (9, 256, 1152)])
+def test_w4a16_asym_mid_m(eng, m, n, k):
+    """4 < M <= 32 on the mid-M kernel (one and two M tiles, 8 and 4 waves);
+    K = 1152 (9 groups) does not split over its waves and takes
+    gemv_kernel."""
+    q, s, z = synth.int4_asym_weight(synth.config_seed(3, 4000 + n + k), n, k)
+    x = synth.bf16_normal(synth.config_seed(3, 4100 + m), (m, k))
+    got, flag = _w4a16(x, q, s, z, abi.W4A16_ASYMMETRIC, m, n, k)
+    assert flag == 0
+    ref = oracle.w4a16_asym(x, q, s, z)
+    assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref), f"w4a16 asym {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m", [9, 20])
+def test_w4a16_symmetric_mid_m_and_errors(eng, m):
+    """Reference format on the mid-M kernel: results against the oracle, then
+    a reserved nibble raises code 12 and a negative scale code 13."""
+    n, k = 1024, 2048
+    q, s = synth.int4_sym_weight(synth.config_seed(3, 4200 + m), n, k)
+    x = synth.bf16_normal(synth.config_seed(3, 4300 + m), (m, k))
+    got, flag = _w4a16(x, q, s, None, abi.W4A16_SYMMETRIC, m, n, k)
+    assert flag == 0
+    assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(oracle.w4a16_sym(x, q, s)), f"sym {m}")
+    q2 = q.copy()
+    q2[517, 300] = (q2[517, 300] & 0x0F) | 0x80  # reserved nibble (high half)
+    _, flag = _w4a16(x, q2, s, None, abi.W4A16_SYMMETRIC, m, n, k)
+    assert flag == 12
+    s2 = s.copy()
+    s2[1000, 15] = 0xBC00  # -1.0
+    _, flag = _w4a16(x, q, s2, None, abi.W4A16_SYMMETRIC, m, n, k)
+    assert flag == 13
+
+
 def _w4a16_grouped(xs, weights, fmt, m, k):
     """weights: list of (q, s, z, n); xs: list of bf16 inputs [m, k]."""
     import torch
@@ -173,8 +221,8 @@ def _w4a16_grouped(xs, weights, fmt, m, k):
 @pytest.mark.parametrize("m", [1, 4, 16])
 def test_w4a16_grouped_qkv_and_gate_up(eng, m):
     """q/k/v and gate/up of Qwen3-8B as two grouped launches (one input per
-    problem); each output against the oracle's strict-k sum.  m = 16 takes
-    the per-problem fallback path."""
+    problem); each output against the oracle's strict-k sum.  m = 1 and 4
+    run the small-M kernel, m = 16 the mid-M kernel, one launch per group."""
     k = 4096
     for ns in ((4096, 1024, 1024), (12288, 12288)):
         weights = [synth.int4_asym_weight(synth.config_seed(3, 3000 + i + n), n, k) + (n,) for i, n in enumerate(ns)]
