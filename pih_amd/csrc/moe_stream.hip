@@ -18,11 +18,14 @@
 // dead activation rows when an expert has a few rows):
 //   * a block of 4 waves owns 128 W rows of one light expert (<= 64 rows)
 //     and up to 64 (e4m3) or 32 (bf16) of its rows; each wave owns 32
-//     W rows (two 16-row MFMA fragments) and loads them straight into
-//     registers in the MFMA operand layout, non-temporal, 3-4 steps of
-//     256 k ahead (lane (lr, lg): row lr, bytes [16lg, +16) and
-//     [64 + 16lg, +16) of the row's 128-byte step: the 32 k of sub-step 0
-//     and of sub-step 1 that the lane's group multiplies);
+//     W rows (two 16-row MFMA fragments) and loads them into registers,
+//     non-temporal, 3-4 steps of 256 k ahead, as whole 128-byte lines (8
+//     rows x 128 B per instruction, four per step: the MFMA operand layout,
+//     16 rows x 64 B per instruction, streams ~25 % slower from HBM); a
+//     wave-private LDS tile turns each step into the operand layout (lane
+//     (lr, lg): row lr, bytes [16lg, +16) and [64 + 16lg, +16) of the row's
+//     128-byte step, the 32 k of sub-step 0 and of sub-step 1 that the
+//     lane's group multiplies);
 //   * the expert's activation rows (only the 16-row groups it has: staging
 //     loads cost as much as the weight stream when a tile is mostly dead
 //     rows) go through a double-buffered LDS tile
@@ -48,6 +51,7 @@ namespace {
 constexpr int NTH = 256;    // 4 waves
 constexpr int BNW = 128;    // W rows per block
 constexpr int KSTEP = 256;  // k per step: 128 weight bytes per row
+constexpr uint32_t kWPitch = 144;  // W tile row: one 128-byte step + pad
 
 template <int ACT>
 struct Act {
@@ -178,6 +182,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   constexpr uint32_t RPI = C::RPI;    // staging instruction i covers rows [i RPI, (i + 1) RPI)
   __shared__ __align__(16) uint8_t sA[2][MAXR * ROW];
   __shared__ __align__(16) uint32_t sSa[2][MAXR];  // e4m3: the row's 2 scale bytes of the step
+  __shared__ __align__(16) uint8_t sW[NTH / 64][32 * kWPitch];  // per wave: its 32 W rows of one step
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
@@ -216,25 +221,28 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   // activation scales (e4m3): thread t < MAXR loads the 2 bytes of row t
   const uint32_t s_off = a_source(tid < MAXR ? tid : 0u) * (K / 128);
 
-  // W rows of this wave: fragment f, lane row lr
-  auto w_row = [&](int f) -> uint32_t {
+  // W rows of this wave: fragment f, fragment row r
+  auto w_row = [&](uint32_t f, uint32_t r) -> uint32_t {
     if constexpr (OUT == kOutSwiGlu) {
-      const uint32_t c = wb * (BNW / 2) + wave * 16 + lr;  // output column
+      const uint32_t c = wb * (BNW / 2) + wave * 16 + r;  // output column
       return f ? p.n / 2 + c : c;
     } else {
-      return wb * BNW + wave * 32 + f * 16 + lr;
+      return wb * BNW + wave * 32 + f * 16 + r;
     }
   };
   const uint8_t* w_base = p.w + (uint64_t)expert * p.n * (K / 2);
   const uint8_t* ws_base = p.w_scale + (uint64_t)expert * p.n * (K / 32);
-  uint32_t w_off[2], ws_off[2];
-#pragma unroll
-  for (int f = 0; f < 2; ++f) {
-    w_off[f] = w_row(f) * (K / 2) + lg * 16;
-    ws_off[f] = w_row(f) * (K / 32);
-  }
+  // line load i: tile row 8i + lane / 8 (fragment i / 2, fragment row
+  // 8 (i % 2) + lane / 8), bytes 16 (lane % 8) of the step.  The rows of
+  // fragment 1 sit a uniform distance after those of fragment 0, so each
+  // load is one per-lane offset plus a wave-uniform one.
+  const uint32_t frag_rows = OUT == kOutSwiGlu ? p.n / 2 : 16u;
+  const uint32_t w_off = w_row(0, lane >> 3) * (K / 2) + (lane & 7) * 16;
+  const uint32_t ws_off = w_row(0, lr) * (K / 32);
+  const uint32_t ws_d1 = frag_rows * (K / 32);
+  uint8_t* wtile = sW[wave];
 
-  v8i rw[kDepth][2];     // weights: [step][fragment], sub-step 0 low, 1 high
+  v4i rl[kDepth][4];     // weight lines of the step (tile rows 8i .. 8i + 7)
   uint2 rws[kDepth][2];  // weight scales of the step (8 bytes per row)
   v4i ra[kDepth][CH];    // activation chunks
   uint32_t rsa[kDepth];  // activation scales (e4m3)
@@ -242,12 +250,13 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
     const uint32_t kc = min(kb, last);
     const uint8_t* wb8 = w_base + (uint64_t)kc * 128;
 #pragma unroll
-    for (int f = 0; f < 2; ++f)
-      rw[slot][f] = cat8(__builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb8 + w_off[f])),
-                         __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wb8 + 64 + w_off[f])));
+    for (uint32_t i = 0; i < 4; ++i) {
+      const uint8_t* line = wb8 + (uint64_t)((i & 1) * 8 + (i >> 1) * frag_rows) * (K / 2);  // wave-uniform
+      rl[slot][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(line + w_off));
+    }
     const uint8_t* sb8 = ws_base + (uint64_t)kc * 8;
-#pragma unroll
-    for (int f = 0; f < 2; ++f) rws[slot][f] = *reinterpret_cast<const uint2*>(sb8 + ws_off[f]);
+    rws[slot][0] = *reinterpret_cast<const uint2*>(sb8 + ws_off);
+    rws[slot][1] = *reinterpret_cast<const uint2*>(sb8 + ws_d1 + ws_off);
     // only the staging instructions that cover live rows (the tile rows past
     // the expert's are never stored; their LDS contents are left stale)
     const uint8_t* ab = static_cast<const uint8_t*>(p.a) + (uint64_t)kc * ROW;
@@ -289,6 +298,16 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
 #pragma unroll
     for (int f = 0; f < 2; ++f)
       if (ff_bytes(rws[slot][f].x) | ff_bytes(rws[slot][f].y)) bad |= kErrScale;
+    // the step's lines through the wave's tile into the operand layout (a
+    // wave's LDS accesses complete in order: no barrier)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<v4i*>(wtile + (8 * i + (lane >> 3)) * kWPitch + (lane & 7) * 16) = rl[slot][i];
+    // fragment f, sub-step s: row f*16 + lr, bytes 64 s + 16 lg (read where
+    // used, so only the current sub-step's weights occupy registers)
+    auto wfrag = [&](int f, int s) -> v4i {
+      return *reinterpret_cast<const v4i*>(wtile + (f * 16 + lr) * kWPitch + s * 64 + lg * 16);
+    };
     if constexpr (ACT == kActE4m3) {
       auto frag = [&](auto R) __attribute__((always_inline)) {
         constexpr int r = decltype(R)::value;
@@ -303,8 +322,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
           const int sa = (int)((sSa[buf][row] >> (8 * s)) & 0xffu);
 #pragma unroll
           for (int f = 0; f < 2; ++f) {
-            const v8i w = rw[slot][f];
-            const v4i w4 = s ? v4i{w[4], w[5], w[6], w[7]} : v4i{w[0], w[1], w[2], w[3]};
+            const v4i w4 = wfrag(f, s);
             const int sw = (int)(((s ? rws[slot][f].y : rws[slot][f].x) >> (8 * lg)) & 0xffu);
             acc[f][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cat8(w4, v4i{0, 0, 0, 0}), af, acc[f][r],
                                                                          4, 0, 0, sw, 0, sa);
@@ -323,6 +341,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
       // per fragment, against chunk 16s + 4lg + j of each activation row
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
+        const v4i w4[2] = {wfrag(0, s), wfrag(1, s)};
         float sc[2];
 #pragma unroll
         for (int f = 0; f < 2; ++f) sc[f] = ue8m0_value(((s ? rws[slot][f].y : rws[slot][f].x) >> (8 * lg)) & 0xffu);
@@ -335,7 +354,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
             av[r] = *reinterpret_cast<const v4i*>(&sA[buf][(r * 16 + lr) * ROW + ((c ^ lr) << 4)]);
 #pragma unroll
           for (int f = 0; f < 2; ++f) {
-            const uint32_t wd = (uint32_t)rw[slot][f][4 * s + j];
+            const uint32_t wd = (uint32_t)w4[f][j];
             const v4i wv{__builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 0)),
                          __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 1)),
                          __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 2)),
