@@ -29,12 +29,16 @@
 //     wn*64 + [0,64): 4 x 4 MFMAs of 16x16x128 per K step;
 //   * fp32 scales: each MFMA starts from zero and the lane adds
 //     t * (a_scale[row] * w_scale[block]) in fp32 (DeepSeek-V3 promotion,
-//     bit-identical to the 128x128-tile kernel); UE8M0 scales ride in the
-//     MFMA's E8M0 operands and the MFMAs chain on the accumulator.
+//     bit-identical to the 128x128-tile kernel), software-pipelined so the
+//     FMAs of one A block run while the next block's MFMAs execute; UE8M0
+//     scales ride in the MFMA's E8M0 operands and the MFMAs chain on the
+//     accumulator.
 // Tiles are numbered expert-major and, inside an expert, in groups of up to
 // 32 M-tiles walked M-fastest; each XCD (blocks b % 8) walks one contiguous
 // range of that order so concurrently running tiles share W and A in its L2.
 // (An 8 M x 4 N grouping cut the L2-miss bytes by 9 % but ran 3 % slower.)
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -308,39 +312,69 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       const uint8_t* pa = sA(stage) + (wm * 64 + r * 16 + lr) * LDS_ROW;
       return cat8(*reinterpret_cast<const v4i*>(pa + rd0), *reinterpret_cast<const v4i*>(pa + (rd0 ^ 64)));
     };
-    auto mma = [&](int r, const v8i& af) {
-      if constexpr (SCALE == kScaleF32) {
-        const float sa = __uint_as_float((uint32_t)sa4[r]);
-        const float c0 = sa * __uint_as_float(sw0), c1 = sa * __uint_as_float(sw1);
-        v4f t[4];
+    if constexpr (SCALE == kScaleF32) {
+      // fp32 scales: each MFMA starts from zero and its result is added
+      // with one FMA per output.  Software-pipelined: the four MFMAs of A
+      // block r + 1 are issued before the FMAs of block r, so those read
+      // results that finished while the next MFMAs ran (consuming a result
+      // right after its MFMA stalls the wave for the MFMA's latency).
+      auto mfma4 = [&](const v8i& af, v4f (&t)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
           t[nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[nb], af, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
                                                                    127, 0, 127);
+      };
+      auto fma4 = [&](auto R, const v4f (&t)[4]) __attribute__((always_inline)) {
+        constexpr int r = decltype(R)::value;
+        const float sa = __uint_as_float((uint32_t)sa4[r]);
+        const float c0 = sa * __uint_as_float(sw0), c1 = sa * __uint_as_float(sw1);
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
           const float c = (OUT == kOutSwiGlu && nb >= 2) ? c1 : c0;
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[nb][r][i] = __builtin_fmaf(t[nb][i], c, acc[nb][r][i]);
         }
-      } else {
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+      using I2 = std::integral_constant<int, 2>;
+      using I3 = std::integral_constant<int, 3>;
+      v4f tA[4], tB[4];
+      const v8i af0 = a_frag(0), af1 = a_frag(1);
+      mfma4(af0, tA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb_live > 1) mfma4(af1, tB);
+      const v8i af2 = a_frag(2), af3 = a_frag(3);
+      fma4(I0{}, tA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb_live > 2) mfma4(af2, tA);
+      if (rb_live > 1) fma4(I1{}, tB);
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb_live > 3) mfma4(af3, tB);
+      if (rb_live > 2) fma4(I2{}, tA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (rb_live > 3) fma4(I3{}, tB);
+    } else {
+      // UE8M0 scales ride in the MFMA's E8M0 operands and the MFMAs chain on
+      // the accumulator
+      auto mma = [&](int r, const v8i& af) {
         const int sb = (int)sa4[r];
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
           acc[nb][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
               wf[nb], af, acc[nb][r], 0, 0, 0, (int)((OUT == kOutSwiGlu && nb >= 2) ? sw1 : sw0), 0, sb);
-      }
-    };
-    // A fragments one block ahead (at most four LDS reads in flight)
-    v8i af = a_frag(0);
+      };
+      // A fragments one block ahead (at most four LDS reads in flight)
+      v8i af = a_frag(0);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (r < (int)rb_live) {
-        const v8i afn = a_frag(r < 3 ? r + 1 : 3);
-        mma(r, af);
-        af = afn;
+      for (int r = 0; r < 4; ++r) {
+        if (r < (int)rb_live) {
+          const v8i afn = a_frag(r < 3 ? r + 1 : 3);
+          mma(r, af);
+          af = afn;
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
