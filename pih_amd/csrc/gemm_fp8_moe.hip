@@ -33,10 +33,9 @@
 //     FMAs of one A block run while the next block's MFMAs execute; UE8M0
 //     scales ride in the MFMA's E8M0 operands and the MFMAs chain on the
 //     accumulator.
-// Tiles are numbered expert-major and, inside an expert, in groups of up to
-// 32 M-tiles walked M-fastest; each XCD (blocks b % 8) walks one contiguous
-// range of that order so concurrently running tiles share W and A in its L2.
-// (An 8 M x 4 N grouping cut the L2-miss bytes by 9 % but ran 3 % slower.)
+// Tile order: see moe_tile (streaming and multi-tile experts interleaved;
+// an 8 M x 4 N grouping of the multi-tile ones cut the L2-miss bytes by
+// 9 % but ran 3 % slower than M-fastest groups of 32).
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -84,72 +83,118 @@ __device__ __forceinline__ v8i cat8(v4i x, v4i y) {
 }
 
 // Block -> (expert, first row, rows, N tile); false for blocks past the
-// last tile.  The per-expert M-tile counts are scanned by the whole block
-// (one wave-level shuffle scan plus the eight wave totals).
+// last tile.
+//
+// Tile order.  An expert with one M tile (<= 128 rows) reads each weight
+// tile once and is weight-streaming (HBM) work; an expert with more M
+// tiles reuses each weight tile across its M tiles and is MFMA work.  Run
+// one after the other the two kinds add up (cfg4: 0.62 ms of streaming,
+// 1.40 ms of MFMA work), so the tile sequence interleaves them in
+// proportion: position t is a streaming tile when floor((t + 1) L / T)
+// steps up (L streaming tiles of T), and each XCD (blocks b % 8) walks one
+// contiguous range of the sequence, so its CUs run both kinds at once.
+// Streaming experts are ordered by expert index, one M tile x all N tiles
+// each; multi-tile experts are expert-major, in groups of up to 32 M tiles
+// walked M-fastest, so concurrently running tiles share W in L2.
+// The per-expert tile counts are scanned by the whole block (wave-level
+// shuffle scans plus the eight wave totals).
 __device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, uint32_t& rows, uint32_t& nt) {
-  __shared__ uint32_t s_wave[NTH / 64];
+  __shared__ uint32_t s_wave[2][NTH / 64];
   __shared__ uint32_t s_res[3];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t E = p.experts, NTL = p.n_tiles;
   const uint32_t per_t = (E + NTH - 1) / NTH;
-  uint32_t cnt = 0;
+  auto m_tiles = [&](uint32_t e) -> uint32_t {
+    const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
+    return hi > lo ? (hi - lo + BM - 1) / BM : 0u;
+  };
+  uint32_t cnt_h = 0, cnt_s = 0;  // this thread's multi-tile M tiles / streaming experts
   for (uint32_t j = 0; j < per_t; ++j) {
     const uint32_t e = tid * per_t + j;
     if (e < E) {
-      const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
-      cnt += hi > lo ? (hi - lo + BM - 1) / BM : 0u;
+      const uint32_t c = m_tiles(e);
+      cnt_h += c > 1 ? c : 0u;
+      cnt_s += c == 1 ? 1u : 0u;
     }
   }
-  uint32_t incl = cnt;
+  uint32_t inc_h = cnt_h, inc_s = cnt_s;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t v = __shfl_up(incl, off, 64);
-    if ((int)lane >= off) incl += v;
+    const uint32_t vh = __shfl_up(inc_h, off, 64), vs = __shfl_up(inc_s, off, 64);
+    if ((int)lane >= off) inc_h += vh, inc_s += vs;
   }
-  if (lane == 63) s_wave[wave] = incl;
+  if (lane == 63) s_wave[0][wave] = inc_h, s_wave[1][wave] = inc_s;
   if (tid == 0) s_res[0] = 0xffffffffu;
   __syncthreads();
-  uint32_t before = 0, total_m = 0;
+  uint32_t before_h = 0, before_s = 0, tot_h = 0, tot_s = 0;
 #pragma unroll
   for (int w = 0; w < NTH / 64; ++w) {
-    const uint32_t v = s_wave[w];
-    if (w < (int)wave) before += v;
-    total_m += v;
+    const uint32_t vh = s_wave[0][w], vs = s_wave[1][w];
+    if (w < (int)wave) before_h += vh, before_s += vs;
+    tot_h += vh, tot_s += vs;
   }
-  incl += before;
-  const uint32_t excl = incl - cnt;
-  const uint32_t total = total_m * NTL;
-  const uint32_t per = (total + 7) / 8;
+  inc_h += before_h, inc_s += before_s;
+  const uint32_t exc_h = inc_h - cnt_h, exc_s = inc_s - cnt_s;
+  const uint64_t Ls = (uint64_t)tot_s * NTL, T = ((uint64_t)tot_h + tot_s) * NTL;
+  const uint32_t per = (uint32_t)((T + 7) / 8);
   const uint32_t xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
-  const uint32_t t = xcd * per + jj;
-  if (jj >= per || t >= total) return false;  // same for every thread
-  const uint32_t slot = t / NTL;              // M tile, expert-major
-  if (slot >= excl && slot < incl) {
-    uint32_t acc = excl;
-    for (uint32_t j = 0; j < per_t; ++j) {
-      const uint32_t e = tid * per_t + j;
-      if (e >= E) break;
-      const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
-      const uint32_t c = hi > lo ? (hi - lo + BM - 1) / BM : 0u;
-      if (slot < acc + c) {
-        s_res[0] = e;
-        s_res[1] = acc;
-        s_res[2] = c;
-        break;
+  const uint64_t t = (uint64_t)xcd * per + jj;
+  if (jj >= per || t >= T) return false;  // same for every thread
+  const uint32_t s_lo = (uint32_t)(t * Ls / T), s_hi = (uint32_t)((t + 1) * Ls / T);
+  const bool streaming = s_hi > s_lo;
+  uint32_t mtile = 0;
+  if (streaming) {
+    // streaming tile s_lo: expert #(s_lo / NTL) among the one-tile experts
+    const uint32_t k = s_lo / NTL;
+    nt = s_lo % NTL;
+    if (k >= exc_s && k < inc_s) {
+      uint32_t acc = exc_s;
+      for (uint32_t j = 0; j < per_t; ++j) {
+        const uint32_t e = tid * per_t + j;
+        if (e >= E) break;
+        if (m_tiles(e) == 1) {
+          if (k == acc) {
+            s_res[0] = e;
+            break;
+          }
+          ++acc;
+        }
       }
-      acc += c;
+    }
+    __syncthreads();
+  } else {
+    // multi-tile position h = t - s_hi, expert-major over those experts
+    const uint32_t h = (uint32_t)(t - s_hi), slot = h / NTL;
+    if (slot >= exc_h && slot < inc_h) {
+      uint32_t acc = exc_h;
+      for (uint32_t j = 0; j < per_t; ++j) {
+        const uint32_t e = tid * per_t + j;
+        if (e >= E) break;
+        const uint32_t c = m_tiles(e);
+        if (c > 1) {
+          if (slot < acc + c) {
+            s_res[0] = e;
+            s_res[1] = acc;
+            s_res[2] = c;
+            break;
+          }
+          acc += c;
+        }
+      }
+    }
+    __syncthreads();
+    if (s_res[0] != 0xffffffffu) {
+      const uint32_t mbase = s_res[1], mt = s_res[2];
+      const uint32_t local = h - mbase * NTL;
+      const uint32_t mg = local / (GROUP_M * NTL);
+      const uint32_t gsize = min((uint32_t)GROUP_M, mt - mg * GROUP_M);
+      const uint32_t r = local - mg * GROUP_M * NTL;
+      mtile = mg * GROUP_M + r % gsize;
+      nt = r / gsize;
     }
   }
-  __syncthreads();
   const uint32_t e = s_res[0];
   if (e == 0xffffffffu) return false;
-  const uint32_t mbase = s_res[1], mt = s_res[2];
-  const uint32_t local = t - mbase * NTL;
-  const uint32_t mg = local / (GROUP_M * NTL);
-  const uint32_t gsize = min((uint32_t)GROUP_M, mt - mg * GROUP_M);
-  const uint32_t r = local - mg * GROUP_M * NTL;
-  const uint32_t mtile = mg * GROUP_M + r % gsize;
-  nt = r / gsize;
   const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
   if (hi > p.m || lo > hi) {
     if (tid == 0) atomicOr(p.err, p.err_code);
