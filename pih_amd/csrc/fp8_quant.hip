@@ -82,12 +82,18 @@ __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restri
       scale = amax / 448.0f;
       if (sub == 0) static_cast<float*>(scales)[gi] = scale;
     }
-    uint32_t packed[2] = {0u, 0u};
+    // q = v / scale clamped to the e4m3 range, then round-to-nearest-even
+    // to e4m3 by the hardware pack (v_cvt_pk_fp8_f32: operand a to the low
+    // byte of the selected half-word, b to the high byte)
+    float q[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float q = v[i] / scale;
-      q = fminf(fmaxf(q, -448.0f), 448.0f);
-      packed[i >> 2] |= e4m3_encode(q) << (8 * (i & 3));
+    for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(v[i] / scale, -448.0f), 448.0f);
+    uint32_t packed[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * h], q[4 * h + 1], 0, false);
+      w = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * h + 2], q[4 * h + 3], w, true);
+      packed[h] = (uint32_t)w;
     }
     *reinterpret_cast<uint2*>(codes + (uint64_t)row * k + kg * 128u + sub * 8u) =
         make_uint2(packed[0], packed[1]);
