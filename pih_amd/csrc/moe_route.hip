@@ -199,16 +199,30 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* expert_out
   }
   uint32_t bad = 0;
   const uint32_t vec = hidden / 8u;
+  // rows past n (n <= 8 in the unrolled path) repeat row r[0]; their values
+  // are replaced by +0.0f, which leaves the sum unchanged (it starts at +0.0f
+  // and so is never -0.0f), so the sum keeps the ascending row order exactly
+  constexpr uint32_t kUnroll = 8;
   for (uint32_t c = threadIdx.x; c < vec; c += blockDim.x) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (uint32_t j = 0; j < n; ++j) {
-      const uint4 x = reinterpret_cast<const uint4*>(expert_out)[(uint64_t)r[j] * vec + c];
+    auto add = [&](const uint4& x, bool live) {
       const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += bf16_bits_to_f32(w[i] & 0xffffu);
-        acc[2 * i + 1] += bf16_bits_to_f32(w[i] >> 16);
+        acc[2 * i] += live ? bf16_bits_to_f32(w[i] & 0xffffu) : 0.0f;
+        acc[2 * i + 1] += live ? bf16_bits_to_f32(w[i] >> 16) : 0.0f;
       }
+    };
+    if (n > 0 && n <= kUnroll) {
+      // every load first (unconditional, in bounds), then the adds in order
+      uint4 x[kUnroll];
+#pragma unroll
+      for (uint32_t j = 0; j < kUnroll; ++j)
+        x[j] = reinterpret_cast<const uint4*>(expert_out)[(uint64_t)r[j < n ? j : 0] * vec + c];
+#pragma unroll
+      for (uint32_t j = 0; j < kUnroll; ++j) add(x[j], j < n);
+    } else {
+      for (uint32_t j = 0; j < n; ++j) add(reinterpret_cast<const uint4*>(expert_out)[(uint64_t)r[j] * vec + c], true);
     }
     if (shared) {
       const uint4 x = reinterpret_cast<const uint4*>(shared)[(uint64_t)t * vec + c];
