@@ -178,6 +178,10 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   // the 256 registers of two waves per SIMD), 4 in the generic loop (whose
   // 8-step body needs a depth dividing 8)
   constexpr int kDepth = KBT > 0 ? 3 : 4;
+  // whether a chunk of <= 16 rows takes a path computing only its one live
+  // activation fragment (the second copy of the step's code fits the
+  // registers of the unrolled e4m3 loops and of the short bf16 loop)
+  constexpr bool kLiveSplit = KBT > 0 && !(ACT == kActBf16 && KBT > 8);
   constexpr uint32_t CPR = ROW / 16;  // chunks per activation row
   constexpr uint32_t RPI = C::RPI;    // staging instruction i covers rows [i RPI, (i + 1) RPI)
   __shared__ __align__(16) uint8_t sA[2][MAXR * ROW];
@@ -193,6 +197,8 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   row0 = __builtin_amdgcn_readfirstlane(row0);
   rows = __builtin_amdgcn_readfirstlane(rows);
   wb = __builtin_amdgcn_readfirstlane(wb);
+  // live 16-row activation fragments of this chunk (wave-uniform)
+  const uint32_t na_live = __builtin_amdgcn_readfirstlane((rows + 15) / 16);
 
   const uint32_t K = p.k, KB = K / KSTEP, last = KB - 1;
   uint32_t bad = 0;
@@ -329,12 +335,16 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
           }
         }
       };
-      // every activation fragment is computed (rows past the expert's hold
-      // stale data and are never stored): MFMA time stays below the stream
+      // a chunk of <= 16 rows (most decode experts) computes its one live
+      // 16-row activation fragment only: the dead fragments' LDS reads and
+      // MFMAs cost more than the weight stream (rows past the chunk's in a
+      // live fragment hold stale data and are never stored)
       frag(std::integral_constant<int, 0>{});
-      frag(std::integral_constant<int, 1>{});
-      frag(std::integral_constant<int, 2>{});
-      frag(std::integral_constant<int, 3>{});
+      if (!kLiveSplit || na_live > 1) {
+        frag(std::integral_constant<int, 1>{});
+        frag(std::integral_constant<int, 2>{});
+        frag(std::integral_constant<int, 3>{});
+      }
     } else {
       // bf16: MFMA j of sub-step s multiplies k 32lg + 8j .. +7 of the
       // sub-step: weight dword 4s + j (8 nibbles, low first), converted once
@@ -345,26 +355,35 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
         float sc[2];
 #pragma unroll
         for (int f = 0; f < 2; ++f) sc[f] = ue8m0_value(((s ? rws[slot][f].y : rws[slot][f].x) >> (8 * lg)) & 0xffu);
+        // a chunk of <= 16 rows reads and multiplies its one live
+        // activation fragment only (a uniform branch around whole copies
+        // of the loop, so every fragment index stays a constant)
+        auto body = [&](auto NL) __attribute__((always_inline)) {
+          constexpr uint32_t nl = decltype(NL)::value;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t c = 16 * s + 4 * lg + j;
-          v4i av[NA];
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t c = 16 * s + 4 * lg + j;
+            v4i av[nl];
 #pragma unroll
-          for (uint32_t r = 0; r < NA; ++r)
-            av[r] = *reinterpret_cast<const v4i*>(&sA[buf][(r * 16 + lr) * ROW + ((c ^ lr) << 4)]);
+            for (uint32_t r = 0; r < nl; ++r)
+              av[r] = *reinterpret_cast<const v4i*>(&sA[buf][(r * 16 + lr) * ROW + ((c ^ lr) << 4)]);
 #pragma unroll
-          for (int f = 0; f < 2; ++f) {
-            const uint32_t wd = (uint32_t)w4[f][j];
-            const v4i wv{__builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 0)),
-                         __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 1)),
-                         __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 2)),
-                         __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 3))};
+            for (int f = 0; f < 2; ++f) {
+              const uint32_t wd = (uint32_t)w4[f][j];
+              const v4i wv{__builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 0)),
+                           __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 1)),
+                           __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 2)),
+                           __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, sc[f], 3))};
 #pragma unroll
-            for (uint32_t r = 0; r < NA; ++r)
-              acc[f][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, wv),
-                                                                  __builtin_bit_cast(v8bf, av[r]), acc[f][r], 0, 0, 0);
+              for (uint32_t r = 0; r < nl; ++r)
+                acc[f][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, wv),
+                                                                    __builtin_bit_cast(v8bf, av[r]), acc[f][r], 0, 0,
+                                                                    0);
+            }
           }
-        }
+        };
+        if (!kLiveSplit || na_live > 1) body(std::integral_constant<uint32_t, NA>{});
+        else body(std::integral_constant<uint32_t, 1>{});
       }
     }
     // Pin this step's results here: the MFMAs read only registers, and the
