@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void accumulate_kernel(const uint16_t* out, co
 // expert id) + shared).  The fp32 adds run in the order the reference's
 // accumulator oracle applies them (src/model/
 // deepseek_expert_accumulator_oracle.cpp:20-85), so results are bit-exact.
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* expert_out,
+__global__ __launch_bounds__(512) void combine_kernel(const uint16_t* expert_out,
                                                       const uint32_t* token_rows,
                                                       const uint16_t* shared, uint16_t* out,
                                                       uint32_t* err, uint32_t tokens,
@@ -337,7 +337,12 @@ St LaunchMoeCombine(const CombineArgs& a) {
     return Invalid("moe_combine_shape_invalid");
   St clean = RequireCleanLastError();
   if (!clean.ok()) return clean;
-  hipLaunchKernelGGL(combine_kernel, dim3(a.tokens), dim3(256), 0, a.stream, a.expert_out,
+  // one block per token; its threads cover the row's 16-byte chunks in
+  // equal passes (hidden 7168: 896 chunks = 2 passes of 448 threads, where
+  // 256 threads left the fourth pass half empty)
+  const uint32_t vec = a.hidden / 8u, passes = (vec + 511u) / 512u;
+  const uint32_t threads = ((vec + passes - 1) / passes + 63u) / 64u * 64u;
+  hipLaunchKernelGGL(combine_kernel, dim3(a.tokens), dim3(threads), 0, a.stream, a.expert_out,
                      a.token_rows, a.shared, a.out, a.error_flag, a.tokens, a.topk, a.hidden,
                      a.rows);
   return AfterLaunch("moe_combine_launch_failed");
