@@ -6,12 +6,12 @@ renormalised), hidden 7168, expert intermediate 2048, fused gate/up
 7168->4096, SiLU-mul, down 2048->7168; e4m3 weights with fp32 128x128 block
 scales, e4m3 activations with fp32 per-token per-128 scales.  One step is
 one pass of the whole expert layer through the gfx950 packs: device route
-plan -> activation quant -> grouped gate/up GEMM (+SwiGLU*w epilogue) ->
-quant -> grouped down GEMM -> ordered combine.  Inputs are resident in HBM
+plan -> activation quant -> grouped gate/up GEMM (+SwiGLU*w epilogue that
+quantises the intermediate to e4m3) -> grouped down GEMM -> ordered combine.  Inputs are resident in HBM
 before timing starts.
 
 A timed step is one call of the linear pack's C++ layer entry
-(``launch_moe_layer``), which enqueues the six grouped launches; a staged
+(``launch_moe_layer``), which enqueues the five grouped launches; a staged
 copy of the same layer launched stage by stage gives the per-kernel times.
 
 Prints one JSON line.  ``value`` is the layer's TFLOP/s (2*R*(2I*H + H*I)
@@ -395,7 +395,10 @@ def main() -> int:
     flop_gu = 2.0 * R * 2 * I * H
     # algorithmic bytes of the gate/up kernel: weights + scales of touched
     # experts, fp8 activations + scales of all tokens, bf16 mid out
-    bytes_gu = touched * (2 * I * H + (2 * I // 128) * (H // 128) * 4) + T * H + T * (H // 128) * 4 + R * I * 2
+    # weights + fp32 block scales of the touched experts, e4m3 tokens + scales,
+    # e4m3 SwiGLU output + fp32 per-128 scales (the epilogue quantises it)
+    bytes_gu = (touched * (2 * I * H + (2 * I // 128) * (H // 128) * 4) + T * H + T * (H // 128) * 4
+                + R * I + R * (I // 128) * 4)
     bytes_layer = (touched * (3 * I * H + ((2 * I // 128) * (H // 128) + (H // 128) * (I // 128)) * 4)
                    + T * H * 2 + T * H * 2)
 
@@ -476,7 +479,8 @@ def main() -> int:
         "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
         "layer_hbm_gbs": round(bytes_layer / (ms * 1e-3) / 1e9, 1),
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
-        "roofline": {"kernel": "fp8_moe_gemm_kernel<1, 3> (MoE gate/up, SwiGLU epilogue)", "bound": "hbm",
+        "roofline": {"kernel": "fp8_moe_gemm_kernel<1, 4> (MoE gate/up, SwiGLU + e4m3 requant epilogue)",
+                     "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                      "algorithmic_bytes": int(bytes_gu), "flop": flop_gu, "ms": round(gu_ms, 4),

@@ -83,6 +83,7 @@ extern "C" {
  * g, u are the bf16-rounded GEMM results and L = swiglu_limit (<= 0: no
  * clamp). */
 #define PIH_AMD_OUTPUT_SWIGLU_BF16_V1 3U
+#define PIH_AMD_OUTPUT_SWIGLU_E4M3_V1 4U /* launch_moe_fp8_gemm only */
 
 #define PIH_AMD_ACTIVATION_E4M3_V1 1U
 #define PIH_AMD_ACTIVATION_BF16_V1 2U
@@ -153,6 +154,11 @@ typedef struct pih_amd_moe_fp8_gemm_launch_v1 {
   uint32_t row_capacity, expert_count, n, k, activation_rows;
   uint32_t scale_format, output_type;
   float swiglu_limit;
+  /* output_type PIH_AMD_OUTPUT_SWIGLU_E4M3_V1 only: the SwiGLU output is
+   * rounded to bf16 and quantised to e4m3 as launch_fp8_quant would quantise
+   * it; output receives the codes [row_capacity, n/2], output_scale the
+   * scales [row_capacity, n/256] in scale_format.  Otherwise 0. */
+  uintptr_t output_scale;
 } pih_amd_moe_fp8_gemm_launch_v1;
 
 /* Grouped MXFP4-weight GEMM over MoE expert segments: weight e2m1 packed

@@ -190,7 +190,7 @@ LN["moe_fp8_gemm"] = _struct("MoeFp8Gemm", _hdr(
     *_u("activation_e4m3", "activation_scale", "row_token_u32", "weight_e4m3", "weight_scale",
         "expert_offsets_u32", "row_weight_f32", "output", "error_flag_u32", "stream"),
     *_i("row_capacity", "expert_count", "n", "k", "activation_rows", "scale_format", "output_type"),
-    ("swiglu_limit", F32)))
+    ("swiglu_limit", F32), *_u("output_scale")))
 LN["moe_mxfp4_gemm"] = _struct("MoeMxfp4Gemm", _hdr(
     *_u("activation", "activation_scale_ue8m0", "row_token_u32", "packed_weight", "weight_scale_ue8m0",
         "expert_offsets_u32", "row_weight_f32", "output", "error_flag_u32", "stream"),
@@ -243,7 +243,7 @@ QWEN_API = _struct("QwenKernelsApi", [("struct_size", U32), ("contract_version",
                                       ("root", C.CFUNCTYPE(Status, C.POINTER(C.c_char_p)))])
 
 SCALE_F32, SCALE_UE8M0 = 1, 2
-OUTPUT_BF16, OUTPUT_F32, OUTPUT_SWIGLU_BF16 = 1, 2, 3
+OUTPUT_BF16, OUTPUT_F32, OUTPUT_SWIGLU_BF16, OUTPUT_SWIGLU_E4M3 = 1, 2, 3, 4
 ACTIVATION_E4M3, ACTIVATION_BF16 = 1, 2
 W4A16_SYMMETRIC, W4A16_ASYMMETRIC = 1, 2
 WORKSPACE_ROUTE_PLAN, WORKSPACE_BF16_GEMM, WORKSPACE_W4A16 = 1, 2, 3

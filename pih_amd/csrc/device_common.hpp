@@ -45,6 +45,29 @@ __device__ __forceinline__ float bf16_round(float v) {
 
 // Nearest finite e4m3fn code with ties to the even code; |v| <= 448 and
 // finite is the caller's contract (every quantizer clamps first).
+// Exponent e of the UE8M0 scale 2^e of a 128-value group with absolute
+// maximum amax (amax >= 1e-4): the smallest e with amax <= 448 * 2^e.
+__device__ __forceinline__ int ue8m0_exponent(float amax) {
+  // start from the exponent of amax/448 and correct by exact comparisons
+  int e = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127 - 8;
+  // 448*2^e is exact for every e reached here (amax in [1e-4, FLT_MAX])
+  while (amax > ldexpf(448.0f, e)) ++e;
+  while (amax <= ldexpf(448.0f, e - 1)) --e;
+  return e;
+}
+
+// e4m3 codes of v[0..3] / scale (clamped to the e4m3 range), rounded to
+// nearest even by the hardware pack (v_cvt_pk_fp8_f32: operand a to the low
+// byte of the selected half-word, b to the high byte); byte i is v[i].
+__device__ __forceinline__ uint32_t e4m3_quant4(const float* v, float scale) {
+  float q[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = fminf(fmaxf(v[i] / scale, -448.0f), 448.0f);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w, true);
+  return (uint32_t)w;
+}
+
 __device__ __forceinline__ uint32_t e4m3_encode(float v) {
   const uint32_t raw = __float_as_uint(v);
   const uint32_t sign = (raw >> 24) & 0x80u;

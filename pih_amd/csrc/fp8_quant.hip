@@ -21,15 +21,6 @@
 namespace pih_amd {
 namespace {
 
-__device__ __forceinline__ int ue8m0_exponent(float amax) {
-  // start from the exponent of amax/448 and correct by exact comparisons
-  int e = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127 - 8;
-  // 448*2^e is exact for every e reached here (amax in [1e-4, FLT_MAX])
-  while (amax > ldexpf(448.0f, e)) ++e;
-  while (amax <= ldexpf(448.0f, e - 1)) --e;
-  return e;
-}
-
 template <int FMT>
 __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restrict__ in,
                                                         const uint32_t* __restrict__ rows,
@@ -82,19 +73,7 @@ __global__ __launch_bounds__(256) void fp8_quant_kernel(const uint16_t* __restri
       scale = amax / 448.0f;
       if (sub == 0) static_cast<float*>(scales)[gi] = scale;
     }
-    // q = v / scale clamped to the e4m3 range, then round-to-nearest-even
-    // to e4m3 by the hardware pack (v_cvt_pk_fp8_f32: operand a to the low
-    // byte of the selected half-word, b to the high byte)
-    float q[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[i] = fminf(fmaxf(v[i] / scale, -448.0f), 448.0f);
-    uint32_t packed[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * h], q[4 * h + 1], 0, false);
-      w = __builtin_amdgcn_cvt_pk_fp8_f32(q[4 * h + 2], q[4 * h + 3], w, true);
-      packed[h] = (uint32_t)w;
-    }
+    const uint32_t packed[2] = {e4m3_quant4(v, scale), e4m3_quant4(v + 4, scale)};
     *reinterpret_cast<uint2*>(codes + (uint64_t)row * k + kg * 128u + sub * 8u) =
         make_uint2(packed[0], packed[1]);
   }

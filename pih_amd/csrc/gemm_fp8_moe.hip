@@ -71,6 +71,7 @@ struct MoeParams {
   const float* row_weight;
   const uint32_t* offsets;
   uint32_t* err;
+  void* out_scale;  // kOutSwiGluFp8: [rows, n / 256] group scales
   uint32_t m, n, k, experts, a_rows_total;
   uint64_t out_row_stride;
   uint32_t n_tiles;
@@ -225,6 +226,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
   const uint32_t wm = __builtin_amdgcn_readfirstlane(wave >> 2), wn = __builtin_amdgcn_readfirstlane(wave & 3);
+  constexpr bool kSwi = OUT == kOutSwiGlu || OUT == kOutSwiGluFp8;  // gate/up pairs in the tile
 
   uint32_t expert, row0, rows, nt;
   if (!moe_tile(p, expert, row0, rows, nt)) return;
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // W tile row R: for SwiGLU, wave block R >> 6 holds 32 gate rows (R & 63
   // below 32) and the 32 matching up rows, so each wave owns gate/up pairs
   auto w_row = [&](uint32_t R) -> uint32_t {
-    if constexpr (OUT == kOutSwiGlu) {
+    if constexpr (kSwi) {
       const uint32_t wv = R >> 6, j = (R & 63) >> 4, rr = R & 15;
       const uint32_t base = nt * 128 + wv * 32 + (j & 1) * 16 + rr;
       return j >= 2 ? p.n / 2 + base : base;
@@ -266,7 +268,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   const uint8_t* w_base = p.w + (uint64_t)expert * p.n * K;
   // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
   uint32_t wblk0, wblk1;
-  if constexpr (OUT == kOutSwiGlu) {
+  if constexpr (kSwi) {
     wblk0 = nt;
     wblk1 = (p.n / 2 + nt * 128) / 128;
   } else {
@@ -351,8 +353,8 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb + rd0), *reinterpret_cast<const v4i*>(pb + (rd0 ^ 64)));
     }
     const v4i sa4 = *reinterpret_cast<const v4i*>(sSa(stage) + wm * 64 + lr * 4);
-    const uint32_t sw0 = sSw(stage)[OUT == kOutSwiGlu ? 0 : (wn >> 1)];
-    const uint32_t sw1 = sSw(stage)[OUT == kOutSwiGlu ? 1 : (wn >> 1)];
+    const uint32_t sw0 = sSw(stage)[kSwi ? 0 : (wn >> 1)];
+    const uint32_t sw1 = sSw(stage)[kSwi ? 1 : (wn >> 1)];
     auto a_frag = [&](int r) -> v8i {
       const uint8_t* pa = sA(stage) + (wm * 64 + r * 16 + lr) * LDS_ROW;
       return cat8(*reinterpret_cast<const v4i*>(pa + rd0), *reinterpret_cast<const v4i*>(pa + (rd0 ^ 64)));
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
         const float c0 = sa * __uint_as_float(sw0), c1 = sa * __uint_as_float(sw1);
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
-          const float c = (OUT == kOutSwiGlu && nb >= 2) ? c1 : c0;
+          const float c = (kSwi && nb >= 2) ? c1 : c0;
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[nb][r][i] = __builtin_fmaf(t[nb][i], c, acc[nb][r][i]);
         }
@@ -407,7 +409,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
           acc[nb][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wf[nb], af, acc[nb][r], 0, 0, 0, (int)((OUT == kOutSwiGlu && nb >= 2) ? sw1 : sw0), 0, sb);
+              wf[nb], af, acc[nb][r], 0, 0, 0, (int)((kSwi && nb >= 2) ? sw1 : sw0), 0, sb);
       };
       // A fragments one block ahead (at most four LDS reads in flight)
       v8i af = a_frag(0);
@@ -468,8 +470,76 @@ done:
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
   // ---- epilogue: lane holds out[row wm*64 + r*16 + lr][4*lg + i] of block nb
+  if constexpr (OUT == kOutSwiGluFp8) {
+    // SwiGLU x route weight rounded to bf16 (the values the bf16 output
+    // holds), then quantised to e4m3 exactly as fp8_quant_kernel would: the
+    // tile's 128 output columns of a row (nt*128 ..) are one 128-group, and
+    // its absolute maximum meets across the 4 waves of a row half in LDS
+    __shared__ float s_amax[BM][4];
+    float vq[4][2][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t rr = wm * 64 + r * 16 + lr;
+      const bool live = rr < rows;
+      const float rwt = live && p.row_weight ? p.row_weight[row0 + rr] : 1.0f;
+      float am = 0.0f;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float gt = bf16_round(acc[h][r][i]);
+          float up = bf16_round(acc[h + 2][r][i]);
+          float v = 0.0f;
+          if (__builtin_isfinite(gt) && __builtin_isfinite(up)) {
+            if (p.limit > 0.0f) {
+              gt = fminf(gt, p.limit);
+              up = fminf(fmaxf(up, -p.limit), p.limit);
+            }
+            v = bf16_round((gt / (1.0f + expf(-gt))) * up * rwt);
+          } else {
+            v = __builtin_nanf("");
+          }
+          if (!__builtin_isfinite(v)) {
+            if (live) bad |= kErrNonFinite;
+            v = 0.0f;
+          }
+          vq[r][h][i] = v;
+          am = fmaxf(am, fabsf(v));
+        }
+      am = fmaxf(am, __shfl_xor(am, 16));
+      am = fmaxf(am, __shfl_xor(am, 32));
+      if (lg == 0) s_amax[rr][wn] = am;
+    }
+    __syncthreads();
+    const uint32_t groups = p.n / 256;  // 128-groups per output row
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t rr = wm * 64 + r * 16 + lr;
+      if (rr >= rows) continue;
+      float amax = fmaxf(fmaxf(s_amax[rr][0], s_amax[rr][1]), fmaxf(s_amax[rr][2], s_amax[rr][3]));
+      amax = fmaxf(amax, 1.0e-4f);
+      float scale;
+      const uint64_t g = (uint64_t)(row0 + rr) * groups + nt;
+      if constexpr (SCALE == kScaleUe8m0) {
+        int e = ue8m0_exponent(amax);
+        if (e < -127 || e > 127) {
+          bad |= kErrScale;
+          e = 0;
+        }
+        scale = ldexpf(1.0f, e);
+        if (wn == 0 && lg == 0) static_cast<uint8_t*>(p.out_scale)[g] = (uint8_t)(e + 127);
+      } else {
+        scale = amax / 448.0f;
+        if (wn == 0 && lg == 0) static_cast<float*>(p.out_scale)[g] = scale;
+      }
+      uint8_t* dst = static_cast<uint8_t*>(p.out) + (uint64_t)(row0 + rr) * p.out_row_stride + nt * 128 + wn * 32 +
+                     4 * lg;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) *reinterpret_cast<uint32_t*>(dst + h * 16) = e4m3_quant4(vq[r][h], scale);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4 && OUT != kOutSwiGluFp8; ++r) {
     const uint32_t rr = wm * 64 + r * 16 + lr;
     if (rr >= rows) continue;
     const uint64_t orow = (uint64_t)(row0 + rr) * p.out_row_stride;
@@ -548,6 +618,8 @@ done:
 template <int SCALE>
 void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out) {
   if (out == kOutSwiGlu) hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutSwiGlu>), dim3(grid), dim3(NTH), 0, s, mp);
+  else if (out == kOutSwiGluFp8)
+    hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutSwiGluFp8>), dim3(grid), dim3(NTH), 0, s, mp);
   else if (out == kOutF32) hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutF32>), dim3(grid), dim3(NTH), 0, s, mp);
   else hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutBf16>), dim3(grid), dim3(NTH), 0, s, mp);
 }
@@ -572,8 +644,10 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
   mp.k = a.k;
   mp.experts = a.problems;
   mp.a_rows_total = a.a_rows_total;
-  mp.out_row_stride = a.out_row_stride ? a.out_row_stride : (a.out_kind == kOutSwiGlu ? a.n / 2 : a.n);
-  mp.n_tiles = a.out_kind == kOutSwiGlu ? a.n / 256 : (a.n + BN - 1) / BN;
+  const bool swiglu = a.out_kind == kOutSwiGlu || a.out_kind == kOutSwiGluFp8;
+  mp.out_scale = a.out_scale;
+  mp.out_row_stride = a.out_row_stride ? a.out_row_stride : (swiglu ? a.n / 2 : a.n);
+  mp.n_tiles = swiglu ? a.n / 256 : (a.n + BN - 1) / BN;
   mp.limit = a.swiglu_limit;
   mp.err_code = a.err_code_bit;
   mp.err_scale = a.err_scale_bit;

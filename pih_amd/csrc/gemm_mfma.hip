@@ -564,9 +564,13 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
     return Invalid("fp8_gemm_null_argument");
   if (a.k == 0 || a.k % 128 || a.n == 0 || a.n % 128 || a.problems == 0 || a.m == 0)
     return Invalid("fp8_gemm_shape_invalid");
-  if (a.out_kind == kOutSwiGlu && (a.n % 256)) return Invalid("fp8_gemm_swiglu_shape_invalid");
+  if ((a.out_kind == kOutSwiGlu || a.out_kind == kOutSwiGluFp8) && (a.n % 256))
+    return Invalid("fp8_gemm_swiglu_shape_invalid");
   if (a.scale_fmt != kScaleF32 && a.scale_fmt != kScaleUe8m0) return Invalid("fp8_gemm_scale_format_invalid");
-  if (a.out_kind != kOutBf16 && a.out_kind != kOutF32 && a.out_kind != kOutSwiGlu)
+  if (a.out_kind != kOutBf16 && a.out_kind != kOutF32 && a.out_kind != kOutSwiGlu && a.out_kind != kOutSwiGluFp8)
+    return Invalid("fp8_gemm_output_type_invalid");
+  // the quantised SwiGLU output exists in the MoE kernel only
+  if (a.out_kind == kOutSwiGluFp8 && (!a.moe || a.check_codes || !a.out_scale))
     return Invalid("fp8_gemm_output_type_invalid");
   if (a.moe && !a.offsets) return Invalid("fp8_gemm_offsets_missing");
   if (a.a_rows_total == 0) return Invalid("fp8_gemm_a_rows_invalid");

@@ -13,7 +13,10 @@
 namespace pih_amd {
 
 enum ScaleFmt : uint32_t { kScaleF32 = 1, kScaleUe8m0 = 2 };
-enum OutKind : uint32_t { kOutBf16 = 1, kOutF32 = 2, kOutSwiGlu = 3 };
+// kOutSwiGluFp8 (MoE FP8 GEMM only): the SwiGLU output rounded to bf16 and
+// quantised to e4m3 with one scale per (row, 128 columns) in the GEMM's
+// scale format, exactly as LaunchFp8Quant would quantise the bf16 output
+enum OutKind : uint32_t { kOutBf16 = 1, kOutF32 = 2, kOutSwiGlu = 3, kOutSwiGluFp8 = 4 };
 enum ActKind : uint32_t { kActE4m3 = 1, kActBf16 = 2 };
 
 // ------------------------------------------------------------- FP8 quant
@@ -46,6 +49,7 @@ struct BlockGemmArgs {
   const uint8_t* w = nullptr;      // e4m3 [problems][n][k]
   const void* w_scale = nullptr;   // [problems][n/128][k/128]
   void* out = nullptr;
+  void* out_scale = nullptr;           // kOutSwiGluFp8: [m, n/256] scales (codes in out)
   const float* row_weight = nullptr;   // SwiGLU epilogue, per logical row
   const uint32_t* offsets = nullptr;   // MoE: [problems+1] on device
   uint32_t* error_flag = nullptr;

@@ -105,7 +105,8 @@ St Fp8Gemm(const pih_amd_fp8_gemm_launch_v1* r) {
 }
 
 St MoeFp8Gemm(const pih_amd_moe_fp8_gemm_launch_v1* r) {
-  if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format) || !OutOk(r->output_type))
+  if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format) ||
+      !(OutOk(r->output_type) || r->output_type == PIH_AMD_OUTPUT_SWIGLU_E4M3_V1))
     return Invalid("moe_fp8_gemm_request_invalid");
   if (r->expert_count == 0 || r->row_capacity == 0 || r->activation_rows == 0)
     return Invalid("moe_fp8_gemm_shape_invalid");
@@ -118,6 +119,7 @@ St MoeFp8Gemm(const pih_amd_moe_fp8_gemm_launch_v1* r) {
   a.offsets = Ptr<const uint32_t>(r->expert_offsets_u32);
   a.row_weight = Ptr<const float>(r->row_weight_f32);
   a.out = Ptr<void>(r->output);
+  a.out_scale = Ptr<void>(r->output_scale);
   a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
   a.stream = AsStream(r->stream);
   a.m = r->row_capacity;

@@ -8,8 +8,10 @@
 // host synchronisation:
 //   route plan -> activation quant -> grouped gate/up GEMM (+ SwiGLU x route
 //   weight) -> intermediate quant -> grouped down GEMM -> ordered combine.
-// The numerics are the stage entries' own (the same kernels run in the same
-// order), so the layer's output equals launching the stages one by one.
+// FP8 weights fold the intermediate quant into the gate/up epilogue (one
+// launch and the bf16 intermediate's write and read fewer); it quantises the
+// bf16-rounded SwiGLU values with the quant entry's arithmetic, so the
+// layer's output still equals launching the stages one by one.
 //
 // Weights: FP8 e4m3 with 128x128 block scales (fp32 or UE8M0), or MXFP4
 // (e2m1 + UE8M0 per 32 k) with e4m3 (UE8M0 per 128) or bf16 activations.
@@ -143,7 +145,11 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
       g.a_gather = gate_up ? row_token : nullptr;
       g.w = static_cast<const uint8_t*>(gate_up ? a.w13 : a.w2);
       g.w_scale = gate_up ? a.w13_scale : a.w2_scale;
-      g.out = gate_up ? (void*)mid : (void*)y;
+      // FP8 experts: the gate/up epilogue writes the e4m3 intermediate and
+      // its group scales itself (kOutSwiGluFp8, the values LaunchFp8Quant
+      // would produce from the bf16 SwiGLU output)
+      g.out = gate_up ? (void*)at(c.mq) : (void*)y;
+      g.out_scale = gate_up ? (void*)at(c.ms) : nullptr;
       g.row_weight = gate_up ? row_weight : nullptr;
       g.offsets = offsets;
       g.error_flag = a.error_flag;
@@ -155,7 +161,7 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
       g.a_rows_total = gate_up ? a.tokens : R;
       g.moe = true;
       g.scale_fmt = a.scale_fmt;
-      g.out_kind = gate_up ? kOutSwiGlu : kOutBf16;
+      g.out_kind = gate_up ? kOutSwiGluFp8 : kOutBf16;
       g.swiglu_limit = a.swiglu_limit;
       return LaunchFp8BlockGemm(g);
     }
@@ -182,7 +188,7 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
     return LaunchFp4Gemm(g);
   };
   if (!(s = gemm(true)).ok()) return s;
-  if (c.quant_mid && !(s = quant(mid, R, a.inter, c.mq, c.ms)).ok()) return s;
+  if (!fp8 && c.quant_mid && !(s = quant(mid, R, a.inter, c.mq, c.ms)).ok()) return s;
   if (!(s = gemm(false)).ok()) return s;
 
   CombineArgs cb;

@@ -99,9 +99,16 @@ def fp8_gemm(a, a_scale, w, w_scale, scale_format: int, output_type: int = abi.O
 def moe_fp8_gemm(a, a_scale, row_token, w, w_scale, offsets, rows: int, scale_format: int,
                  output_type: int, row_weight=None, swiglu_limit: float = 0.0,
                  flag: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None):
+    """Returns (out, flag); OUTPUT_SWIGLU_E4M3 returns ((codes, scales), flag)."""
     experts, n, k = w.shape
-    ncols = n // 2 if output_type == abi.OUTPUT_SWIGLU_BF16 else n
-    if out is None:
+    e4m3 = output_type == abi.OUTPUT_SWIGLU_E4M3
+    ncols = n // 2 if output_type in (abi.OUTPUT_SWIGLU_BF16, abi.OUTPUT_SWIGLU_E4M3) else n
+    scales = None
+    if e4m3:
+        out = torch.empty(rows, ncols, dtype=torch.uint8, device=a.device) if out is None else out
+        sdt = torch.float32 if scale_format == abi.SCALE_F32 else torch.uint8
+        scales = torch.empty(rows, ncols // 128, dtype=sdt, device=a.device)
+    elif out is None:
         out = torch.empty(rows, ncols, dtype=torch.float32 if output_type == abi.OUTPUT_F32 else torch.bfloat16,
                           device=a.device)
     flag = error_flag() if flag is None else flag
@@ -110,9 +117,9 @@ def moe_fp8_gemm(a, a_scale, row_token, w, w_scale, offsets, rows: int, scale_fo
                     expert_offsets_u32=ptr(offsets), row_weight_f32=ptr(row_weight), output=ptr(out),
                     error_flag_u32=ptr(flag), stream=stream_handle(), row_capacity=rows, expert_count=experts,
                     n=n, k=k, activation_rows=a.shape[0], scale_format=scale_format, output_type=output_type,
-                    swiglu_limit=swiglu_limit)
+                    swiglu_limit=swiglu_limit, output_scale=ptr(scales))
     _check(_ln().call("launch_moe_fp8_gemm", r), "moe_fp8_gemm")
-    return out, flag
+    return ((out, scales) if e4m3 else out), flag
 
 
 def moe_mxfp4_gemm(a, a_scale, row_token, w_packed, w_scale, offsets, rows: int, activation_type: int,
@@ -152,8 +159,9 @@ def moe_combine(expert_out, token_rows, shared=None, flag: Optional[torch.Tensor
 class MoeFp8Layer:
     """The BASELINE FP8 MoE expert layer on device, one launch per stage:
     route plan -> FP8 quant of the token rows -> grouped gate/up GEMM with
-    the fused SwiGLU * route-weight epilogue -> FP8 quant of the
-    intermediate -> grouped down GEMM -> ordered combine.
+    the fused SwiGLU * route-weight epilogue that also quantises the
+    intermediate to FP8 (as the quant entry would quantise its bf16 values)
+    -> grouped down GEMM -> ordered combine.
 
     Buffers are allocated once at construction for ``tokens`` x ``topk``
     routes, so ``forward`` allocates nothing and can be timed or replayed.
@@ -179,14 +187,13 @@ class MoeFp8Layer:
         self.token_rows = torch.empty(tokens, topk, dtype=torch.int32, device=dev)
         self.xq = torch.empty(tokens, self.hidden, dtype=torch.uint8, device=dev)
         self.xs = torch.empty(tokens, self.hidden // 128, dtype=sdt, device=dev)
-        self.mid = torch.empty(self.rows, self.inter, dtype=torch.bfloat16, device=dev)
         self.mq = torch.empty(self.rows, self.inter, dtype=torch.uint8, device=dev)
         self.ms = torch.empty(self.rows, self.inter // 128, dtype=sdt, device=dev)
         self.y = torch.empty(self.rows, self.hidden, dtype=torch.bfloat16, device=dev)
         self.out = torch.empty(tokens, self.hidden, dtype=torch.bfloat16, device=dev)
         self.flag = error_flag()
 
-    STAGES = ("route_plan", "quant_x", "gate_up", "quant_mid", "down", "combine")
+    STAGES = ("route_plan", "quant_x", "gate_up", "down", "combine")
 
     def forward(self, x, topk_ids, topk_weights, shared=None, marks=None):
         """``marks``: optional list of len(STAGES)+1 events recorded on the
@@ -213,18 +220,12 @@ class MoeFp8Layer:
         st = L.call("launch_moe_fp8_gemm", abi.request(
             abi.LN["moe_fp8_gemm"], activation_e4m3=ptr(self.xq), activation_scale=ptr(self.xs),
             row_token_u32=ptr(self.row_token), weight_e4m3=ptr(self.w13), weight_scale=ptr(self.w13_scale),
-            expert_offsets_u32=ptr(self.offsets), row_weight_f32=ptr(self.row_weight), output=ptr(self.mid),
-            error_flag_u32=f, stream=s, row_capacity=self.rows, expert_count=self.experts, n=2 * self.inter,
-            k=self.hidden, activation_rows=self.tokens, scale_format=self.fmt,
-            output_type=abi.OUTPUT_SWIGLU_BF16, swiglu_limit=self.limit))
+            expert_offsets_u32=ptr(self.offsets), row_weight_f32=ptr(self.row_weight), output=ptr(self.mq),
+            output_scale=ptr(self.ms), error_flag_u32=f, stream=s, row_capacity=self.rows,
+            expert_count=self.experts, n=2 * self.inter, k=self.hidden, activation_rows=self.tokens,
+            scale_format=self.fmt, output_type=abi.OUTPUT_SWIGLU_E4M3, swiglu_limit=self.limit))
         _check(st, "moe_fp8_gemm(gate/up)")
         mark(3)
-        st = L.call("launch_fp8_quant", abi.request(
-            abi.LN["fp8_quant"], input_bf16=ptr(self.mid), row_index_u32=0, output_e4m3=ptr(self.mq),
-            scale=ptr(self.ms), error_flag_u32=f, stream=s, row_count=self.rows, logical_k=self.inter,
-            input_rows=self.rows, scale_format=self.fmt))
-        _check(st, "fp8_quant(mid)")
-        mark(4)
         st = L.call("launch_moe_fp8_gemm", abi.request(
             abi.LN["moe_fp8_gemm"], activation_e4m3=ptr(self.mq), activation_scale=ptr(self.ms),
             row_token_u32=0, weight_e4m3=ptr(self.w2), weight_scale=ptr(self.w2_scale),
@@ -232,13 +233,13 @@ class MoeFp8Layer:
             stream=s, row_capacity=self.rows, expert_count=self.experts, n=self.hidden, k=self.inter,
             activation_rows=self.rows, scale_format=self.fmt, output_type=abi.OUTPUT_BF16, swiglu_limit=0.0))
         _check(st, "moe_fp8_gemm(down)")
-        mark(5)
+        mark(4)
         st = L.call("launch_moe_combine", abi.request(
             abi.LN["moe_combine"], expert_output_bf16=ptr(self.y), token_rows_u32=ptr(self.token_rows),
             shared_bf16=ptr(shared), output_bf16=ptr(self.out), error_flag_u32=f, stream=s,
             token_count=self.tokens, top_k=self.topk, hidden_size=self.hidden, row_count=self.rows))
         _check(st, "moe_combine")
-        mark(6)
+        mark(5)
         return self.out
 
 

@@ -174,3 +174,30 @@ def test_layer_query_and_request_checks(eng):
     assert L.call("launch_moe_layer", r).code == abi.INVALID_ARGUMENT  # workspace too small
     r.weight_format = 9
     assert L.call("launch_moe_layer", r).code == abi.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("tokens,experts,topk,limit,ue8m0",
+                         [(200, 8, 2, 0.0, False), (300, 16, 4, 10.0, False), (130, 8, 3, 0.0, True)])
+def test_swiglu_e4m3_output_equals_bf16_then_quant(eng, tokens, experts, topk, limit, ue8m0):
+    """The gate/up GEMM's quantising epilogue (OUTPUT_SWIGLU_E4M3) writes the
+    codes and scales the quant entry produces from its bf16 SwiGLU output,
+    bit for bit (routed rows only; rows past offsets[E] are not written)."""
+    from pih_amd import linear
+
+    hidden, inter = 512, 256
+    fmt = abi.SCALE_UE8M0 if ue8m0 else abi.SCALE_F32
+    ids, wts = synth.zipf_router(synth.config_seed(4, 9700 + tokens), tokens, experts, topk)
+    x = synth.bf16_normal(synth.config_seed(4, 9701), (tokens, hidden))
+    w13, s13, _, _ = [to_dev(t) for t in _fp8_weights(experts, hidden, inter, 9800, ue8m0)]
+    off, rt, rw, _ = oracle.route_plan(ids, wts, experts)
+    rows = tokens * topk
+    xq, xs, flag0 = linear.fp8_quant(to_dev(x), fmt)
+    args = (xq, xs, to_dev(rt), w13, s13, to_dev(off), rows, fmt)
+    mid, flag1 = linear.moe_fp8_gemm(*args, abi.OUTPUT_SWIGLU_BF16, row_weight=to_dev(rw), swiglu_limit=limit)
+    q_ref, s_ref, flag2 = linear.fp8_quant(mid, fmt)
+    (q, s), flag3 = linear.moe_fp8_gemm(*args, abi.OUTPUT_SWIGLU_E4M3, row_weight=to_dev(rw), swiglu_limit=limit)
+    _sync()
+    assert [_flag(f) for f in (flag0, flag1, flag2, flag3)] == [0, 0, 0, 0]
+    n = int(off[-1])
+    np.testing.assert_array_equal(to_host(q)[:n], to_host(q_ref)[:n])
+    np.testing.assert_array_equal(to_host(s)[:n], to_host(s_ref)[:n])
