@@ -201,3 +201,23 @@ def test_swiglu_e4m3_output_equals_bf16_then_quant(eng, tokens, experts, topk, l
     n = int(off[-1])
     np.testing.assert_array_equal(to_host(q)[:n], to_host(q_ref)[:n])
     np.testing.assert_array_equal(to_host(s)[:n], to_host(s_ref)[:n])
+
+
+def test_swiglu_e4m3_output_flags_nonfinite(eng):
+    """Weight scales that overflow the gate/up products: both SwiGLU output
+    kinds raise the non-finite bit (4) and nothing else."""
+    from pih_amd import linear
+
+    tokens, experts, topk, hidden, inter = 64, 8, 2, 256, 256
+    fmt = abi.SCALE_F32
+    ids, wts = synth.zipf_router(synth.config_seed(4, 9900), tokens, experts, topk)
+    x = synth.bf16_normal(synth.config_seed(4, 9901), (tokens, hidden))
+    w13, s13, _, _ = _fp8_weights(experts, hidden, inter, 9902, False)
+    s13 = np.full_like(s13, 3.0e38)
+    off, rt, rw, _ = oracle.route_plan(ids, wts, experts)
+    xq, xs, _ = linear.fp8_quant(to_dev(x), fmt)
+    args = (xq, xs, to_dev(rt), to_dev(w13), to_dev(s13), to_dev(off), tokens * topk, fmt)
+    _, f_bf16 = linear.moe_fp8_gemm(*args, abi.OUTPUT_SWIGLU_BF16, row_weight=to_dev(rw))
+    _, f_e4m3 = linear.moe_fp8_gemm(*args, abi.OUTPUT_SWIGLU_E4M3, row_weight=to_dev(rw))
+    _sync()
+    assert _flag(f_bf16) == 4 and _flag(f_e4m3) == 4
