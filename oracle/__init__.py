@@ -338,3 +338,15 @@ def moe_fp8_forward(x_bits, topk_ids, topk_weights, experts, hidden, inter,
         y[b:en] = expert_fp8(xs, row_weight[b:en], hidden, inter, w13[e], w13s[e], w2[e], w2s[e], limit)
     acc = ordered_accumulate(y, row_token, t)
     return finalize(acc), y, (offsets, row_token, row_weight, token_rows)
+
+
+def qwen_mlp(x_bits, wg_bits, wu_bits, wd_bits):
+    """Qwen3 MLP block as the reference computes it:
+    gate and up through the BF16 linear (fp32 strict-k dot, bf16 RNE out,
+    GemmPlan at src/backend/cuda/gemm_plan.cpp:169-198), SiLU-mul with one
+    rounding at its output (plugins/model-qwen3/qwen3_cpu_oracle.cpp:114-126),
+    then the down linear.  Returns the bf16 bits [M, hidden]."""
+    gate = f32_to_bf16_bits(bf16_gemm(x_bits, wg_bits))
+    up = f32_to_bf16_bits(bf16_gemm(x_bits, wu_bits))
+    h = silu_mul(gate, up)
+    return f32_to_bf16_bits(bf16_gemm(h, wd_bits))

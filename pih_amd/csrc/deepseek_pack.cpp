@@ -113,9 +113,11 @@ St GroupedFp8Gemm(const pih_deepseek_grouped_fp8_gemm_launch_v1* r) {
   a.scale_fmt = kScaleUe8m0;
   a.out_kind = kOutBf16;
   // the reference grouped kernel reports scale 0xFF as 1024 and a
-  // non-finite sum as 2048 (deepseek_attention_dense_primitives.cu:205-250)
+  // non-finite sum as 2048, and stores the non-finite bf16 value all the
+  // same (deepseek_attention_dense_primitives.cu:205-250)
   a.err_scale_bit = 1024u;
   a.err_nonfinite_bit = 2048u;
+  a.write_nonfinite = true;
   return LaunchFp8BlockGemm(a);
 }
 

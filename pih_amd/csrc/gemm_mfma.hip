@@ -102,6 +102,7 @@ struct GemmParams {
   uint32_t light_rows;  // MoE: experts with at most this many rows are skipped
   float limit;
   uint32_t err_code, err_scale, err_nonfinite;
+  uint32_t write_nonfinite;  // store a non-finite result as well as flagging it
 };
 
 // Expert lookup for MoE tile g: returns false when g is past the last tile.
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
           const float v = acc[ms][ns][i];
           if (!__builtin_isfinite(v) && p.err_nonfinite) {
             bad |= kErrNonFinite;
-            continue;
+            if (!p.write_nonfinite) continue;
           }
           const uint32_t col = nt * BN + wn * 64 + ns * 16 + lr;
           if constexpr (OUT == kOutF32) {
@@ -593,6 +594,7 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
   gp.err_code = a.err_code_bit;
   gp.err_scale = a.err_scale_bit;
   gp.err_nonfinite = a.err_nonfinite_bit;
+  gp.write_nonfinite = a.write_nonfinite ? 1u : 0u;
   uint32_t grid;
   St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, a.out_row_stride);
   if (!s.ok()) return s;

@@ -70,6 +70,10 @@ struct BlockGemmArgs {
   float swiglu_limit = 0.0f;  // <= 0: plain SiLU-mul
   // error bits for: invalid code / A row, UE8M0 0xFF, non-finite result
   uint32_t err_code_bit = 1u, err_scale_bit = 2u, err_nonfinite_bit = 4u;
+  // a non-finite result is flagged and, when set, also stored (the
+  // reference's grouped FP8 kernel stores it; its dense FP8 and FP4 kernels
+  // skip the element)
+  bool write_nonfinite = false;
 };
 St LaunchFp8BlockGemm(const BlockGemmArgs& a);
 // MoE problems without the code scan (called by LaunchFp8BlockGemm after its

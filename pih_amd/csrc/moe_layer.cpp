@@ -53,7 +53,9 @@ Carve Layout(const MoeLayerArgs& a) {
     take(c.xq, T * H);
     take(c.xs, T * (H / 128) * ssz);
   }
-  take(c.mid, R * I * 2);
+  // FP8 weights: the gate/up epilogue writes the e4m3 intermediate
+  // directly, so only MXFP4 needs the bf16 one
+  if (!fp8) take(c.mid, R * I * 2);
   if (c.quant_mid) {
     take(c.mq, R * I);
     take(c.ms, R * (I / 128) * ssz);
@@ -96,9 +98,9 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
   uint32_t* row_token = reinterpret_cast<uint32_t*>(at(c.row_token));
   float* row_weight = reinterpret_cast<float*>(at(c.row_weight));
   uint32_t* token_rows = reinterpret_cast<uint32_t*>(at(c.token_rows));
-  uint16_t* mid = reinterpret_cast<uint16_t*>(at(c.mid));
-  uint16_t* y = reinterpret_cast<uint16_t*>(at(c.y));
   const bool fp8 = a.weight_format == kWeightFp8;
+  uint16_t* mid = fp8 ? nullptr : reinterpret_cast<uint16_t*>(at(c.mid));
+  uint16_t* y = reinterpret_cast<uint16_t*>(at(c.y));
   const ScaleFmt act_fmt = fp8 ? a.scale_fmt : kScaleUe8m0;
 
   RoutePlanArgs rp;

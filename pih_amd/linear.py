@@ -156,6 +156,55 @@ def moe_combine(expert_out, token_rows, shared=None, flag: Optional[torch.Tensor
     return out, flag
 
 
+def bf16_gemm(a: torch.Tensor, w: torch.Tensor, output_type: int = abi.OUTPUT_BF16,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """C[m, n] = A[m, k] . W[n, k]^T through ``launch_bf16_gemm`` (the
+    GemmPlan::execute replacement, src/backend/cuda/gemm_plan.cpp:169-198):
+    bf16 in, fp32 accumulate, bf16 or fp32 out."""
+    m, k = a.shape
+    n = w.shape[0]
+    if out is None:
+        out = torch.empty(m, n, dtype=torch.bfloat16 if output_type == abi.OUTPUT_BF16 else torch.float32,
+                          device=a.device)
+    r = abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(a), w_bf16=ptr(w), output=ptr(out), workspace=0,
+                    workspace_bytes=0, stream=stream_handle(), m=m, n=n, k=k, output_type=output_type)
+    _check(_ln().call("launch_bf16_gemm", r), "bf16_gemm")
+    return out
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16(silu(g) * u) elementwise (pih_qwen_silu_mul_bf16_v1)."""
+    if out is None:
+        out = torch.empty_like(gate)
+    r = abi.request(abi.LN["silu_mul"], gate_bf16=ptr(gate), up_bf16=ptr(up), output_bf16=ptr(out),
+                    stream=stream_handle(), count=gate.numel())
+    _check(_ln().call("launch_silu_mul", r), "silu_mul")
+    return out
+
+
+class QwenMlpBlock:
+    """The Qwen3 MLP block as the reference's model issues it per layer:
+    gate = x.Wg^T and up = x.Wu^T (GemmPlan, bf16 out;
+    plugins/model-qwen3/qwen3_bf16_execution_schedule.cpp:34-37), then
+    silu_mul (qwen3_cpu_oracle.cpp:114-126 semantics), then down = h.Wd^T.
+    Buffers are allocated at construction, so ``forward`` only enqueues."""
+
+    def __init__(self, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, tokens: int):
+        self.wg, self.wu, self.wd = w_gate, w_up, w_down
+        inter, hidden = w_gate.shape
+        dev = w_gate.device
+        self.gate = torch.empty(tokens, inter, dtype=torch.bfloat16, device=dev)
+        self.up = torch.empty(tokens, inter, dtype=torch.bfloat16, device=dev)
+        self.h = torch.empty(tokens, inter, dtype=torch.bfloat16, device=dev)
+        self.out = torch.empty(tokens, hidden, dtype=torch.bfloat16, device=dev)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        bf16_gemm(x, self.wg, out=self.gate)
+        bf16_gemm(x, self.wu, out=self.up)
+        silu_mul(self.gate, self.up, out=self.h)
+        return bf16_gemm(self.h, self.wd, out=self.out)
+
+
 class MoeFp8Layer:
     """The BASELINE FP8 MoE expert layer on device, one launch per stage:
     route plan -> FP8 quant of the token rows -> grouped gate/up GEMM with

@@ -84,13 +84,15 @@ def test_bf16_gemm_prefill(eng, m, n, k, out_type):
 @pytest.mark.parametrize("m", [1, 8, 64])
 @pytest.mark.parametrize("n,k", [(1024, 4096), (4096, 12288), (256, 1024)])
 def test_bf16_gemv_decode(eng, m, n, k):
-    if m == 64 and k == 12288:
-        pytest.skip("covered by the smaller K at M=64 (oracle time)")
     a = synth.bf16_normal(synth.config_seed(2, 30 + m), (m, k))
     w = synth.bf16_normal(synth.config_seed(2, 40 + n), (n, k), std=0.02)
-    ref = oracle.bf16_gemm(a, w)
-    assert_close(_bf16_gemm(a, w, abi.OUTPUT_BF16), ref, f"bf16 gemv {m}x{n}x{k}")
-    assert_close(_bf16_gemm(a, w, abi.OUTPUT_F32, use_ws=False), ref, f"bf16 gemv no-ws {m}x{n}x{k}")
+    # the largest case (64 x 4096 x 12288) is checked on every 4th output
+    # column plus both ends of each 16-row weight block, to bound oracle time
+    cols = np.arange(n) if m * n * k < 2 ** 31 else np.unique(
+        np.concatenate([np.arange(0, n, 4), np.arange(15, n, 16)]))
+    ref = oracle.bf16_gemm(a, np.ascontiguousarray(w[cols]))
+    assert_close(_bf16_gemm(a, w, abi.OUTPUT_BF16)[:, cols], ref, f"bf16 gemv {m}x{n}x{k}")
+    assert_close(_bf16_gemm(a, w, abi.OUTPUT_F32, use_ws=False)[:, cols], ref, f"bf16 gemv no-ws {m}x{n}x{k}")
 
 
 @pytest.mark.parametrize("m,n,k", [(5, 1024, 4096), (20, 1024, 4096), (40, 256, 1024), (64, 8192, 1024),

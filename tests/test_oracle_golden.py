@@ -355,8 +355,183 @@ def test_routed_expert_reference_kat_and_golden(gold):
     np.testing.assert_array_equal(out, gold["re_out"])
 
 
+# ------------------------------------------ FP8 expert chain (BASELINE cfg4)
+def _e4m3_codes(values):
+    codes = [oracle.e4m3_encode(float(v)) for v in np.ravel(values)]
+    assert all(c is not None for c in codes)
+    return np.array(codes, np.uint8).reshape(np.shape(values))
+
+
+def _kat_expert(route_weight):
+    """H = I = 128.  x = [0.875, 5*2^-9, 0, ...]: one 128-group with amax
+    0.875 = 448 * 2^-9, so the fp32 activation scale is exactly 2^-9 and the
+    codes are 448 and 5 (exact).
+    gate rows c < 64:  w[c,0] = -2.5,  w[c,1] = 1.875  (block scale 1.0)
+    gate rows c >= 64: w[c,0] = 1.75,  w[c,1] = 1.125
+    up rows c < 64:    w[c,0] = 2.75,  w[c,1] = 3.25   (block scale 0.5)
+    up rows c >= 64:   w[c,0] = -6.0,  w[c,1] = 2.75
+    down: w2[h, (h+1) % 128] = 1.0, block scale 2.0 (y[h] = mid[h+1], so a
+    transposed W2 would read mid[h-1] instead)."""
+    h = i = 128
+    x = np.zeros((1, h), np.float32)
+    x[0, 0], x[0, 1] = 0.875, 5 * 2.0 ** -9
+    w13v = np.zeros((2 * i, h), np.float32)
+    w13v[:64, 0], w13v[:64, 1], w13v[64:i, 0], w13v[64:i, 1] = -2.5, 1.875, 1.75, 1.125
+    w13v[i:i + 64, 0], w13v[i:i + 64, 1], w13v[i + 64:, 0], w13v[i + 64:, 1] = 2.75, 3.25, -6.0, 2.75
+    w2v = np.zeros((h, i), np.float32)
+    w2v[np.arange(h), (np.arange(h) + 1) % i] = 1.0
+    s13 = np.array([[1.0], [0.5]], np.float32)  # [2I/128, H/128]: gate block, up block
+    s2 = np.array([[2.0]], np.float32)
+    return (oracle.f32_to_bf16_bits(x), np.array([route_weight], np.float32), h, i,
+            _e4m3_codes(w13v), s13, _e4m3_codes(w2v), s2)
+
+
+def test_expert_fp8_known_answer():
+    """Hand-derived answer of the cfg4 expert chain (po_expert_fp8), every
+    rounding point at least 0.2 bf16 ulp from a tie:
+      gate_lo = (448*-2.5 + 5*1.875) * 2^-9 * 1.0 = -2.169189453125 -> bf16 -2.171875
+      up_lo   = (448*2.75 + 5*3.25) * 2^-9 * 0.5  =  1.218994140625 -> bf16  1.21875
+      gate_hi = (448*1.75 + 5*1.125) * 2^-9       =  1.542236328125 -> bf16  1.5390625
+      up_hi   = (448*-6 + 5*2.75) * 2^-9 * 0.5    = -2.611572265625 -> bf16 -2.609375
+      mid_lo  = silu(-2.171875) * 1.21875 * 0.8 = -0.2222 * 1.21875 * 0.8
+              = -0.216638 -> bf16 -0.216796875
+      mid_hi  = silu(1.5390625) * -2.609375 * 0.8 = 1.267154 * -2.609375 * 0.8
+              = -2.645184 -> bf16 -2.640625
+      quant:  s = 2.640625 / 448; mid_hi -> code -448, mid_lo / s = -36.78
+              -> e4m3 -36
+      down:   y_lo = -36 * s * 2.0 = -0.4243862 -> bf16 -0.423828125
+              y_hi = -448 * s * 2.0 = -5.28125
+    and y[h] reads mid[h+1]: h in 0..62 and 127 -> y_lo, h in 63..126 -> y_hi.
+    The mistakes this pins, each giving another output: gate and up halves
+    swapped; gate/up not rounded to bf16; the route weight applied after the
+    intermediate's bf16 rounding, or after the down GEMM; the intermediate
+    not rounded to bf16 or not quantised; the up block read with the gate
+    block's scale; W2 read transposed."""
+    out = oracle.expert_fp8(*_kat_expert(0.8))
+    lo, hi = oracle.f32_to_bf16_bits(np.array([-0.423828125, -5.28125], np.float32))
+    want = np.full(128, lo, np.uint16)
+    want[63:127] = hi
+    np.testing.assert_array_equal(out[0], want)
+
+
+def test_expert_fp8_route_weight_and_clamp():
+    """Route weight 0.2 in the same derivation: mid_hi = -2.645184 * 0.25 =
+    -0.661296 -> bf16 -0.66015625, mid_lo = -0.0541596 -> bf16
+    -0.05419921875, mid_lo / s = -36.76 -> e4m3 -36 with s = 0.66015625/448,
+    so y_hi = -1.3203125 and y_lo = bf16(-36 * s * 2).  The clamp (limit
+    1.0) caps the gate at 1.0 and the up at +-1.0; a zero route weight gives
+    an all-zero output (amax floor 1e-4, codes 0)."""
+    out = oracle.bf16_bits_to_f32(oracle.expert_fp8(*_kat_expert(0.2)))[0]
+    s = np.float32(0.66015625) / np.float32(448.0)
+    lo = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(np.array([-36 * s * 2], np.float32)))[0]
+    assert out[0] == lo and out[63] == np.float32(-1.3203125)
+    args = list(_kat_expert(0.8))
+    clamped = oracle.bf16_bits_to_f32(oracle.expert_fp8(*args, limit=1.0))[0]
+    # gate_lo -2.171875 (not clamped from below), up_lo 1.21875 -> 1.0;
+    # gate_hi 1.5390625 -> 1.0, up_hi -2.609375 -> -1.0
+    silu = lambda g: np.float32(g) / (np.float32(1) + np.exp(np.float32(-g)))
+    m_lo = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(np.array([silu(-2.171875) * 1.0 * 0.8], np.float32)))[0]
+    m_hi = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(np.array([silu(1.0) * -1.0 * np.float32(0.8)], np.float32)))[0]
+    assert (m_lo, m_hi) == (np.float32(-0.177734375), np.float32(-0.5859375))
+    assert clamped[63] == np.float32(2 * m_hi)
+    assert abs(clamped[0] - 2 * m_lo) <= abs(2 * m_lo) / 16  # e4m3 rounding of the lo lane only
+    args[1] = np.array([0.0], np.float32)
+    assert np.all(oracle.bf16_bits_to_f32(oracle.expert_fp8(*args)) == 0)
+
+
+def test_expert_fp8_float64_brute_force():
+    """A tiny expert with exactly representable inputs (activation groups
+    with amax 448 * 2^k, integer e4m3 weight codes, power-of-two block
+    scales), so both GEMMs are exact in float64 and fp32 alike.  The float64
+    chain (gate/up rows split as [gate; up], SwiGLU, x route weight, the
+    pinned bf16 rounding and fp32-scale quant at the same points) must agree
+    with po_expert_fp8 to one bf16 ulp everywhere, and exactly on >= 95 % of
+    outputs (the fp32 vs float64 SiLU may flip a rounding)."""
+    t, h, i = 3, 256, 256
+    rng = np.random.default_rng(7)
+    ints = np.array([-8, -6, -5, -4, -3, -2, -1, 0, 1, 2, 3, 4, 5, 6, 8], np.float32)
+    x = rng.choice(ints, (t, h)).astype(np.float32)
+    x[:, ::128] = 448.0  # group amax 448 -> activation scale exactly 1
+    w13 = _e4m3_codes(rng.choice(ints, (2 * i, h)))
+    w2 = _e4m3_codes(rng.choice(ints, (h, i)))
+    # gate/up values of order 1 (SiLU well away from its linear range)
+    s13 = np.ldexp(1.0, rng.integers(-11, -8, (2 * i // 128, h // 128))).astype(np.float32)
+    s2 = np.ldexp(1.0, rng.integers(-6, -3, (h // 128, i // 128))).astype(np.float32)
+    rw = np.array([0.7, 0.25, 1.0], np.float32)
+    xb = oracle.f32_to_bf16_bits(x)
+    got = oracle.bf16_bits_to_f32(oracle.expert_fp8(xb, rw, h, i, w13, s13, w2, s2)).astype(np.float64)
+
+    tab = oracle.e4m3_table().astype(np.float64)
+    rnd = lambda v: oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits(np.asarray(v, np.float32))).astype(np.float64)
+    W13 = tab[w13] * np.repeat(np.repeat(s13, 128, 0), 128, 1)
+    W2 = tab[w2] * np.repeat(np.repeat(s2, 128, 0), 128, 1)
+    gu = x.astype(np.float64) @ W13.T  # exact: integer products, power-of-two scales
+    g, u = rnd(gu[:, :i]), rnd(gu[:, i:])
+    mid = rnd(g / (1.0 + np.exp(-g)) * u * rw[:, None].astype(np.float64))
+    mq, ms = oracle.fp8_quant_f32(mid.astype(np.float32))
+    mdq = tab[mq] * np.repeat(ms.astype(np.float64), 128, 1)
+    want = rnd(mdq @ W2.T)
+    ulp = np.abs(got - want) / np.maximum(np.ldexp(1.0, np.floor(np.log2(np.abs(want) + 1e-300)).astype(int) - 7), 1e-300)
+    assert ulp.max() <= 1.0 + 1e-9
+    assert (got == want).mean() >= 0.95
+    # the same float64 chain with the gate/up halves swapped is far outside
+    # that band, so the band tells the split apart
+    g2, u2 = rnd(gu[:, i:]), rnd(gu[:, :i])
+    mid2 = rnd(g2 / (1.0 + np.exp(-g2)) * u2 * rw[:, None].astype(np.float64))
+    q2, s2q = oracle.fp8_quant_f32(mid2.astype(np.float32))
+    other = rnd((tab[q2] * np.repeat(s2q.astype(np.float64), 128, 1)) @ W2.T)
+    assert np.abs(other - got).max() > 0.1 * np.abs(got).max()
+
+
+def test_moe_fp8_forward_known_answer():
+    """Layer level (moe_fp8_forward): one token routed to experts [1, 0]
+    with weights [0.2, 0.8].  Expert 0 is the KAT expert, expert 1 has
+    all-zero weights (its rows are exactly 0).  The output must be the KAT
+    expert's answer at route weight 0.8; pairing the weights with the wrong
+    expert gives the 0.2 answer instead."""
+    xb, _, h, i, w13, s13, w2, s2 = _kat_expert(0.8)
+    W13 = np.stack([w13, np.zeros_like(w13)])
+    S13 = np.stack([s13, s13])
+    W2 = np.stack([w2, np.zeros_like(w2)])
+    S2 = np.stack([s2, s2])
+    out, y, _ = oracle.moe_fp8_forward(xb, np.array([[1, 0]], np.uint32), np.array([[0.2, 0.8]], np.float32),
+                                       2, h, i, W13, S13, W2, S2)
+    np.testing.assert_array_equal(out[0], oracle.expert_fp8(*_kat_expert(0.8))[0])
+    assert not np.array_equal(out[0], oracle.expert_fp8(*_kat_expert(0.2))[0])
+    assert not y[1].any()
+
+
+def test_moe_fp8_forward_matches_token_major_composition():
+    """moe_fp8_forward works expert-major (route plan, per-expert chains over
+    gathered rows, ordered accumulate).  Restated token-major from the pinned
+    per-row chain: each token's routes, experts ascending, fp32 sum of the
+    bf16 expert rows, one bf16 rounding; must agree bit for bit (the chain is
+    row-independent and the accumulate order is experts ascending)."""
+    tokens, experts, topk, hidden, inter = 19, 6, 3, 256, 128
+    ids, wts = synth.zipf_router(synth.config_seed(4, 77), tokens, experts, topk)
+    x = synth.bf16_normal(synth.config_seed(4, 78), (tokens, hidden))
+    w13 = np.empty((experts, 2 * inter, hidden), np.uint8)
+    s13 = np.empty((experts, 2 * inter // 128, hidden // 128), np.float32)
+    w2 = np.empty((experts, hidden, inter), np.uint8)
+    s2 = np.empty((experts, hidden // 128, inter // 128), np.float32)
+    for e in range(experts):
+        w13[e], s13[e] = synth.fp8_block_weight(synth.config_seed(4, 80 + e), 2 * inter, hidden)
+        w2[e], s2[e] = synth.fp8_block_weight(synth.config_seed(4, 90 + e), hidden, inter)
+    got, _, _ = oracle.moe_fp8_forward(x, ids, wts, experts, hidden, inter, w13, s13, w2, s2)
+    want = np.empty_like(got)
+    for t in range(tokens):
+        acc = np.zeros(hidden, np.float32)
+        for j in np.argsort(ids[t], kind="stable"):
+            e = int(ids[t, j])
+            row = oracle.expert_fp8(x[t:t + 1], wts[t, j:j + 1], hidden, inter, w13[e], s13[e], w2[e], s2[e])
+            acc = (acc + oracle.bf16_bits_to_f32(row[0])).astype(np.float32)
+        want[t] = oracle.f32_to_bf16_bits(acc)
+    np.testing.assert_array_equal(got, want)
+
+
 # --------------------------------------------- live reference (optional)
-@pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref not built (needs the reference checkout)")
+@pytest.mark.skipif(not os.path.exists(oracle._REF_PATH),
+                    reason="oracle/_ref not built (needs the reference checkout)")
 def test_against_live_reference_library():
     R = oracle.ref()
     P = oracle.P

@@ -212,3 +212,34 @@ def test_w4a16_grouped_rejects_bad_groups():
     assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
     r.format = 7
     assert ln.call("launch_w4a16_grouped", r).code == abi.INVALID_ARGUMENT
+
+
+def test_moe_layer_workspace_carve():
+    """query_moe_layer_workspace (host only) returns the exact carve: route
+    plan scratch, offsets, row_token / row_weight / token_rows, the quantised
+    tokens and intermediate (+ scales) and the bf16 expert rows, each rounded
+    up to 256 bytes.  FP8 weights write the e4m3 intermediate straight from
+    the gate/up epilogue, so they carry no bf16 intermediate; MXFP4 weights
+    do (their intermediate is re-quantised by its own launch)."""
+    ln = abi.linear_pack()
+    up = lambda b: (b + 255) // 256 * 256
+    T, k, E, H, I = 4096, 8, 256, 7168, 2048
+    R = T * k
+    out = (C.c_uint64 * 1)()
+    ln.call("query_workspace", abi.request(abi.LN["workspace_query"], kind=abi.WORKSPACE_ROUTE_PLAN, m=T, n=k,
+                                           k=E, bytes_u64=C.addressof(out)))
+    plan = up(out[0]) + up((E + 1) * 4) + 3 * up(R * 4)
+
+    def query(fmt, scale_fmt, act):
+        need = (C.c_uint64 * 1)()
+        q = abi.request(abi.LN["moe_layer"], required_bytes_u64=C.addressof(need), token_count=T, top_k=k,
+                        expert_count=E, hidden_size=H, intermediate_size=I, weight_format=fmt,
+                        scale_format=scale_fmt, activation_type=act)
+        assert ln.call("query_moe_layer_workspace", q).code == abi.OK
+        return int(need[0])
+
+    fp8 = plan + up(T * H) + up(T * H // 128 * 4) + up(R * I) + up(R * I // 128 * 4) + up(R * H * 2)
+    assert query(abi.WEIGHT_FP8, abi.SCALE_F32, 0) == fp8
+    mx_e4m3 = plan + up(T * H) + up(T * H // 128) + up(R * I * 2) + up(R * I) + up(R * I // 128) + up(R * H * 2)
+    assert query(abi.WEIGHT_MXFP4, 0, abi.ACTIVATION_E4M3) == mx_e4m3
+    assert query(abi.WEIGHT_MXFP4, 0, abi.ACTIVATION_BF16) == plan + up(R * I * 2) + up(R * H * 2)
