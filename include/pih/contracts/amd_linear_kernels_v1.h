@@ -308,7 +308,23 @@ typedef struct pih_amd_linear_kernels_api_v1 {
   pih_status_v1 (*launch_w4a16_grouped)(const pih_amd_w4a16_grouped_launch_v1*);
   pih_status_v1 (*query_moe_layer_workspace)(const pih_amd_moe_layer_launch_v1*);
   pih_status_v1 (*launch_moe_layer)(const pih_amd_moe_layer_launch_v1*);
+  /* launch_route_plan_noalloc: no counterpart in the reference.  For callers
+   * that cannot allocate device memory (code under HIP graph capture, tight
+   * serving loops): launch_route_plan with its scratch (per-chunk expert
+   * masks and bases) in a device array the pack owns, one per GPU, instead
+   * of a caller workspace.  `workspace` and `workspace_bytes` must be 0.
+   * Limit: the scratch launch_route_plan would need,
+   * query_workspace(ROUTE_PLAN, tokens, top_k, experts), must not exceed
+   * PIH_AMD_ROUTE_PLAN_NOALLOC_MAX_SCRATCH_V1 bytes (for example T <= 16384
+   * tokens at E = 256, or T <= 4096 at E = 1024); larger plans are
+   * INVALID_ARGUMENT.  Every call on one GPU uses that GPU's one array, so
+   * calls that overlap on one GPU (other streams, other threads) race; the
+   * kernels rewrite all of it on every call, so no state carries over.
+   * Outputs equal launch_route_plan's bit for bit. */
+  pih_status_v1 (*launch_route_plan_noalloc)(const pih_amd_route_plan_launch_v1*);
 } pih_amd_linear_kernels_api_v1;
+
+#define PIH_AMD_ROUTE_PLAN_NOALLOC_MAX_SCRATCH_V1 (1ULL << 20)
 
 #ifdef __cplusplus
 }

@@ -233,7 +233,7 @@ LN_ORDER = [("query_workspace", "workspace_query"), ("launch_route_plan", "route
             ("launch_w4a16_gemm", "w4a16"), ("launch_silu_mul", "silu_mul"), ("launch_swiglu", "swiglu"),
             ("launch_mxfp4_decode", "mxfp4_decode"), ("launch_w4a16_dequant", "w4a16_dequant"),
             ("launch_w4a16_grouped", "w4a16_grouped"), ("query_moe_layer_workspace", "moe_layer"),
-            ("launch_moe_layer", "moe_layer")]
+            ("launch_moe_layer", "moe_layer"), ("launch_route_plan_noalloc", "route_plan")]
 LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_version", U32),
                                          ("identity", C.POINTER(Identity))] +
                  [(f, C.CFUNCTYPE(Status, C.POINTER(LN[s]))) for f, s in LN_ORDER])

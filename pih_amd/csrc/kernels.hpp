@@ -166,6 +166,12 @@ struct RoutePlanArgs {
 };
 St LaunchRoutePlan(const RoutePlanArgs& a);
 uint64_t RoutePlanWorkspaceBytes(uint32_t tokens, uint32_t topk, uint32_t experts);
+// LaunchRoutePlan with the pack's own per-device scratch array instead of a
+// caller workspace (a.workspace and a.workspace_bytes must be 0); plans
+// needing more than kRoutePlanNoAllocScratchBytes are rejected.  Calls that
+// overlap on one device share the array and race.
+constexpr uint64_t kRoutePlanNoAllocScratchBytes = 1ull << 20;
+St LaunchRoutePlanNoAlloc(const RoutePlanArgs& a);
 
 struct GatherArgs {
   const uint16_t* source = nullptr;   // bf16 [tokens, hidden]

@@ -66,6 +66,27 @@ St RoutePlan(const pih_amd_route_plan_launch_v1* r) {
   return LaunchRoutePlan(a);
 }
 
+St RoutePlanNoAlloc(const pih_amd_route_plan_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("route_plan_request_invalid");
+  static_assert(PIH_AMD_ROUTE_PLAN_NOALLOC_MAX_SCRATCH_V1 == kRoutePlanNoAllocScratchBytes,
+                "contract limit and scratch array size differ");
+  RoutePlanArgs a;
+  a.topk_ids = Ptr<const uint32_t>(r->topk_ids_u32);
+  a.topk_weights = Ptr<const float>(r->topk_weights_f32);
+  a.expert_offsets = Ptr<uint32_t>(r->expert_offsets_u32);
+  a.row_token = Ptr<uint32_t>(r->row_token_u32);
+  a.row_weight = Ptr<float>(r->row_weight_f32);
+  a.token_rows = Ptr<uint32_t>(r->token_rows_u32);
+  a.workspace = Ptr<void>(r->workspace);
+  a.workspace_bytes = r->workspace_bytes;
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.tokens = r->token_count;
+  a.topk = r->top_k;
+  a.experts = r->expert_count;
+  return LaunchRoutePlanNoAlloc(a);
+}
+
 St Fp8Quant(const pih_amd_fp8_quant_launch_v1* r) {
   if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format)) return Invalid("fp8_quant_request_invalid");
   Fp8QuantArgs a;
@@ -354,11 +375,13 @@ PIH_AMD_CONTAINED(CW4a16Dequant, W4a16Dequant, pih_amd_w4a16_dequant_launch_v1)
 PIH_AMD_CONTAINED(CW4a16Grouped, W4a16Grouped, pih_amd_w4a16_grouped_launch_v1)
 PIH_AMD_CONTAINED(CQueryMoeLayer, QueryMoeLayer, pih_amd_moe_layer_launch_v1)
 PIH_AMD_CONTAINED(CMoeLayer, MoeLayer, pih_amd_moe_layer_launch_v1)
+PIH_AMD_CONTAINED(CRoutePlanNoAlloc, RoutePlanNoAlloc, pih_amd_route_plan_launch_v1)
 
 const pih_amd_linear_kernels_api_v1 kContract = {
     sizeof(pih_amd_linear_kernels_api_v1), kAbi, &kIdentity, &CQueryWorkspace, &CRoutePlan,
     &CFp8Quant, &CFp8Gemm, &CMoeFp8Gemm, &CMoeMxfp4Gemm, &CMoeCombine, &CBf16Gemm, &CW4a16,
-    &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant, &CW4a16Grouped, &CQueryMoeLayer, &CMoeLayer};
+    &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant, &CW4a16Grouped, &CQueryMoeLayer, &CMoeLayer,
+    &CRoutePlanNoAlloc};
 
 pih_status_v1 BindOrigin(const char* path) noexcept {
   return ToAbi(path && path[0] == '/' ? Ok() : Invalid("bind_origin_path_not_absolute"));

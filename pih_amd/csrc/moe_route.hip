@@ -17,8 +17,18 @@
 // Error bits: 1 expert id out of range, 2 expert repeated within a token,
 // 4 route weight non-finite or negative.  An invalid route gets no row
 // (token_rows = 0xffffffff) and is left out of the offsets.
+#include <mutex>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
+
+// Scratch of the no-allocation route plan (LaunchRoutePlanNoAlloc): the
+// per-chunk expert masks and bases, kRoutePlanNoAllocScratchBytes at most.
+// Every device the library runs on holds its own copy until the process
+// ends.  Host code never passes this name to a kernel (on the host it is a
+// stand-in, not a device address); it uses the address hipGetSymbolAddress
+// returns for the current device.
+static __device__ __align__(256) unsigned char scratch[pih_amd::kRoutePlanNoAllocScratchBytes];
 
 namespace pih_amd {
 namespace {
@@ -301,6 +311,46 @@ St LaunchRoutePlan(const RoutePlanArgs& a) {
                      a.topk_weights, masks, bases, a.expert_offsets, a.row_token, a.row_weight,
                      a.token_rows, a.tokens, a.topk, a.experts);
   return AfterLaunch("route_plan_launch_failed");
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipErrorNotInitialized;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+// The scratch array's address on the current device, looked up once per
+// device (with that device current) and kept.
+St NoAllocScratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return Internal("route_plan_noalloc_device_unavailable");
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&slot] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
+  if (slot.err != hipSuccess || slot.ptr == nullptr) return Internal("route_plan_noalloc_scratch_unavailable");
+  *out = slot.ptr;
+  return Ok();
+}
+
+}  // namespace
+
+St LaunchRoutePlanNoAlloc(const RoutePlanArgs& args) {
+  if (args.workspace || args.workspace_bytes) return Invalid("route_plan_noalloc_workspace_must_be_zero");
+  if (args.tokens == 0 || args.topk == 0 || args.topk > kMaxTopk || args.experts == 0 ||
+      args.experts > kMaxExperts || (uint64_t)args.tokens * args.topk > 0x7fffffffull)
+    return Invalid("route_plan_shape_invalid");
+  if (RoutePlanWorkspaceBytes(args.tokens, args.topk, args.experts) > kRoutePlanNoAllocScratchBytes)
+    return Invalid("route_plan_noalloc_plan_exceeds_scratch");
+  RoutePlanArgs a = args;
+  St s = NoAllocScratch(&a.workspace);
+  if (!s.ok()) return s;
+  a.workspace_bytes = kRoutePlanNoAllocScratchBytes;
+  return LaunchRoutePlan(a);
 }
 
 St LaunchRouteGather(const GatherArgs& a) {
