@@ -49,7 +49,16 @@
  *                          and K in one launch (the Qwen decode step's
  *                          q/k/v and gate/up projections each read the
  *                          same input; the reference issues one launch per
- *                          projection, qwen3_int4_gemm_plan.cpp:55-85).
+ *                          projection, qwen3_int4_gemm_plan.cpp:55-85);
+ *   launch_route_plan_noalloc
+ *                          launch_route_plan with the pack's own scratch
+ *                          (no reference counterpart; for callers that
+ *                          cannot allocate);
+ *   launch_router_topk     the host DeepSeekLearnedRouter::Route
+ *                          (plugins/model-deepseek-v4-flash/
+ *                          deepseek_learned_router.cpp:21-94) on the device,
+ *                          plus BASELINE's softmax top-k, so router scores
+ *                          never travel to the host.
  *
  * Conventions are those of the reference's pack tables: one request pointer
  * in, pih_status_v1 by value out; a NULL request, wrong struct_size or wrong
@@ -288,6 +297,30 @@ typedef struct pih_amd_mxfp4_decode_launch_v1 {
   uint32_t rows, k;
 } pih_amd_mxfp4_decode_launch_v1;
 
+/* Router top-k on the device (the step between the router GEMM and the
+ * route plan): raw scores f32 [T, E] -> topk_ids u32 [T, top_k] and
+ * topk_weights f32 [T, top_k] in rank order, ranked by (selection
+ * descending, expert id ascending).
+ * SQRT_SOFTPLUS: the V4 learned router (plugins/model-deepseek-v4-flash/
+ *   deepseek_learned_router.cpp:21-81; E = 256, top-6, scale 1.5 there):
+ *   base = sqrt(softplus(raw)), selection = base + bias[e] (bias_f32 [E],
+ *   0 = none), weight = base / sum of the top-k bases * route_scale.
+ * SOFTMAX: softmax over the E scores, top-k, renormalised to sum
+ *   route_scale (BASELINE's DeepSeek-V3-style router; selection by score,
+ *   which orders like the probability).
+ * E <= 1024, top_k <= min(32, E), route_scale finite and > 0.  Error bits:
+ * 1 non-finite score, 2 non-finite bias, 4 top-k weight sum non-finite or
+ * <= 0 (the reference rejects all three). */
+#define PIH_AMD_ROUTER_SOFTMAX_V1 1U
+#define PIH_AMD_ROUTER_SQRT_SOFTPLUS_V1 2U
+typedef struct pih_amd_router_topk_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t scores_f32, bias_f32, topk_ids_u32, topk_weights_f32;
+  uintptr_t error_flag_u32, stream;
+  uint32_t token_count, expert_count, top_k, mode;
+  float route_scale;
+} pih_amd_router_topk_launch_v1;
+
 typedef struct pih_amd_linear_kernels_api_v1 {
   uint32_t struct_size;
   uint32_t contract_version;
@@ -322,6 +355,10 @@ typedef struct pih_amd_linear_kernels_api_v1 {
    * kernels rewrite all of it on every call, so no state carries over.
    * Outputs equal launch_route_plan's bit for bit. */
   pih_status_v1 (*launch_route_plan_noalloc)(const pih_amd_route_plan_launch_v1*);
+  /* Router top-k (pih_amd_router_topk_launch_v1 above); replaces the host
+   * DeepSeekLearnedRouter::Route (deepseek_learned_router.cpp:84-94) and the
+   * scores D2H before it. */
+  pih_status_v1 (*launch_router_topk)(const pih_amd_router_topk_launch_v1*);
 } pih_amd_linear_kernels_api_v1;
 
 #define PIH_AMD_ROUTE_PLAN_NOALLOC_MAX_SCRATCH_V1 (1ULL << 20)

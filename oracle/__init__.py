@@ -67,6 +67,7 @@ def lib() -> C.CDLL:
             "po_finalize": (C.c_int, [P, P, C.c_size_t, P]),
             "po_routed_expert_fp4": (C.c_int, [P, P, U32, U32, U32, P, P, P, P, P, P, P]),
             "po_expert_fp8": (C.c_int, [P, P, U32, U32, U32, P, P, P, P, F32, P]),
+            "po_router_topk": (C.c_int, [P, P, U32, U32, U32, U32, F32, P, P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -97,6 +98,7 @@ def ref() -> Optional[C.CDLL]:
             "pr_accumulate": (C.c_int, [P, U32, P, P, U32, P, P]),
             "pr_routed_expert": (C.c_int, [P, P, U32, U32, U32, P, P, P, P, P, P, P]),
             "pr_int4_quantize": (C.c_int, [P, U64, U64, P, P]),
+            "pr_learned_router": (C.c_int, [P, U32, P, P, P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(R, name)
@@ -350,3 +352,18 @@ def qwen_mlp(x_bits, wg_bits, wu_bits, wd_bits):
     up = f32_to_bf16_bits(bf16_gemm(x_bits, wu_bits))
     h = silu_mul(gate, up)
     return f32_to_bf16_bits(bf16_gemm(h, wd_bits))
+
+
+ROUTER_SOFTMAX, ROUTER_SQRT_SOFTPLUS = 1, 2
+
+
+def router_topk(scores, topk: int, mode: int, scale: float = 1.0, bias=None):
+    """po_router_topk: (ids u32 [T, k], weights f32 [T, k]) in rank order."""
+    s = np.ascontiguousarray(scores, np.float32)
+    t, e = s.shape
+    ids = np.empty((t, topk), np.uint32)
+    w = np.empty((t, topk), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    _check("po_router_topk", lib().po_router_topk(
+        _ptr(s), None if b is None else _ptr(b), t, e, topk, mode, float(scale), _ptr(ids), _ptr(w)))
+    return ids, w

@@ -444,6 +444,99 @@ int po_swiglu(const float* gate, const float* up, size_t count, float limit,
   return 0;
 }
 
+/* ------------------------------------------------------------ router top-k */
+typedef struct {
+  uint32_t expert;
+  float base, selection;
+} po_ranked;
+
+/* (selection descending, expert ascending): the order of the reference's
+ * partial_sort comparator (deepseek_learned_router.cpp:57-64). */
+static int ranked_before(const po_ranked* a, const po_ranked* b) {
+  if (a->selection != b->selection) return a->selection > b->selection;
+  return a->expert < b->expert;
+}
+
+static float stable_softplus(float v) {
+  /* deepseek_learned_router.cpp:10-13 */
+  return v > 0.0f ? v + log1pf(expf(-v)) : log1pf(expf(v));
+}
+
+int po_router_topk(const float* scores, const float* bias, uint32_t tokens,
+                   uint32_t experts, uint32_t topk, uint32_t mode, float scale,
+                   uint32_t* ids, float* weights) {
+  if (tokens == 0 || experts == 0 || topk == 0 || topk > experts || topk > 32 ||
+      (mode != 1 && mode != 2))
+    return 1;
+  if (mode == 2 && bias)
+    for (uint32_t e = 0; e < experts; ++e)
+      if (!isfinite(bias[e])) return 3;
+  for (size_t i = 0; i < (size_t)tokens * experts; ++i)
+    if (!isfinite(scores[i])) return 2;
+  int bad = 0;
+  PO_PARALLEL_FOR
+  for (uint32_t t = 0; t < tokens; ++t) {
+    const float* s = scores + (size_t)t * experts;
+    po_ranked best[32];
+    uint32_t count = 0;
+    float mx = -INFINITY;
+    for (uint32_t e = 0; e < experts; ++e) mx = s[e] > mx ? s[e] : mx;
+    for (uint32_t e = 0; e < experts; ++e) {
+      po_ranked r;
+      r.expert = e;
+      if (mode == 2) {
+        /* deepseek_learned_router.cpp:44-52: base = sqrt(softplus(raw)),
+         * selection = base + bias */
+        r.base = sqrtf(stable_softplus(s[e]));
+        r.selection = r.base + (bias ? bias[e] : 0.0f);
+      } else {
+        /* softmax is strictly increasing in the score, so the top-k of the
+         * probabilities is the top-k of the scores */
+        r.base = s[e];
+        r.selection = s[e];
+      }
+      /* insertion into the sorted best-k list */
+      uint32_t at = count;
+      while (at > 0 && ranked_before(&r, &best[at - 1])) --at;
+      if (at >= topk) continue;
+      const uint32_t last = count < topk ? count++ : topk - 1;
+      for (uint32_t j = last; j > at; --j) best[j] = best[j - 1];
+      best[at] = r;
+    }
+    uint32_t* oid = ids + (size_t)t * topk;
+    float* ow = weights + (size_t)t * topk;
+    if (mode == 2) {
+      /* deepseek_learned_router.cpp:65-81: weights base / sum(base) * 1.5 */
+      float den = 0.0f;
+      for (uint32_t j = 0; j < topk; ++j) den += best[j].base;
+      if (!isfinite(den) || den <= 0.0f) {
+#pragma omp atomic write
+        bad = 4;
+        continue;
+      }
+      for (uint32_t j = 0; j < topk; ++j) {
+        oid[j] = best[j].expert;
+        ow[j] = best[j].base / den * scale;
+      }
+    } else {
+      /* BASELINE: p = softmax over all experts (exp of score - max, summed
+       * in expert order), then the selected p renormalised to sum 1 */
+      float sum = 0.0f;
+      for (uint32_t e = 0; e < experts; ++e) sum += expf(s[e] - mx);
+      float psel = 0.0f, p[32];
+      for (uint32_t j = 0; j < topk; ++j) {
+        p[j] = expf(best[j].base - mx) / sum;
+        psel += p[j];
+      }
+      for (uint32_t j = 0; j < topk; ++j) {
+        oid[j] = best[j].expert;
+        ow[j] = p[j] / psel * scale;
+      }
+    }
+  }
+  return bad;
+}
+
 /* -------------------------------------------------------- MoE route plan */
 typedef struct {
   uint32_t expert, token, ordinal;

@@ -138,6 +138,25 @@ void po_silu_mul(const uint16_t* gate, const uint16_t* up, size_t count,
 int po_swiglu(const float* gate, const float* up, size_t count, float limit,
               float* out);
 
+/* ------------------------------------------------------------ router top-k */
+/* Router selection over raw scores [tokens, experts] (one token's scores
+ * contiguous), top_k <= 32, ranked by (selection descending, expert id
+ * ascending); ids/weights [tokens, top_k] in rank order.
+ * mode 2 (V4 learned router, plugins/model-deepseek-v4-flash/
+ *   deepseek_learned_router.cpp:10-81, generalised from E=256, k=6):
+ *   base = sqrt(softplus(raw)) with the stable softplus, selection = base +
+ *   bias[e] (bias NULL: 0), weight = base / sum(base over the top-k, rank
+ *   order) * scale (the reference's 1.5).
+ * mode 1 (BASELINE softmax top-k, no reference counterpart): selection =
+ *   raw (softmax is strictly increasing); p = exp(raw - max) / sum over all
+ *   experts (expert order), weight = p / sum(p over the top-k, rank order)
+ *   * scale.
+ * Codes: 1 geometry/mode, 2 non-finite score, 3 non-finite bias, 4 top-k
+ * weight sum non-finite or <= 0 (mode 2). */
+int po_router_topk(const float* scores, const float* bias, uint32_t tokens,
+                   uint32_t experts, uint32_t topk, uint32_t mode, float scale,
+                   uint32_t* ids, float* weights);
+
 /* -------------------------------------------------------- MoE route plan */
 /* plugins/model-deepseek-v4-flash/deepseek_expert_subwave_plan.cpp:32-101,
  * generalised to any top-k and expert count: validates, sorts routes by

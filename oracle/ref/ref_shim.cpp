@@ -5,6 +5,7 @@
 // restatement in oracle/pih_oracle.c; never loaded by product code.
 //
 // Return convention: 0 OK, 1 the reference returned a non-OK status.
+#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
@@ -19,6 +20,7 @@
 #include "pih/model/deepseek_fp4_gemm_oracle.h"
 #include "pih/model/deepseek_fp8_activation_codec.h"
 #include "pih/model/deepseek_fp8_gemm_oracle.h"
+#include "pih/model/deepseek_learned_router.h"
 #include "pih/model/deepseek_mxfp4_codec.h"
 #include "pih/model/deepseek_routed_expert_oracle.h"
 #include "pih/model/qwen3_cpu_oracle.h"
@@ -202,6 +204,23 @@ int pr_int4_quantize(const uint16_t* src, uint64_t rows, uint64_t cols,
   if (!q.ok()) return 1;
   std::memcpy(packed, q->packed_values().data(), q->packed_values().size());
   std::memcpy(scales, q->scale_bits().data(), q->scale_bits().size() * 2U);
+  return 0;
+}
+
+// The V4 learned router (256 experts, top-6, x1.5): raw scores [tokens, 256]
+// and bias [256] -> expert ids and weights [tokens, 6] by (token, ordinal).
+int pr_learned_router(const float* raw, uint32_t token_count, const float* bias,
+                      uint32_t* ids, float* weights) {
+  std::vector<float> scores(raw, raw + static_cast<std::size_t>(token_count) * 256U);
+  std::array<float, 256> b{};
+  for (std::size_t e = 0; e < 256; ++e) b[e] = bias[e];
+  auto plan = DeepSeekLearnedRouter::Route(token_count, scores, b);
+  if (!plan.ok()) return 1;
+  for (const auto& r : plan->routes()) {
+    const std::size_t at = static_cast<std::size_t>(r.token_index) * 6U + r.route_ordinal;
+    ids[at] = r.expert_id;
+    weights[at] = r.weight;
+  }
   return 0;
 }
 

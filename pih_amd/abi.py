@@ -205,6 +205,10 @@ LN["bf16_gemm"] = _struct("Bf16Gemm", _hdr(*_u("a_bf16", "w_bf16", "output", "wo
 LN["w4a16"] = _struct("W4a16", _hdr(*_u("input_bf16", "qweight", "scales", "zeros", "output_bf16", "workspace"),
                                     ("workspace_bytes", U64), *_u("error_flag_u32", "stream"),
                                     *_i("m", "n", "k", "format")))
+LN["router_topk"] = _struct("RouterTopk", _hdr(*_u("scores_f32", "bias_f32", "topk_ids_u32", "topk_weights_f32",
+                                                    "error_flag_u32", "stream"),
+                                                *_i("token_count", "expert_count", "top_k", "mode"),
+                                                ("route_scale", C.c_float)))
 LN["silu_mul"] = _struct("SiluMul", _hdr(*_u("gate_bf16", "up_bf16", "output_bf16", "stream"), ("count", U64)))
 LN["swiglu"] = _struct("SwiGlu", _hdr(*_u("gate_bf16", "up_bf16", "route_weights_f32", "output_bf16",
                                           "error_flag_u32", "stream"), *_i("rows", "cols"), ("limit", F32)))
@@ -233,7 +237,8 @@ LN_ORDER = [("query_workspace", "workspace_query"), ("launch_route_plan", "route
             ("launch_w4a16_gemm", "w4a16"), ("launch_silu_mul", "silu_mul"), ("launch_swiglu", "swiglu"),
             ("launch_mxfp4_decode", "mxfp4_decode"), ("launch_w4a16_dequant", "w4a16_dequant"),
             ("launch_w4a16_grouped", "w4a16_grouped"), ("query_moe_layer_workspace", "moe_layer"),
-            ("launch_moe_layer", "moe_layer"), ("launch_route_plan_noalloc", "route_plan")]
+            ("launch_moe_layer", "moe_layer"), ("launch_route_plan_noalloc", "route_plan"),
+            ("launch_router_topk", "router_topk")]
 LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_version", U32),
                                          ("identity", C.POINTER(Identity))] +
                  [(f, C.CFUNCTYPE(Status, C.POINTER(LN[s]))) for f, s in LN_ORDER])
@@ -247,6 +252,7 @@ OUTPUT_BF16, OUTPUT_F32, OUTPUT_SWIGLU_BF16, OUTPUT_SWIGLU_E4M3 = 1, 2, 3, 4
 ACTIVATION_E4M3, ACTIVATION_BF16 = 1, 2
 W4A16_SYMMETRIC, W4A16_ASYMMETRIC = 1, 2
 WORKSPACE_ROUTE_PLAN, WORKSPACE_BF16_GEMM, WORKSPACE_W4A16 = 1, 2, 3
+ROUTER_SOFTMAX, ROUTER_SQRT_SOFTPLUS = 1, 2
 
 
 class PackError(RuntimeError):

@@ -150,6 +150,24 @@ uint64_t W4a16WorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
 // exact dequant (q - z) * s (or q * s) to fp32 [n, k]
 St LaunchW4a16Dequant(const W4a16Args& a, float* out);
 
+// ---------------------------------------------------------- router top-k
+// Raw router scores [tokens, experts] -> ids u32 / weights f32 [tokens,
+// topk] in rank order (router.hip).  Error bits: 1 non-finite score,
+// 2 non-finite bias, 4 top-k weight sum invalid.
+enum RouterMode : uint32_t { kRouterSoftmax = 1, kRouterSqrtSoftplus = 2 };
+struct RouterTopkArgs {
+  const float* scores = nullptr;  // [tokens, experts]
+  const float* bias = nullptr;    // [experts], sqrt-softplus selection only (nullptr: 0)
+  uint32_t* ids = nullptr;        // [tokens, topk]
+  float* weights = nullptr;       // [tokens, topk]
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t tokens = 0, experts = 0, topk = 0;
+  uint32_t mode = kRouterSoftmax;
+  float scale = 1.0f;
+};
+St LaunchRouterTopk(const RouterTopkArgs& a);
+
 // --------------------------------------------------------------- MoE glue
 struct RoutePlanArgs {
   const uint32_t* topk_ids = nullptr;     // [tokens, topk]

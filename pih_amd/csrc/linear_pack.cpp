@@ -87,6 +87,23 @@ St RoutePlanNoAlloc(const pih_amd_route_plan_launch_v1* r) {
   return LaunchRoutePlanNoAlloc(a);
 }
 
+St RouterTopk(const pih_amd_router_topk_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("router_topk_request_invalid");
+  RouterTopkArgs a;
+  a.scores = Ptr<const float>(r->scores_f32);
+  a.bias = Ptr<const float>(r->bias_f32);
+  a.ids = Ptr<uint32_t>(r->topk_ids_u32);
+  a.weights = Ptr<float>(r->topk_weights_f32);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.tokens = r->token_count;
+  a.experts = r->expert_count;
+  a.topk = r->top_k;
+  a.mode = r->mode;
+  a.scale = r->route_scale;
+  return LaunchRouterTopk(a);
+}
+
 St Fp8Quant(const pih_amd_fp8_quant_launch_v1* r) {
   if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format)) return Invalid("fp8_quant_request_invalid");
   Fp8QuantArgs a;
@@ -376,12 +393,13 @@ PIH_AMD_CONTAINED(CW4a16Grouped, W4a16Grouped, pih_amd_w4a16_grouped_launch_v1)
 PIH_AMD_CONTAINED(CQueryMoeLayer, QueryMoeLayer, pih_amd_moe_layer_launch_v1)
 PIH_AMD_CONTAINED(CMoeLayer, MoeLayer, pih_amd_moe_layer_launch_v1)
 PIH_AMD_CONTAINED(CRoutePlanNoAlloc, RoutePlanNoAlloc, pih_amd_route_plan_launch_v1)
+PIH_AMD_CONTAINED(CRouterTopk, RouterTopk, pih_amd_router_topk_launch_v1)
 
 const pih_amd_linear_kernels_api_v1 kContract = {
     sizeof(pih_amd_linear_kernels_api_v1), kAbi, &kIdentity, &CQueryWorkspace, &CRoutePlan,
     &CFp8Quant, &CFp8Gemm, &CMoeFp8Gemm, &CMoeMxfp4Gemm, &CMoeCombine, &CBf16Gemm, &CW4a16,
     &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant, &CW4a16Grouped, &CQueryMoeLayer, &CMoeLayer,
-    &CRoutePlanNoAlloc};
+    &CRoutePlanNoAlloc, &CRouterTopk};
 
 pih_status_v1 BindOrigin(const char* path) noexcept {
   return ToAbi(path && path[0] == '/' ? Ok() : Invalid("bind_origin_path_not_absolute"));

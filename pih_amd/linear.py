@@ -65,6 +65,26 @@ def route_plan(topk_ids: torch.Tensor, topk_weights: torch.Tensor, experts: int,
     return offsets, row_token, row_weight, token_rows, flag
 
 
+def router_topk(scores: torch.Tensor, topk: int, mode: int, route_scale: float = 1.0,
+                bias: Optional[torch.Tensor] = None, flag: Optional[torch.Tensor] = None,
+                out: Optional[Tuple[torch.Tensor, torch.Tensor]] = None):
+    """Raw router scores f32 [T, E] -> (topk_ids int32 [T, k], topk_weights
+    f32 [T, k], flag) on the device (``launch_router_topk``): softmax top-k
+    renormalised (abi.ROUTER_SOFTMAX) or the V4 learned router's
+    sqrt-softplus + bias selection (abi.ROUTER_SQRT_SOFTPLUS)."""
+    tokens, experts = scores.shape
+    if out is None:
+        out = (torch.empty(tokens, topk, dtype=torch.int32, device=scores.device),
+               torch.empty(tokens, topk, dtype=torch.float32, device=scores.device))
+    ids, wts = out
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["router_topk"], scores_f32=ptr(scores), bias_f32=ptr(bias), topk_ids_u32=ptr(ids),
+                    topk_weights_f32=ptr(wts), error_flag_u32=ptr(flag), stream=stream_handle(),
+                    token_count=tokens, expert_count=experts, top_k=topk, mode=mode, route_scale=route_scale)
+    _check(_ln().call("launch_router_topk", r), "router_topk")
+    return ids, wts, flag
+
+
 # ------------------------------------------------------------- FP8 quant
 def fp8_quant(x: torch.Tensor, scale_format: int, rows: Optional[torch.Tensor] = None,
               flag: Optional[torch.Tensor] = None):

@@ -129,6 +129,17 @@ def main():
     assert R.pr_accumulate(_p(offs), 256, _p(rows_t), _p(eo), tokens, _p(shared), _p(res)) == 0
     out.update(acc_rows=oracle.f32_to_bf16_bits(eo), acc_shared=oracle.f32_to_bf16_bits(shared), acc_out=res)
 
+    # V4 learned router (sqrt-softplus + bias, top-6, x1.5): random scores,
+    # a zero-bias token block, and integer scores with exact ties
+    rt = 96
+    raw = (synth.normal(31, rt * 256) * 3).astype(np.float32).reshape(rt, 256)
+    raw[32:64] = np.round(raw[32:64])
+    bias = (synth.normal(32, 256) * 0.5).astype(np.float32)
+    rid = np.empty((rt, 6), np.uint32)
+    rw = np.empty((rt, 6), np.float32)
+    assert R.pr_learned_router(_p(raw), rt, _p(bias), _p(rid), _p(rw)) == 0
+    out.update(router_raw=raw, router_bias=bias, router_ids=rid, router_weights=rw)
+
     path = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")

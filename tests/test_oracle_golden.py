@@ -355,6 +355,86 @@ def test_routed_expert_reference_kat_and_golden(gold):
     np.testing.assert_array_equal(out, gold["re_out"])
 
 
+# ----------------------------------------------------------- router top-k
+def _v4_route(raw, bias=None):
+    return oracle.router_topk(np.asarray(raw, np.float32).reshape(-1, 256), 6, oracle.ROUTER_SQRT_SOFTPLUS, 1.5,
+                              np.zeros(256, np.float32) if bias is None else bias)
+
+
+def test_router_sqrt_softplus_reference_kats():
+    # deepseek_learned_router_test.cpp:26-40: top-6 of raw = expert id, sum 1.5
+    raw = np.full(256, -10.0, np.float32)
+    raw[:8] = np.arange(8)
+    ids, w = _v4_route(raw)
+    assert list(ids[0]) == [7, 6, 5, 4, 3, 2]
+    assert abs(float(w.sum()) - 1.5) <= 1e-6
+    # :42-55: a bias of 100 promotes expert 9 to rank 0 with a smaller weight
+    raw = np.full(256, -20.0, np.float32)
+    raw[:6] = 2.0
+    raw[9] = -2.0
+    bias = np.zeros(256, np.float32)
+    bias[9] = 100.0
+    ids, w = _v4_route(raw, bias)
+    assert ids[0, 0] == 9 and w[0, 0] < w[0, 1]
+    # :57-66: exact ties prefer the smaller id
+    ids, _ = _v4_route(np.zeros(256, np.float32))
+    assert list(ids[0]) == [0, 1, 2, 3, 4, 5]
+    # :68-86: ungrouped selection across the legacy 32-expert groups
+    raw = np.full(256, -20.0, np.float32)
+    for o, e in enumerate((0, 32, 64, 96, 128, 160)):
+        raw[e] = 16.0 - o
+    ids, _ = _v4_route(raw)
+    assert list(ids[0]) == [0, 32, 64, 96, 128, 160]
+    # :88-99: tokens routed independently
+    raw = np.full(512, -10.0, np.float32)
+    for e in range(6):
+        raw[e] = raw[256 + 100 + e] = 10.0 - e
+    ids, _ = _v4_route(raw)
+    assert ids[0, 0] == 0 and ids[1, 0] == 100
+    # :101-109: non-finite scores or bias are rejected
+    raw = np.zeros(256, np.float32)
+    raw[17] = np.nan
+    with pytest.raises(oracle.OracleError):
+        _v4_route(raw)
+    bias = np.zeros(256, np.float32)
+    bias[3] = np.inf
+    with pytest.raises(oracle.OracleError):
+        _v4_route(np.zeros(256, np.float32), bias)
+
+
+def test_router_sqrt_softplus_golden(gold):
+    ids, w = _v4_route(gold["router_raw"], gold["router_bias"])
+    np.testing.assert_array_equal(ids, gold["router_ids"])
+    np.testing.assert_array_equal(w.view(np.uint32), gold["router_weights"].view(np.uint32))
+
+
+def test_router_softmax_closed_form():
+    """BASELINE softmax top-k (no reference counterpart): the ids are the
+    top-k of the float64 softmax probabilities (stable order, ties to the
+    smaller id) and the weights their renormalised values to fp32 rounding;
+    a token whose logits tie keeps the smaller ids."""
+    t, e, k = 200, 256, 8
+    ids64, w64 = synth.zipf_router(synth.config_seed(4, 91), t, e, k)
+    logits = (synth.normal(synth.config_seed(4, 91), t * e).reshape(t, e))
+    rank = np.empty(e, np.int64)
+    rank[np.argsort(synth.splitmix64(synth.config_seed(4, 91) ^ 0xA11CE, e), kind="stable")] = np.arange(e)
+    z = (logits - 1.1 * np.log1p(rank)[None, :]).astype(np.float32)
+    z[7] = 0.5  # an all-tie token
+    ids, w = oracle.router_topk(z, k, oracle.ROUTER_SOFTMAX, 1.0)
+    p = np.exp(z.astype(np.float64) - z.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    want = np.argsort(-p, axis=1, kind="stable")[:, :k]
+    np.testing.assert_array_equal(ids, want)
+    sel = np.take_along_axis(p, want, axis=1)
+    np.testing.assert_allclose(w, sel / sel.sum(axis=1, keepdims=True), rtol=2e-6, atol=0)
+    assert list(ids[7]) == list(range(k))
+    # away from the all-tie row, the float32 logits route like the synthetic
+    # float64 router they were rounded from
+    keep = np.ones(t, bool)
+    keep[7] = False
+    assert (ids[keep] == ids64[keep]).mean() > 0.99
+
+
 # ------------------------------------------ FP8 expert chain (BASELINE cfg4)
 def _e4m3_codes(values):
     codes = [oracle.e4m3_encode(float(v)) for v in np.ravel(values)]
@@ -555,3 +635,13 @@ def test_against_live_reference_library():
     assert R.pr_fp4_gemm(q1.ctypes.data_as(P), s1.ctypes.data_as(P), p.ctypes.data_as(P), ps.ctypes.data_as(P),
                          16, 128, 1024, o2.ctypes.data_as(P)) == 0
     np.testing.assert_array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    raw = (synth.normal(84, 300 * 256) * 4).astype(np.float32).reshape(300, 256)
+    raw[100:150] = np.round(raw[100:150] * 2) / 2  # exact ties
+    bias = (synth.normal(85, 256) * 0.3).astype(np.float32)
+    ids1, w1 = _v4_route(raw, bias)
+    ids2 = np.empty_like(ids1)
+    w2 = np.empty_like(w1)
+    assert R.pr_learned_router(raw.ctypes.data_as(P), 300, bias.ctypes.data_as(P), ids2.ctypes.data_as(P),
+                               w2.ctypes.data_as(P)) == 0
+    np.testing.assert_array_equal(ids1, ids2)
+    np.testing.assert_array_equal(w1.view(np.uint32), w2.view(np.uint32))
