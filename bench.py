@@ -78,34 +78,120 @@ def build_inputs(torch):
     return ids, wts, x, t(ids.view(np.int32)), t(wts), t(x.view(np.int16)).view(torch.bfloat16), w13, s13, w2, s2
 
 
-def cpu_baseline(ids, wts, x_bits, budget_s: float = 12.0):
-    """Time po_expert_fp8 (the reference's per-expert CPU chain, restated) on
-    a bounded sample: routed rows of the hottest expert, grown until the
-    sample takes about ``budget_s``.  Returns the CPU TFLOP/s."""
+def cpu_threads_available() -> int:
+    """Threads the CPU baseline may use: the cores this job is allowed to
+    run on, at most 16 (a one-GPU box's CPU share), or PIH_CPU_THREADS."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        allowed = os.cpu_count() or 1
+    return int(os.environ.get("PIH_CPU_THREADS", min(16, allowed)))
+
+
+def _grow(run, start: int, limit: int, budget_s: float):
+    """Doubles the sample size from ``start`` until one run takes about
+    ``budget_s`` / 2 or the sample reaches ``limit``; returns (size, s)."""
+    size = max(1, min(start, limit))
+    while True:
+        t0 = time.perf_counter()
+        run(size)
+        elapsed = time.perf_counter() - t0
+        if elapsed * 2 > budget_s or size * 2 > limit:
+            return size, elapsed
+        size *= 2
+
+
+def cpu_baselines(ids, wts, x_bits):
+    """The reference's CPU arithmetic (the C restatement oracle/pih_oracle.c,
+    built -O2 without fast-math) timed on this host, single-threaded and on
+    every thread the job may use (OpenMP over output elements; per-element
+    arithmetic and results are identical for any thread count).  Each line
+    times the same work its GPU counterpart measures, in that line's unit:
+      cfg4  po_expert_fp8 (quant, gate/up, SiLU-mul x w, requant, down) on
+            routed rows of the hottest expert, TFLOP/s (the headline's unit);
+      cfg1  the Qwen3-0.6B MLP block in full, GB/s of its weights;
+      cfg2  the seven Qwen3-8B BF16 projections at M = 1 in full, GB/s;
+      cfg3  the seven W4A16 projections at M = 1 in full, GB/s;
+      cfg5  the MXFP4 routed-expert chain (e4m3 activations) on the rows of
+            one expert of the 64-token decode batch, GB/s of its weights."""
     import oracle
     from pih_amd import synth
 
-    threads = int(os.environ.get("PIH_CPU_THREADS", min(16, os.cpu_count() or 1)))
-    oracle.set_threads(threads)
-    offsets, row_token, row_weight, _ = oracle.route_plan(ids, wts, E)
-    counts = np.diff(offsets.astype(np.int64))
+    t_all = cpu_threads_available()
+    lines = {}
+
+    def line(name, unit, work, run, start, limit, budget, what):
+        out = {}
+        for label, th in (("threads_1", 1), ("threads_all", t_all)):
+            oracle.set_threads(th)
+            size, sec = _grow(run, start if th == 1 else start * th, limit, budget)
+            out[label] = {"value": round(work(size) / sec, 4), "unit": unit, "threads": th,
+                          "seconds": round(sec, 3), "sample": what(size)}
+        lines[name] = out
+
+    # cfg4: the headline's expert chain
+    offsets = np.concatenate([[0], np.cumsum(np.bincount(ids.ravel(), minlength=E))])
+    order = np.lexsort((np.tile(np.arange(TOPK), T), np.repeat(np.arange(T), TOPK), ids.ravel()))
+    row_token = np.repeat(np.arange(T), TOPK)[order]
+    row_weight = wts.ravel()[order].astype(np.float32)
+    counts = np.diff(offsets)
     e = int(np.argmax(counts))
     b = int(offsets[e])
     w13, s13 = synth.fp8_block_weight(synth.config_seed(4, 20 + e), 2 * I, H)
     w2, s2 = synth.fp8_block_weight(synth.config_seed(4, 600 + e), H, I)
-    flop_per_row = 2.0 * (2 * I * H + H * I)
-    rows, elapsed = threads, 0.0
-    while True:
-        xs = np.ascontiguousarray(x_bits[row_token[b:b + rows]])
-        t0 = time.perf_counter()
-        oracle.expert_fp8(xs, row_weight[b:b + rows], H, I, w13, s13, w2, s2)
-        elapsed = time.perf_counter() - t0
-        if elapsed * 2 > budget_s or rows * 2 > int(counts[e]):
-            break
-        rows *= 2
-    return {"value": flop_per_row * rows / elapsed / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"po_expert_fp8 on {rows} routed rows of expert {e} (gate/up+SiLU-mul+down, fp32 scales), "
-                      f"{elapsed:.2f} s"}
+    flop_row = 2.0 * (2 * I * H + H * I)
+    line("cfg4_fp8_expert", "TFLOP/s", lambda r: flop_row * r / 1e12,
+         lambda r: oracle.expert_fp8(np.ascontiguousarray(x_bits[row_token[b:b + r]]), row_weight[b:b + r], H, I,
+                                     w13, s13, w2, s2), 2, int(counts[e]), 5.0,
+         lambda r: f"po_expert_fp8 on {r} routed rows of expert {e} (fp32 scales)")
+    # cfg1: Qwen3-0.6B MLP block, x [16, 1024]
+    xq = synth.bf16_normal(synth.config_seed(1, 0), (16, 1024))
+    wg = synth.bf16_normal(synth.config_seed(1, 1), (3072, 1024), std=0.02)
+    wu = synth.bf16_normal(synth.config_seed(1, 2), (3072, 1024), std=0.02)
+    wd = synth.bf16_normal(synth.config_seed(1, 3), (1024, 3072), std=0.02)
+    mlp_bytes = 3 * 3072 * 1024 * 2
+    line("cfg1_qwen_mlp_m16", "GB/s", lambda r: mlp_bytes * r / 1e9,
+         lambda r: [oracle.qwen_mlp(xq, wg, wu, wd) for _ in range(r)], 1, 64, 2.0,
+         lambda r: f"{r} x the full MLP block (x [16,1024], gate/up [3072,1024], down [1024,3072])")
+    # cfg2 / cfg3: the seven Qwen3-8B projections at M = 1
+    xs = {k: synth.bf16_normal(synth.config_seed(2, 500 + k), (1, k)) for k in (4096, 12288)}
+    # weight values do not change the CPU's time; draw them fast: bf16 bits
+    # with magnitudes below 2^-5 and random signs; INT4 codes, zeros and
+    # scales in their valid ranges
+    rng = np.random.default_rng(synth.config_seed(2, 510))
+    bw = [((rng.integers(0, 1 << 16, (n, k), dtype=np.uint16) & np.uint16(0x3CFF)) | np.uint16(0x8000)
+           * rng.integers(0, 2, (n, k), dtype=np.uint16)).astype(np.uint16) for _, n, k in QWEN8B]
+    b_bytes = sum(n * k * 2 for _, n, k in QWEN8B)
+    line("cfg2_bf16_decode_m1", "GB/s", lambda r: b_bytes * r / 1e9,
+         lambda r: [[oracle.bf16_gemm(xs[k], w) for (_, _, k), w in zip(QWEN8B, bw)] for _ in range(r)], 1, 16, 2.0,
+         lambda r: f"{r} x the 7 projections (bf16 weights, M = 1)")
+    del bw
+    iw = [(rng.integers(0, 1 << 32, (n, k // 8), dtype=np.uint32),
+           oracle.f32_to_bf16_bits(rng.uniform(0.001, 0.02, (n, k // 128)).astype(np.float32)),
+           rng.integers(0, 1 << 32, (n, (k // 128 + 7) // 8), dtype=np.uint32)) for _, n, k in QWEN8B]
+    i_bytes = sum(n * k // 2 + (n * k // 128) * 2 + n * ((k // 128 + 7) // 8) * 4 for _, n, k in QWEN8B)
+    line("cfg3_w4a16_decode_m1", "GB/s", lambda r: i_bytes * r / 1e9,
+         lambda r: [[oracle.w4a16_asym(xs[k], *w) for (_, _, k), w in zip(QWEN8B, iw)] for _ in range(r)], 1, 16,
+         3.0, lambda r: f"{r} x the 7 projections (asymmetric INT4, M = 1)")
+    del iw
+    # cfg5: one expert of the 64-token MXFP4 decode batch
+    ids5, wts5 = synth.zipf_router(synth.config_seed(5, 64), 64, E, TOPK)
+    e5 = int(np.argmax(np.bincount(ids5.ravel(), minlength=E)))
+    tok5 = np.nonzero((ids5 == e5).any(axis=1))[0]
+    rw5 = wts5[ids5 == e5].astype(np.float32)
+    x5 = synth.bf16_normal(synth.config_seed(5, 65), (64, H))
+    w1p, w1s = synth.mxfp4_weight(synth.config_seed(5, 700), I, H)
+    w3p, w3s = synth.mxfp4_weight(synth.config_seed(5, 701), I, H)
+    w2p, w2s = synth.mxfp4_weight(synth.config_seed(5, 702), H, I)
+    mx_bytes = 3 * I * H // 2 + 3 * I * H // 32
+    line("cfg5_mxfp4_expert_t64", "GB/s", lambda r: mx_bytes / 1e9,
+         lambda r: oracle.routed_expert_fp4(np.ascontiguousarray(x5[tok5[:r]]), rw5[:r], H, I, w1p, w1s, w2p, w2s,
+                                            w3p, w3s), len(tok5), len(tok5), 4.0,
+         lambda r: f"po_routed_expert_fp4 on all {r} rows of expert {e5} (one pass over its weights)")
+    head = lines["cfg4_fp8_expert"]["threads_all"]
+    return {"value": head["value"], "unit": "TFLOP/s", "cores": head["threads"], "kind": "port",
+            "sample": head["sample"] + f", {head['seconds']} s", "host_nproc": os.cpu_count(),
+            "threads_available": t_all, "lines": lines}
 
 
 QWEN8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
@@ -127,19 +213,22 @@ def _timed(torch, fn, iters: int):
 
 
 def _graphed(torch, make_calls, nsets: int, iters: int):
-    """Mean ms per pass with each weight set's pass captured once in a HIP
-    graph (torch.cuda.CUDAGraph) and replayed; the launches inside are the
-    same C-ABI calls, captured on the graph's stream."""
+    """Mean ms per pass with the passes over all ``nsets`` weight sets
+    captured back to back in one HIP graph (torch.cuda.CUDAGraph), as a
+    captured decode loop would hold them, and the graph replayed; the
+    launches inside are the same C-ABI calls, captured on the graph's stream.
+    (A graph per pass pays one graph launch per pass; replaying such
+    per-pass graphs measured slower than the eager launches.)"""
     from pih_amd.device import stream_handle
 
-    graphs = []
-    for j in range(nsets):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            keep = make_calls(j, stream_handle())
-        graphs.append((g, keep))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        keep = [make_calls(j, stream_handle()) for j in range(nsets)]
     torch.cuda.synchronize()
-    return _timed(torch, lambda i: graphs[i % nsets][0].replay(), iters)
+    reps = max(2, iters // nsets)
+    ms = _timed(torch, lambda i: g.replay(), reps)
+    del keep
+    return ms / nsets
 
 
 def _decode_line(ms: float, ms_graph: float, algo: int, nsets: int, launches: int = 7) -> dict:
@@ -329,6 +418,195 @@ def bench_mxfp4(torch, iters: int):
     return out
 
 
+def _rotation(torch, gen, per_bytes: int, min_total: int = 600_000_000):
+    """One uint8 buffer of random bytes holding enough weight sets of
+    ``per_bytes`` (each 256-byte aligned) that cycling through them exceeds
+    the 256 MB Infinity Cache; returns (buffer, set stride, set count)."""
+    stride = (per_bytes + 255) // 256 * 256
+    nsets = max(2, -(-min_total // stride))
+    buf = torch.randint(0, 256, (nsets * stride,), dtype=torch.uint8, device="cuda", generator=gen)
+    return buf, stride, nsets
+
+
+def _line(ms: float, algo: int, flop: float, peak_tflops: float) -> dict:
+    gbs = algo / (ms * 1e-3) / 1e9
+    tf = flop / (ms * 1e-3) / 1e12
+    bound = "hbm" if algo / (HBM_PEAK_GBS * 1e9) >= flop / (peak_tflops * 1e12) else "mfma"
+    return {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "tflops": round(tf, 2), "frac_mfma": round(tf / peak_tflops, 4), "bound": bound,
+            "algorithmic_bytes": int(algo)}
+
+
+def bench_dropin(torch, iters: int):
+    """The entries an unchanged reference model calls, one launch each, at
+    the reference's call shapes, weights rotated through > 512 MB:
+      DeepSeek table  launch_fp4_gemm per routed expert (V4 Flash W1/W3
+                      4096 -> 2048, W2 2048 -> 4096) at 8 and 128 rows;
+                      launch_fp8_gemm at the model's dense call shapes at
+                      M = 4 (decode) and 2048 (prefill);
+                      launch_grouped_fp8_gemm at G = 8, 1024, 4096 (wo_a);
+      Qwen model      pih_qwen_w4a16_gemm_compat_v1 launched by name from the
+                      code object with the model plan's geometry at the
+                      Qwen3-0.6B shapes, M = 1; the BF16 MLP block of
+                      configs[0] (x [16, 1024]);
+      router          launch_router_topk (softmax top-8 of 256) and
+                      launch_route_plan at 4096 tokens."""
+    from pih_amd import abi
+    from pih_amd.device import ptr, stream_handle
+    from pih_amd.linear import QwenMlpBlock, route_plan, route_plan_workspace, router_topk
+    from pih_amd.qwen import QwenCodeObject
+
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x50494806)
+    D = abi.deepseek_pack()
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {}
+
+    def codes(shape):  # e4m3 codes without the two NaN codes
+        c = torch.randint(0, 0x7E, shape, dtype=torch.uint8, device=dev, generator=gen)
+        return c | (torch.randint(0, 2, shape, dtype=torch.uint8, device=dev, generator=gen) << 7)
+
+    def scales(shape, lo, hi):
+        return torch.randint(lo, hi, shape, dtype=torch.uint8, device=dev, generator=gen)
+
+    # ---- launch_fp4_gemm per expert
+    for n, k in ((2048, 4096), (4096, 2048)):
+        wb, ws = n * k // 2, n * k // 32
+        buf, stride, nsets = _rotation(torch, gen, wb + ws)
+        buf.view(nsets, stride)[:, wb:wb + ws] = scales((nsets, ws), 118, 125)
+        for m in (8, 128):
+            a, sa = codes((m, k)), scales((m, k // 128), 118, 125)
+            o = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            reqs = [abi.request(abi.DS["fp4_gemm"], activation_e4m3=ptr(a), activation_scale_bits=ptr(sa),
+                                packed_weight=ptr(buf) + j * stride, weight_scale_bits=ptr(buf) + j * stride + wb,
+                                output_bf16=ptr(o), error_flag=ptr(flag), stream=stream_handle(), m=m, n=n, k=k)
+                    for j in range(nsets)]
+            ms = _timed(torch, lambda i: D.call("launch_fp4_gemm", reqs[i % nsets]), iters)
+            out[f"ds_fp4_gemm_m{m}_{k}to{n}"] = _line(ms, wb + ws + m * k + m * k // 128 + m * n * 2,
+                                                     2.0 * m * n * k, FP8_PEAK_TFLOPS)
+        del buf
+    # ---- launch_fp8_gemm (UE8M0) at the dense call shapes (K -> N)
+    for k, n in ((4096, 1024), (1024, 32768), (8192, 4096), (4096, 2048), (2048, 4096)):
+        wb, ws = n * k, (n // 128) * (k // 128)
+        buf, stride, nsets = _rotation(torch, gen, wb + ws)
+        buf.view(nsets, stride)[:, wb:wb + ws] = scales((nsets, ws), 112, 118)
+        buf.view(nsets, stride)[:, :wb] = codes((nsets, wb))
+        for m in (4, 2048):
+            a, sa = codes((m, k)), scales((m, k // 128), 118, 124)
+            o = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            reqs = [abi.request(abi.DS["fp8_gemm"], activation_e4m3=ptr(a), activation_scale_bits=ptr(sa),
+                                weight_e4m3=ptr(buf) + j * stride, weight_scale_bits=ptr(buf) + j * stride + wb,
+                                output=ptr(o), error_flag=ptr(flag), stream=stream_handle(), m=m, n=n, k=k,
+                                output_type=1) for j in range(nsets)]
+            ms = _timed(torch, lambda i: D.call("launch_fp8_gemm", reqs[i % nsets]), iters)
+            out[f"ds_fp8_gemm_m{m}_{k}to{n}"] = _line(ms, wb + ws + m * k + m * (k // 128) + m * n * 2,
+                                                     2.0 * m * n * k, FP8_PEAK_TFLOPS)
+        del buf
+    # ---- launch_grouped_fp8_gemm, G = 8, N_g = 1024, K_g = 4096
+    g, ng, kg = 8, 1024, 4096
+    wb, ws = g * ng * kg, g * (ng // 128) * (kg // 128)
+    buf, stride, nsets = _rotation(torch, gen, wb + ws)
+    buf.view(nsets, stride)[:, wb:wb + ws] = scales((nsets, ws), 112, 118)
+    buf.view(nsets, stride)[:, :wb] = codes((nsets, wb))
+    for t in (4, 2048):
+        x = (torch.randn(t * g, kg, device=dev, generator=gen)).to(torch.bfloat16)
+        aq = torch.empty(t * g, kg, dtype=torch.uint8, device=dev)
+        asb = torch.empty(t * g, kg // 128, dtype=torch.uint8, device=dev)
+        o = torch.empty(t, g * ng, dtype=torch.bfloat16, device=dev)
+        reqs = [abi.request(abi.DS["grouped_fp8_gemm"], input_bf16=ptr(x), activation_e4m3=ptr(aq),
+                            activation_scale_bits=ptr(asb), weight_e4m3=ptr(buf) + j * stride,
+                            weight_scale_bits=ptr(buf) + j * stride + wb, output_bf16=ptr(o),
+                            error_flag_u32=ptr(flag), stream=stream_handle(), token_count=t, group_count=g,
+                            output_per_group=ng, input_per_group=kg) for j in range(nsets)]
+        ms = _timed(torch, lambda i: D.call("launch_grouped_fp8_gemm", reqs[i % nsets]), iters)
+        out[f"ds_grouped_fp8_t{t}_8x1024x4096"] = _line(ms, wb + ws + t * g * kg * 2 + t * g * ng * 2,
+                                                       2.0 * t * g * ng * kg, FP8_PEAK_TFLOPS)
+    del buf
+    # ---- Qwen code object, W4A16 compat kernel by name, Qwen3-0.6B shapes
+    co = QwenCodeObject()
+    for n, k in ((2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072)):
+        wb, ws = n * k // 2, (n * k // 128) * 2
+        buf, stride, nsets = _rotation(torch, gen, wb + ws)
+        buf.view(nsets, stride)[:, :wb] &= 0x77  # nibbles in [0, 7]: no reserved 8
+        buf.view(nsets, stride)[:, wb:wb + ws] = torch.tensor([0x00, 0x20], dtype=torch.uint8,  # fp16 0.0078125
+                                                              device=dev).repeat(nsets * ws // 2).view(nsets, ws)
+        x = torch.randn(1, k, device=dev, generator=gen).to(torch.bfloat16)
+        o = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
+        s = stream_handle()
+        ms = _timed(torch, lambda i: co.w4a16_gemm(ptr(x), ptr(buf) + (i % nsets) * stride,
+                                                   ptr(buf) + (i % nsets) * stride + wb, ptr(o), ptr(flag), 1, n,
+                                                   k, s), iters)
+        out[f"qwen_compat_w4a16_m1_{k}to{n}"] = _line(ms, wb + ws + k * 2 + n * 2, 2.0 * n * k, 2516.6)
+        del buf
+    # ---- configs[0] MLP block (BF16 GemmPlan x3 + SiLU-mul), M = 16
+    per = 3 * 3072 * 1024 * 2
+    nsets = max(2, -(-600_000_000 // per))
+    wv = (torch.randn(nsets, per // 2, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    blocks = [QwenMlpBlock(wv[j, :3072 * 1024].view(3072, 1024), wv[j, 3072 * 1024:2 * 3072 * 1024].view(3072, 1024),
+                           wv[j, 2 * 3072 * 1024:].view(1024, 3072), 16) for j in range(nsets)]
+    x = torch.randn(16, 1024, device=dev, generator=gen).to(torch.bfloat16)
+    ms = _timed(torch, lambda i: blocks[i % nsets].forward(x), iters)
+    out["cfg1_qwen_mlp_m16"] = dict(_line(ms, per + 16 * 1024 * 2 * 2, 2.0 * 16 * 3 * 3072 * 1024, 2516.6),
+                                    launches=4)
+    del blocks, wv
+    # ---- router top-k and route plan, 4096 tokens x 256 experts
+    sc = torch.randn(T, E, device=dev, generator=gen)
+    ids, wts, _ = router_topk(sc, TOPK, abi.ROUTER_SOFTMAX, flag=flag)
+    ms = _timed(torch, lambda i: router_topk(sc, TOPK, abi.ROUTER_SOFTMAX, flag=flag, out=(ids, wts)), iters)
+    out["router_topk_softmax_t4096_e256_k8"] = {"us": round(ms * 1e3, 2)}
+    o_off, o_rt, o_rw, o_tr, _ = route_plan(ids, wts, E, flag=flag)
+    ws = torch.empty(route_plan_workspace(T, TOPK, E), dtype=torch.uint8, device=dev)
+    rp = abi.request(abi.LN["route_plan"], topk_ids_u32=ptr(ids), topk_weights_f32=ptr(wts),
+                     expert_offsets_u32=ptr(o_off), row_token_u32=ptr(o_rt), row_weight_f32=ptr(o_rw),
+                     token_rows_u32=ptr(o_tr), workspace=ptr(ws), workspace_bytes=ws.numel(),
+                     error_flag_u32=ptr(flag), stream=stream_handle(), token_count=T, top_k=TOPK, expert_count=E)
+    L = abi.linear_pack()
+    ms = _timed(torch, lambda i: L.call("launch_route_plan", rp), iters)
+    out["route_plan_t4096_e256_k8"] = {"us": round(ms * 1e3, 2)}
+    if int(flag.item()):
+        raise RuntimeError(f"drop-in leg error flag {int(flag.item()):#x}")
+    return out
+
+
+def bench_buckets(torch, layer, ids, wts, iters: int):
+    """Per-expert-bucket utilisation of the cfg4 gate/up kernel: the same
+    launch restricted to the experts with <= 64 routed rows (weight
+    streaming, HBM-bound) and to the others (weight reuse, MFMA-bound), each
+    over its own contiguous row segments (the plan of the full layer with
+    the other bucket's experts emptied)."""
+    from pih_amd import abi
+    from pih_amd.device import ptr, stream_handle
+
+    L = abi.linear_pack()
+    flat = ids.ravel().astype(np.int64)
+    tok = np.repeat(np.arange(T), TOPK)
+    order = np.lexsort((np.tile(np.arange(TOPK), T), tok, flat))
+    e_sorted, t_sorted, w_sorted = flat[order], tok[order], wts.ravel()[order]
+    counts = np.bincount(flat, minlength=E)
+    out = {}
+    for name, sel in (("light_le64_rows", (counts > 0) & (counts <= 64)), ("heavy_gt64_rows", counts > 64)):
+        keep = sel[e_sorted]
+        offsets = np.concatenate([[0], np.cumsum(np.where(sel, counts, 0))]).astype(np.int32)
+        rows = int(keep.sum())
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        off_d, rt_d = dev(offsets), dev(t_sorted[keep].astype(np.int32))
+        rw_d = dev(w_sorted[keep].astype(np.float32))
+        mq = torch.empty(rows, I, dtype=torch.uint8, device="cuda")
+        ms_ = torch.empty(rows, I // 128, dtype=torch.float32, device="cuda")
+        r = abi.request(abi.LN["moe_fp8_gemm"], activation_e4m3=ptr(layer.xq), activation_scale=ptr(layer.xs),
+                        row_token_u32=ptr(rt_d), weight_e4m3=ptr(layer.w13), weight_scale=ptr(layer.w13_scale),
+                        expert_offsets_u32=ptr(off_d), row_weight_f32=ptr(rw_d), output=ptr(mq),
+                        output_scale=ptr(ms_), error_flag_u32=ptr(layer.flag), stream=stream_handle(),
+                        row_capacity=rows, expert_count=E, n=2 * I, k=H, activation_rows=T,
+                        scale_format=abi.SCALE_F32, output_type=abi.OUTPUT_SWIGLU_E4M3, swiglu_limit=0.0)
+        ms = _timed(torch, lambda i: L.call("launch_moe_fp8_gemm", r), iters)
+        n_exp = int(sel.sum())
+        algo = n_exp * (2 * I * H + (2 * I // 128) * (H // 128) * 4) + rows * (H + H // 32) + rows * (I + I // 32)
+        out[name] = dict(_line(ms, algo, 2.0 * rows * 2 * I * H, FP8_PEAK_TFLOPS), experts=n_exp, rows=rows)
+    return out
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_fp8_cfg4_hbm_traffic.md")
 
 
@@ -369,6 +647,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode GEMV / prefill side measurements")
     ap.add_argument("--no-mxfp4", action="store_true", help="skip the MXFP4 MoE decode side measurement")
+    ap.add_argument("--legs", default=",".join(LEGS),
+                    help="comma-separated legs to run (default all: " + ",".join(LEGS) + "); without moe_fp8 "
+                         "the line carries only the side measurements (for profiling one leg)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 1 GiB device-to-device copies (the reference kernel for scaling the "
                          "FETCH_SIZE / WRITE_SIZE counters to bytes) and exit")
@@ -379,12 +660,23 @@ def main() -> int:
         print("bench.py: this build measures one GPU (the north-star path is a single-GPU kernel "
               "pack); --gpus must be 1", file=sys.stderr)
         return 2
+    legs = {leg for leg in args.legs.split(",") if leg}
+    unknown = legs - set(LEGS)
+    if unknown:
+        print(f"bench.py: unknown legs {sorted(unknown)}", file=sys.stderr)
+        return 2
+    for flag_name, leg in (("no_cpu", "cpu"), ("no_decode", "decode"), ("no_mxfp4", "mxfp4")):
+        if getattr(args, flag_name):
+            legs.discard(leg)
 
     import torch
 
     from pih_amd import abi
     from pih_amd.device import engine_stream, flag_value
     from pih_amd.linear import MoeFp8Layer, MoeLayer
+
+    if "moe_fp8" not in legs:
+        return side_legs_only(torch, legs, args)
 
     log("generating inputs")
     ids, wts, x_bits, ids_d, wts_d, x_d, w13, s13, w2, s2 = build_inputs(torch)
@@ -432,6 +724,14 @@ def main() -> int:
         if flag_value(layer.flag) or flag_value(staged.flag):
             log(f"device error flag {flag_value(layer.flag):#x} {flag_value(staged.flag):#x}")
             return 1
+        buckets = None
+        if "buckets" in legs:
+            log("gate/up kernel per expert bucket")
+            buckets = bench_buckets(torch, staged, ids, wts, iters=max(10, args.steps))
+            if flag_value(staged.flag):
+                log(f"device error flag {flag_value(staged.flag):#x}")
+                return 1
+            log("buckets: " + json.dumps(buckets))
     ms = wall * 1000.0 / args.steps
     tflops = flop / (ms * 1e-3) / 1e12
     gu_ms = stage_ms["gate_up"]
@@ -440,25 +740,11 @@ def main() -> int:
 
     del layer, staged, w13, w2
     torch.cuda.empty_cache()
-    mxfp4 = None
-    if not args.no_mxfp4:
-        log("MXFP4 MoE decode (configs[4])")
-        with engine_stream():
-            mxfp4 = bench_mxfp4(torch, iters=max(10, args.steps))
-        torch.cuda.empty_cache()
-        log("mxfp4: " + json.dumps(mxfp4))
-
-    decode = None
-    if not args.no_decode:
-        log("decode GEMV / prefill side measurements")
-        with engine_stream():
-            decode = bench_decode(torch, iters=max(10, args.steps))
-        log("decode: " + json.dumps(decode))
-
+    side = run_side_legs(torch, legs, args)
     cpu = None
-    if not args.no_cpu:
+    if "cpu" in legs:
         log("cpu baseline")
-        cpu = cpu_baseline(ids, wts, x_bits)
+        cpu = cpu_baselines(ids, wts, x_bits)
 
     line = {
         "metric": METRIC,
@@ -486,11 +772,45 @@ def main() -> int:
                      "algorithmic_bytes": int(bytes_gu), "flop": flop_gu, "ms": round(gu_ms, 4),
                      "mfma_tflops": round(flop_gu / (gu_ms * 1e-3) / 1e12, 1),
                      "mfma_frac": round(flop_gu / (gu_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)},
-        "moe_mxfp4_decode": mxfp4,
-        "decode_gemv": decode,
+        "expert_buckets": buckets,
+        "moe_mxfp4_decode": side.get("mxfp4"),
+        "decode_gemv": side.get("decode"),
+        "drop_in": side.get("dropin"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+LEGS = ("moe_fp8", "buckets", "mxfp4", "decode", "dropin", "cpu")
+
+
+def run_side_legs(torch, legs, args) -> dict:
+    """The side measurements, each on the engine stream, freeing device
+    memory between legs."""
+    from pih_amd.device import engine_stream
+
+    iters = max(10, args.steps)
+    out = {}
+    for leg, fn, what in (("mxfp4", bench_mxfp4, "MXFP4 MoE decode (configs[4])"),
+                          ("decode", bench_decode, "decode GEMV / prefill (configs[1], [2])"),
+                          ("dropin", bench_dropin, "drop-in entries at the reference's call shapes")):
+        if leg not in legs:
+            continue
+        log(what)
+        with engine_stream():
+            out[leg] = fn(torch, iters=iters)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        log(f"{leg}: " + json.dumps(out[leg]))
+    return out
+
+
+def side_legs_only(torch, legs, args) -> int:
+    """A profiling run of chosen side legs: prints their results as one JSON
+    line without the headline (``value`` null)."""
+    side = run_side_legs(torch, legs, args)
+    print(json.dumps({"metric": METRIC, "value": None, "legs": sorted(legs), **side}), flush=True)
     return 0
 
 

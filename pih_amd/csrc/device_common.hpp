@@ -106,6 +106,12 @@ __device__ __forceinline__ uint32_t e4m3_nan_bytes(uint32_t w) {
   return ((w & 0x7f7f7f7fu) + 0x01010101u) & 0x80808080u;
 }
 
+// The word with its NaN codes (bit 7 of their byte set in `nan`, as
+// e4m3_nan_bytes returns) replaced by +0: the value the reference's decode
+// gives a NaN code while it raises the error bit
+// (plugins/kernels/deepseek-v4-sm89/native/deepseek_fp8_gemm.cu:11-17).
+__device__ __forceinline__ uint32_t e4m3_nan_to_zero(uint32_t w, uint32_t nan) { return w & ~((nan >> 7) * 0xffu); }
+
 // e2m1 magnitudes {0, .5, 1, 1.5, 2, 3, 4, 6}, bit 3 is the sign.
 __device__ __forceinline__ float e2m1_decode(uint32_t nib) {
   const uint32_t m = nib & 7u;

@@ -289,8 +289,13 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
     for (int i = 0; i < B_LOADS; ++i) rb[i] = *reinterpret_cast<const v4i*>(w_ptr[i] + (uint64_t)kb * B_STEP);
     if constexpr (ASCALE) {
       if constexpr (E8M0_A) {
+        // a 0xFF scale raises the scale bit; its block then runs with
+        // 2^-127, so it adds (almost) nothing, as the reference skips it
         rsa = static_cast<const uint8_t*>(p.a_scale)[s_src * (K / 128) + kb];
-        if (rsa == 0xffu && tid < rows) bad |= kErrScale;
+        if (rsa == 0xffu) {
+          if (tid < rows) bad |= kErrScale;
+          rsa = 0;
+        }
       } else {
         rsa = __float_as_uint(static_cast<const float*>(p.a_scale)[s_src * (K / 128) + kb]);
       }
@@ -298,22 +303,37 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
     if constexpr (KIND == kFp4) {
       rsb = *reinterpret_cast<const uint32_t*>(ws_row + (uint64_t)kb * 4);
       if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
+      // 0xFF bytes (exactly those) -> E8M0 0
+      const uint32_t ff = ((rsb & 0x7f7f7f7fu) + 0x01010101u) & rsb & 0x80808080u;
+      rsb &= ~((ff >> 7) * 0xffu);
     } else if constexpr (KIND == kBf16Fp4) {
       rsb = *reinterpret_cast<const uint16_t*>(ws_row + (uint64_t)kb * 2);
       if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
     }
     if constexpr (CHECK && FP8A) {
+      // NaN codes count as 0 in the sum (and raise the code bit), as the
+      // reference decodes them
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t t = e4m3_nan_bytes(ra[i][0]) | e4m3_nan_bytes(ra[i][1]) | e4m3_nan_bytes(ra[i][2]) |
-                           e4m3_nan_bytes(ra[i][3]);
+        uint32_t t = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t nq = e4m3_nan_bytes((uint32_t)ra[i][q]);
+          ra[i][q] = (int)e4m3_nan_to_zero((uint32_t)ra[i][q], nq);
+          t |= nq;
+        }
         if (t && (tid >> 3) + 32 * i < rows) bad |= kErrCode;
       }
       if constexpr (KIND == kFp8) {
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) {
-          const uint32_t t = e4m3_nan_bytes(rb[i][0]) | e4m3_nan_bytes(rb[i][1]) | e4m3_nan_bytes(rb[i][2]) |
-                             e4m3_nan_bytes(rb[i][3]);
+          uint32_t t = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t nq = e4m3_nan_bytes((uint32_t)rb[i][q]);
+            rb[i][q] = (int)e4m3_nan_to_zero((uint32_t)rb[i][q], nq);
+            t |= nq;
+          }
           if (t) bad |= kErrCode;
         }
       }
@@ -576,6 +596,12 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
   if (a.moe && !a.offsets) return Invalid("fp8_gemm_offsets_missing");
   if (a.a_rows_total == 0) return Invalid("fp8_gemm_a_rows_invalid");
   if (a.moe && !a.check_codes) return LaunchFp8MoeGemm(a);
+  if (!a.moe && a.m <= kSmallMRows && (a.out_kind == kOutBf16 || a.out_kind == kOutF32)) {
+    // a few activation rows: weight streaming over 16-row blocks
+    bool taken = false;
+    St s = LaunchFp8SmallM(a, taken);
+    if (!s.ok() || taken) return s;
+  }
   GemmParams gp{};
   gp.a = a.a;
   gp.a_scale = a.a_scale;
@@ -614,6 +640,13 @@ St LaunchFp4Gemm(const Fp4GemmArgs& a) {
   if (a.act != kActE4m3 && a.act != kActBf16) return Invalid("fp4_gemm_activation_type_invalid");
   if (a.moe && !a.offsets) return Invalid("fp4_gemm_offsets_missing");
   if (a.a_rows_total == 0) return Invalid("fp4_gemm_a_rows_invalid");
+  if (!a.moe && a.problems == 1 && a.act == kActE4m3 && a.m <= kSmallMRows &&
+      (a.out_kind == kOutBf16 || a.out_kind == kOutF32)) {
+    // a few activation rows (the per-expert decode call): weight streaming
+    bool taken = false;
+    St s = LaunchFp4SmallM(a, taken);
+    if (!s.ok() || taken) return s;
+  }
   GemmParams gp{};
   gp.a = static_cast<const uint8_t*>(a.a);
   gp.a_scale = a.a_scale;

@@ -102,6 +102,14 @@ struct Fp4GemmArgs {
   float swiglu_limit = 0.0f;
 };
 St LaunchFp4Gemm(const Fp4GemmArgs& a);
+
+// Small-M (m <= kSmallMRows) dense GEMM with FP8 or MXFP4 weights and e4m3
+// activations (gemm_small_m.hip): 16 weight rows per block, the block's
+// waves splitting K.  `taken` is false when the shape has no fitting split
+// (the caller then uses the tiled kernel); the callers' checks come first.
+constexpr uint32_t kSmallMRows = 64;
+St LaunchFp8SmallM(const BlockGemmArgs& a, bool& taken);
+St LaunchFp4SmallM(const Fp4GemmArgs& a, bool& taken);
 // MoE problems: experts with at most Fp4MoeLightRows(a) rows (64; 0 when
 // the shape does not fit the streaming kernel) go to the weight-streaming
 // kernel of moe_stream.hip, the others to the tiled kernel; LaunchFp4Gemm

@@ -14,8 +14,10 @@
 // Ranking is (selection descending, expert id ascending), the reference's
 // partial_sort comparator (deepseek_learned_router.cpp:57-64).
 //
-// One wavefront per token: lane l holds experts l, l + 64, ... (E <= 1024,
-// 16 per lane).  Each of the k rounds takes every lane's best untaken
+// One wavefront per token: lane l holds experts l, l + 64, ... (E <= 1024;
+// the kernel is instantiated for the 1, 2, 4, 8 or 16 per lane that E
+// needs, so E = 256 keeps 4 candidates and ~35 registers).  Each of the k
+// rounds takes every lane's best untaken
 // candidate, reduces (selection, id, base) across the wave with xor
 // shuffles so every lane knows the winner, and the owning lane marks it
 // taken.  Every lane adds the winner's base in rank order, which is the
@@ -31,7 +33,6 @@ namespace {
 
 constexpr uint32_t kRouterMaxExperts = 1024;
 constexpr uint32_t kRouterMaxTopk = 32;
-constexpr int kPerLane = kRouterMaxExperts / 64;
 constexpr uint32_t kRouterWaves = 4;
 constexpr uint32_t kNone = 0xffffffffu;
 
@@ -46,7 +47,8 @@ __device__ __forceinline__ bool ranks_before(float a, uint32_t ia, float b, uint
   return a > b || (a == b && ia < ib);
 }
 
-template <int MODE>
+// PER experts per lane (E <= 64 * PER): the candidates stay in registers
+template <int MODE, int PER>
 __global__ __launch_bounds__(64 * kRouterWaves) void router_topk_kernel(
     const float* scores, const float* bias, uint32_t* ids, float* weights, uint32_t* err, uint32_t tokens,
     uint32_t experts, uint32_t topk, float scale) {
@@ -54,10 +56,10 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_topk_kernel(
   const uint32_t t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
   if (t >= tokens) return;  // whole waves only; no block-level barrier below
   const float* s = scores + (uint64_t)t * experts;
-  float sel[kPerLane], base[kPerLane];
+  float sel[PER], base[PER];
   uint32_t taken = 0, bad = 0;
 #pragma unroll
-  for (int j = 0; j < kPerLane; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const uint32_t e = lane + 64u * j;
     sel[j] = -INFINITY;
     base[j] = 0.0f;
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_topk_kernel(
     float bv = -INFINITY, bb = 0.0f;
     uint32_t bi = kNone;
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
+    for (int j = 0; j < PER; ++j) {
       const uint32_t e = lane + 64u * j;
       if (!((taken >> j) & 1u) && ranks_before(sel[j], e, bv, bi)) {
         bv = sel[j];
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_topk_kernel(
     }
     if ((bi & 63u) == lane) {
 #pragma unroll
-      for (int j = 0; j < kPerLane; ++j)
+      for (int j = 0; j < PER; ++j)
         if ((uint32_t)j == (bi >> 6)) taken |= 1u << j;
     }
     if (r == 0) first = bb;
@@ -128,6 +130,13 @@ __global__ __launch_bounds__(64 * kRouterWaves) void router_topk_kernel(
   if (bad) atomicOr(err, bad);
 }
 
+template <int MODE, int PER>
+void launch_per(const RouterTopkArgs& a) {
+  hipLaunchKernelGGL((router_topk_kernel<MODE, PER>), dim3((a.tokens + kRouterWaves - 1) / kRouterWaves),
+                     dim3(64 * kRouterWaves), 0, a.stream, a.scores, a.bias, a.ids, a.weights, a.error_flag,
+                     a.tokens, a.experts, a.topk, a.scale);
+}
+
 }  // namespace
 
 St LaunchRouterTopk(const RouterTopkArgs& a) {
@@ -139,13 +148,20 @@ St LaunchRouterTopk(const RouterTopkArgs& a) {
   if (!__builtin_isfinite(a.scale) || a.scale <= 0.0f) return Invalid("router_topk_scale_invalid");
   St clean = RequireCleanLastError();
   if (!clean.ok()) return clean;
-  const dim3 grid((a.tokens + kRouterWaves - 1) / kRouterWaves);
-  if (a.mode == kRouterSqrtSoftplus)
-    hipLaunchKernelGGL(router_topk_kernel<kRouterSqrtSoftplus>, grid, dim3(64 * kRouterWaves), 0, a.stream,
-                       a.scores, a.bias, a.ids, a.weights, a.error_flag, a.tokens, a.experts, a.topk, a.scale);
-  else
-    hipLaunchKernelGGL(router_topk_kernel<kRouterSoftmax>, grid, dim3(64 * kRouterWaves), 0, a.stream, a.scores,
-                       a.bias, a.ids, a.weights, a.error_flag, a.tokens, a.experts, a.topk, a.scale);
+  const uint32_t per = (a.experts + 63) / 64;
+  if (a.mode == kRouterSqrtSoftplus) {
+    if (per <= 1) launch_per<kRouterSqrtSoftplus, 1>(a);
+    else if (per <= 2) launch_per<kRouterSqrtSoftplus, 2>(a);
+    else if (per <= 4) launch_per<kRouterSqrtSoftplus, 4>(a);
+    else if (per <= 8) launch_per<kRouterSqrtSoftplus, 8>(a);
+    else launch_per<kRouterSqrtSoftplus, 16>(a);
+  } else {
+    if (per <= 1) launch_per<kRouterSoftmax, 1>(a);
+    else if (per <= 2) launch_per<kRouterSoftmax, 2>(a);
+    else if (per <= 4) launch_per<kRouterSoftmax, 4>(a);
+    else if (per <= 8) launch_per<kRouterSoftmax, 8>(a);
+    else launch_per<kRouterSoftmax, 16>(a);
+  }
   return AfterLaunch("router_topk_launch_failed");
 }
 
