@@ -21,15 +21,23 @@
 //   pih_qwen_silu_mul_bf16_v1(gate@0, up@8, output@16, elements@24)
 //     (qwen_bf16_primitives.cu:274-283): out = bf16(silu(g) * u), any grid.
 //
-// W4A16 decomposition: every output of a block lies in one x row (n is a
-// multiple of 256), so block b computes 256 consecutive W rows for row
-// m = 256 b / n.  Wave w streams rows 64w .. 64w+63 of those; for each
-// 1024-deep K chunk lane l owns k [16l, 16l+16) (8 packed bytes: a wave
-// reads one 512-byte row segment per load) and keeps one fp32 partial per
-// row; a transpose-reduction over the 64 lanes then leaves row r's total in
-// lane r.  The per-(row, 128 k) scale multiplies the lane's integer-weight
-// dot product (the sum order differs from the reference's strict k order;
-// results agree to fp32 rounding).
+// W4A16 on the matrix cores, inside the model's launch geometry (ceil(m*n /
+// 256) blocks of 256 threads; which 256 outputs a block computes is the
+// kernel's choice as long as every output is computed once):
+//   * m a multiple of 16: block b computes a 16 x 16 output tile (x rows
+//     16 (b / (n/16)) .., W rows 16 (b % (n/16)) ..), its 4 waves splitting
+//     K, so each W row is read by m/16 blocks instead of m;
+//   * otherwise (decode): block b computes 256 W rows of x row 256 b / n,
+//     64 per wave, every wave walking all of K.
+// Per 128-deep group: a lane loads 16 bytes of its W row (32 nibbles, k
+// [32lg, 32lg+32) of the group) and the 32 matching x values; MFMA j of the
+// four 16x16x32 bf16 MFMAs takes k [32lg + 8j, +8) from every lane (the
+// order of k inside one MFMA does not matter as long as both operands use
+// it).  Nibbles become the bf16 values 128 + u (u = q + 8, two masks and
+// four v_perm per word, x permuted to the same order), so the MFMA sums
+// x (128 + u) and the group's result is s (sum - 136 sum_k x) with the
+// fp16 scale s of (W row, group).  The sum order differs from the
+// reference's strict k order; results agree to fp32 rounding.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -64,15 +72,55 @@ __device__ __forceinline__ uint32_t reserved_nibbles(uint32_t w) {
   return (t - 0x11111111u) & ~t & 0x88888888u;
 }
 
-// sum over the 8 signed nibbles of w (low nibble first) times x[0..7]
-__device__ __forceinline__ float dot8(uint32_t w, const float* x) {
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+// 8 nibbles of a word (k offsets 0..7, low first), each the signed q with
+// 8 subtracted away: u = q + 8 as the bf16 value 128 + u, in the order
+// k = 0, 2, 4, 6, 1, 3, 5, 7 (two masks and four v_perm under the 0x43
+// exponent byte of 128)
+__device__ __forceinline__ v4i nibbles_to_bf16(uint32_t w) {
+  const uint32_t t = w ^ 0x88888888u;  // two's complement nibble -> q + 8
+  const uint32_t lo = t & 0x0F0F0F0Fu, hi = (t >> 4) & 0x0F0F0F0Fu;
+  constexpr uint32_t kExp = 0x43434343u;
+  return v4i{(int)__builtin_amdgcn_perm(kExp, lo, 0x04010400u), (int)__builtin_amdgcn_perm(kExp, lo, 0x04030402u),
+             (int)__builtin_amdgcn_perm(kExp, hi, 0x04010400u), (int)__builtin_amdgcn_perm(kExp, hi, 0x04030402u)};
+}
+
+// eight bf16 x values (k = 0..7) into the order nibbles_to_bf16 produces
+__device__ __forceinline__ v4i x_in_nibble_order(v4i v) {
+  const uint32_t w0 = (uint32_t)v[0], w1 = (uint32_t)v[1], w2 = (uint32_t)v[2], w3 = (uint32_t)v[3];
+  return v4i{(int)__builtin_amdgcn_perm(w1, w0, 0x05040100u), (int)__builtin_amdgcn_perm(w3, w2, 0x05040100u),
+             (int)__builtin_amdgcn_perm(w1, w0, 0x07060302u), (int)__builtin_amdgcn_perm(w3, w2, 0x07060302u)};
+}
+
+__device__ __forceinline__ float sum8(v4i v) {
   float s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int32_t q = (int32_t)((w >> (4 * j)) & 0xfu);
-    s = __builtin_fmaf(x[j], (float)(q < 8 ? q : q - 16), s);
-  }
+  for (int q = 0; q < 4; ++q) s += bf16_to_f32((uint32_t)v[q] & 0xffffu) + bf16_to_f32((uint32_t)v[q] >> 16);
   return s;
+}
+
+// One 128-deep group of one 16-row W block against 16 x rows (A operand
+// rows): w = the lane's 16 packed bytes (W row lr, k [32lg, 32lg+32) of the
+// group), x = its 32 x values in four 8-value pieces (x row lr of the A
+// operand), xs_t = the group's sum of x over the 128 k for A row 4lg + t.
+// Adds s * (sum x (128+u) - 136 sum x) to acc[t] and flags the W row's
+// reserved nibbles and bad scale.
+__device__ __forceinline__ void group_mma(v4i w, const v4i (&x)[4], v4f xs, float s, v4f& acc, uint32_t& bad_nib,
+                                          uint32_t& bad_scale) {
+  v4f pq = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (reserved_nibbles((uint32_t)w[j])) bad_nib = 1;
+    pq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, x_in_nibble_order(x[j])),
+                                                 __builtin_bit_cast(v8bf, nibbles_to_bf16((uint32_t)w[j])), pq, 0, 0,
+                                                 0);
+  }
+  if (!(s > 0.0f) || !__builtin_isfinite(s)) bad_scale = 1;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = __builtin_fmaf(s, __builtin_fmaf(-136.0f, xs[t], pq[t]), acc[t]);
 }
 
 }  // namespace
@@ -89,76 +137,122 @@ extern "C" __global__ __launch_bounds__(256) void pih_qwen_w4a16_gemm_compat_v1(
     return;
   }
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t lr = lane & 15, lg = lane >> 4;
+  const uint64_t kb = k / 2u, groups = k / 128u;
+
+  if (m % 16u == 0) {
+    // ---- 16 x 16 output tiles, the 4 waves splitting the K groups
+    __shared__ float s_acc[4][4][64];
+    __shared__ uint32_t s_bad[4][16];
+    const uint64_t ctiles = n / 16u;
+    const uint64_t xr0 = (blockIdx.x / ctiles) * 16u, wr0 = (blockIdx.x % ctiles) * 16u;
+    const uint16_t* xrow = input + (xr0 + lr) * k + lg * 32u;
+    const uint8_t* wrow = packed_weight + (wr0 + lr) * kb + lg * 16u;
+    const uint16_t* srow = scales + (wr0 + lr) * groups;
+    const uint64_t g0 = wave * groups / 4u, g1 = (wave + 1) * groups / 4u;
+    v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+    uint32_t bad_nib = 0, bad_scale = 0;
+    for (uint64_t g = g0; g < g1; ++g) {
+      const v4i w = *reinterpret_cast<const v4i*>(wrow + g * 64u);
+      v4i x[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = *reinterpret_cast<const v4i*>(xrow + g * 128u + j * 8u);
+      const float s = f16_to_f32(srow[g]);
+      // the group's x sum of A row lr, then of the rows 4lg + t this lane
+      // holds results for
+      float part = sum8(x[0]) + sum8(x[1]) + sum8(x[2]) + sum8(x[3]);
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      v4f xs;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xs[t] = __shfl(part, (int)(4u * lg + t), 64);
+      group_mma(w, x, xs, s, acc, bad_nib, bad_scale);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s_acc[wave][t][lane] = acc[t];
+    // per W row (column lr): OR over the lanes and waves that saw it
+    const uint32_t flags = (bad_nib ? 1u : 0u) | (bad_scale ? 2u : 0u);
+    if (lg == 0) s_bad[wave][lr] = 0;
+    __syncthreads();
+    if (flags) atomicOr(&s_bad[wave][lr], flags);
+    __syncthreads();
+    if (wave == 0) {
+      const uint32_t rf = s_bad[0][lr] | s_bad[1][lr] | s_bad[2][lr] | s_bad[3][lr];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float y = s_acc[0][t][lane] + s_acc[1][t][lane] + s_acc[2][t][lane] + s_acc[3][t][lane];
+        uint32_t code = 0;
+        if (rf & 1u) code = kErrReservedNibble;
+        else if (rf & 2u) code = kErrScale;
+        else if (!__builtin_isfinite(y)) code = kErrNonFinite;
+        if (code) {
+          publish(error_flag, code);
+          continue;
+        }
+        output[(xr0 + 4u * lg + t) * n + wr0 + lr] = (uint16_t)f32_to_bf16(y);
+      }
+    }
+    return;
+  }
+
+  // ---- decode: 256 W rows of one x row, 64 per wave, all of K per wave
   const uint64_t first = (uint64_t)blockIdx.x * 256u;
   const uint64_t row = first / n;
   const uint64_t n0 = first - row * n + wave * 64u;  // this wave's first W row
-  const uint64_t kb = k / 2u, kgroups = k / 128u;
-  const uint16_t* x = input + row * k;
-
-  float part[64];
+  const uint16_t* xrow = input + row * k + lg * 32u;
+  v4f acc[4];
 #pragma unroll
-  for (int r = 0; r < 64; ++r) part[r] = 0.0f;
-  uint64_t bad_nib = 0, bad_scale = 0;  // per-row flags of this lane's k slices
-
-  for (uint64_t c = 0; c < k; c += 1024u) {
-    const uint64_t k0 = c + lane * 16u;  // this lane's 16 k of the chunk
-    if (k0 >= k) continue;               // a last chunk shorter than 1024
-    float xv[16];
-    const uint4 x01 = *reinterpret_cast<const uint4*>(x + k0);
-    const uint4 x23 = *reinterpret_cast<const uint4*>(x + k0 + 8);
-    const uint32_t xw[8] = {x01.x, x01.y, x01.z, x01.w, x23.x, x23.y, x23.z, x23.w};
+  for (int b = 0; b < 4; ++b) acc[b] = v4f{0.f, 0.f, 0.f, 0.f};
+  uint32_t bad_nib[4] = {0, 0, 0, 0}, bad_scale[4] = {0, 0, 0, 0};
+  // next group's operands load while this one computes
+  v4i wn[4], xn[4];
+  uint32_t sn[4];
+  auto load = [&](uint64_t g) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      xv[2 * j] = bf16_to_f32(xw[j] & 0xffffu);
-      xv[2 * j + 1] = bf16_to_f32(xw[j] >> 16);
+    for (int b = 0; b < 4; ++b) {
+      const uint64_t wr = n0 + 16u * b + lr;
+      wn[b] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(packed_weight + wr * kb + g * 64u + lg * 16u));
+      sn[b] = scales[wr * groups + g];
     }
-    const uint64_t g = k0 / 128u;
 #pragma unroll
-    for (int r = 0; r < 64; ++r) {
-      const uint64_t wr = n0 + r;
-      const uint2 w = *reinterpret_cast<const uint2*>(packed_weight + wr * kb + k0 / 2u);
-      const float s = f16_to_f32(scales[wr * kgroups + g]);
-      if (reserved_nibbles(w.x) | reserved_nibbles(w.y)) bad_nib |= 1ull << r;
-      if (!(s > 0.0f) || !__builtin_isfinite(s)) bad_scale |= 1ull << r;
-      part[r] = __builtin_fmaf(s, dot8(w.x, xv) + dot8(w.y, xv + 8), part[r]);
+    for (int j = 0; j < 4; ++j) xn[j] = *reinterpret_cast<const v4i*>(xrow + g * 128u + j * 8u);
+  };
+  load(0);
+  for (uint64_t g = 0; g < groups; ++g) {
+    v4i w[4], x[4];
+    uint32_t sc[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) w[b] = wn[b], sc[b] = sn[b];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = xn[j];
+    if (g + 1 < groups) load(g + 1);
+    // every A row is this x row: the group's x sum is one value
+    float part = sum8(x[0]) + sum8(x[1]) + sum8(x[2]) + sum8(x[3]);
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    const v4f xs = v4f{part, part, part, part};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) group_mma(w[b], x, xs, f16_to_f32(sc[b]), acc[b], bad_nib[b], bad_scale[b]);
+  }
+  // lane (lr, lg) holds W row n0 + 16b + lr in all four rows t (one x row);
+  // the row's flags are the OR over the four lanes lg of that row
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    uint32_t f = (bad_nib[b] ? 1u : 0u) | (bad_scale[b] ? 2u : 0u);
+    f |= __shfl_xor(f, 16, 64);
+    f |= __shfl_xor(f, 32, 64);
+    if (lg != 0) continue;
+    const float y = acc[b][0];
+    uint32_t code = 0;
+    if (f & 1u) code = kErrReservedNibble;
+    else if (f & 2u) code = kErrScale;
+    else if (!__builtin_isfinite(y)) code = kErrNonFinite;
+    if (code) {
+      publish(error_flag, code);
+      continue;
     }
+    output[row * n + n0 + 16u * b + lr] = (uint16_t)f32_to_bf16(y);
   }
-
-  // transpose-reduce: after the stage with distance d, lane l keeps the
-  // rows whose bit log2(d) equals lane bit log2(d); lane r ends with row r
-#pragma unroll
-  for (int d = 32, half = 32; d >= 1; d >>= 1, half >>= 1) {
-    const bool hi = (lane & (uint32_t)d) != 0;
-#pragma unroll
-    for (int i = 0; i < half; ++i) {
-      const float send = hi ? part[i] : part[i + half];
-      const float keep = hi ? part[i + half] : part[i];
-      part[i] = keep + __shfl_xor(send, d, 64);
-    }
-  }
-  // row flags: OR over the lanes (every lane covers a slice of every row)
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    bad_nib |= ((uint64_t)__shfl_xor((uint32_t)(bad_nib >> 32), d, 64) << 32) | __shfl_xor((uint32_t)bad_nib, d, 64);
-    bad_scale |=
-        ((uint64_t)__shfl_xor((uint32_t)(bad_scale >> 32), d, 64) << 32) | __shfl_xor((uint32_t)bad_scale, d, 64);
-  }
-  // an element with a failure is not written (the reference returns at its
-  // first failing k; a reserved nibble is reported before a bad scale)
-  if ((bad_nib >> lane) & 1u) {
-    publish(error_flag, kErrReservedNibble);
-    return;
-  }
-  if ((bad_scale >> lane) & 1u) {
-    publish(error_flag, kErrScale);
-    return;
-  }
-  const float y = part[0];
-  if (!__builtin_isfinite(y)) {
-    publish(error_flag, kErrNonFinite);
-    return;
-  }
-  output[row * n + n0 + lane] = (uint16_t)f32_to_bf16(y);
 }
 
 extern "C" __global__ __launch_bounds__(256) void pih_qwen_silu_mul_bf16_v1(const uint16_t* gate, const uint16_t* up,

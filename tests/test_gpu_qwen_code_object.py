@@ -47,9 +47,11 @@ def _run_w4a16(co, x, q, s, m, n, k, grid=None, block=256):
     return out.cpu().numpy().view(np.uint16), int(flag.item()) & 0xFFFFFFFF
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 16, 17, 48])
 @pytest.mark.parametrize("n,k", QWEN06B)
 def test_w4a16_compat_qwen06b_shapes(co, m, n, k):
+    """m = 16 and 48 take the 16 x 16 tile mapping of the launch's blocks,
+    the others the per-x-row mapping."""
     q, s = synth.int4_sym_weight(synth.config_seed(3, 900 + n + k), n, k)
     x = synth.bf16_normal(synth.config_seed(3, 950 + m), (m, k))
     got, flag = _run_w4a16(co, x, q, s, m, n, k)
@@ -106,6 +108,24 @@ def test_w4a16_compat_errors(co):
     got, flag = _run_w4a16(co, synth.bf16_normal(1, (4097, 128)), *synth.int4_sym_weight(6, 256, 128), 4097, 256,
                            128)
     assert flag == 11
+
+
+def test_w4a16_compat_errors_tile_mapping(co):
+    """m = 32 (16 x 16 output tiles, K split over the block's waves): a
+    reserved nibble in W row 300 leaves that column unwritten in every row
+    (code 12); the other columns match the oracle."""
+    m, n, k = 32, 1024, 1024
+    q, s = synth.int4_sym_weight(synth.config_seed(3, 4300), n, k)
+    x = synth.bf16_normal(synth.config_seed(3, 4301), (m, k))
+    ref = oracle.w4a16_sym(x, q, s)
+    q2 = q.copy()
+    q2[300, 400] = (q2[300, 400] & 0xF0) | 0x08
+    got, flag = _run_w4a16(co, x, q2, s, m, n, k)
+    assert flag == 12
+    assert (got[:, 300] == SENTINEL).all()
+    keep = np.ones(n, bool)
+    keep[300] = False
+    assert_close(oracle.bf16_bits_to_f32(got[:, keep]), oracle.bf16_bits_to_f32(ref[:, keep]), "tile rows kept")
 
 
 def test_w4a16_compat_nonfinite_output(co):
