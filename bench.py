@@ -449,6 +449,8 @@ def bench_dropin(torch, iters: int):
                       code object with the model plan's geometry at the
                       Qwen3-0.6B shapes, M = 1; the BF16 MLP block of
                       configs[0] (x [16, 1024]);
+      LM heads        DeepSeek launch_lm_head at 1, 64 and 512 rows and the
+                      Qwen3-0.6B 1..32-row plan bank at 1 and 32 rows;
       router          launch_router_topk (softmax top-8 of 256) and
                       launch_route_plan at 4096 tokens."""
     from pih_amd import abi
@@ -550,6 +552,26 @@ def bench_dropin(torch, iters: int):
     out["cfg1_qwen_mlp_m16"] = dict(_line(ms, per + 16 * 1024 * 2 * 2, 2.0 * 16 * 3 * 3072 * 1024, 2516.6),
                                     launches=4)
     del blocks, wv
+    # ---- LM heads: DeepSeek launch_lm_head (1.06 GB bf16 weight) and the
+    # Qwen3-0.6B tied head (311 MB, two copies rotated), fp32 logits
+    from pih_amd.linear import QwenLmHead, deepseek_lm_head
+    wd = (torch.randn(129280, 4096, device=dev, generator=gen, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    for m in (1, 64, 512):
+        x = torch.randn(m, 4096, device=dev, generator=gen).to(torch.bfloat16)
+        lo = torch.empty(m, 129280, dtype=torch.float32, device=dev)
+        ms = _timed(torch, lambda i: deepseek_lm_head(x, wd, out=lo, flag=flag), iters)
+        out[f"ds_lm_head_m{m}_4096to129280"] = _line(ms, 129280 * 4096 * 2 + m * 4096 * 2 + m * 129280 * 4,
+                                                     2.0 * m * 129280 * 4096, 2516.6)
+    del wd
+    wq = [(torch.randn(151936, 1024, device=dev, generator=gen) * 0.02).to(torch.bfloat16) for _ in range(2)]
+    head = QwenLmHead(32)
+    for m in (1, 32):
+        x = torch.randn(m, 1024, device=dev, generator=gen).to(torch.bfloat16)
+        lo = torch.empty(m, 151936, dtype=torch.float32, device=dev)
+        ms = _timed(torch, lambda i: head.execute(x, wq[i % 2], lo), iters)
+        out[f"qwen_lm_head_m{m}_1024to151936"] = _line(ms, 151936 * 1024 * 2 + m * 1024 * 2 + m * 151936 * 4,
+                                                       2.0 * m * 151936 * 1024, 2516.6)
+    del wq
     # ---- router top-k and route plan, 4096 tokens x 256 experts
     sc = torch.randn(T, E, device=dev, generator=gen)
     ids, wts, _ = router_topk(sc, TOPK, abi.ROUTER_SOFTMAX, flag=flag)

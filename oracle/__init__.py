@@ -60,6 +60,7 @@ def lib() -> C.CDLL:
             "po_w4a16_asym": (C.c_int, [P, P, P, P, U32, U32, U32, P]),
             "po_w4a16_asym_dequant": (C.c_int, [P, P, P, U32, U32, P]),
             "po_bf16_gemm": (None, [P, P, U32, U32, U32, P]),
+            "po_lm_head": (U32, [P, P, U32, U32, U32, P]),
             "po_silu_mul": (None, [P, P, C.c_size_t, P]),
             "po_swiglu": (C.c_int, [P, P, C.c_size_t, F32, P]),
             "po_route_plan": (C.c_int, [P, P, U32, U32, U32, P, P, P, P]),
@@ -253,6 +254,18 @@ def bf16_gemm(a_bits, w_bits) -> np.ndarray:
     out = np.empty((m, n), np.float32)
     lib().po_bf16_gemm(_ptr(a_bits), _ptr(w_bits), m, n, k, _ptr(out))
     return out
+
+
+def lm_head(x_bits, w_bits):
+    """DeepSeek LM head logits (fp32, the reference kernel's 256-way strided
+    partial sums and tree) and its error bits (64 non-finite operand, 128
+    non-finite logit)."""
+    rows, hidden = x_bits.shape
+    vocab = w_bits.shape[0]
+    out = np.empty((rows, vocab), np.float32)
+    err = lib().po_lm_head(_ptr(np.ascontiguousarray(x_bits)), _ptr(np.ascontiguousarray(w_bits)), rows, vocab,
+                           hidden, _ptr(out))
+    return out, int(err)
 
 
 # ------------------------------------------------------------ elementwise

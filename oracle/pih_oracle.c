@@ -18,6 +18,7 @@ void po_set_threads(int threads) { g_threads = threads < 1 ? 1 : threads; }
 int po_get_threads(void) { return g_threads; }
 
 #define PO_PARALLEL_FOR _Pragma("omp parallel for schedule(static) num_threads(g_threads)")
+#define PO_PARALLEL_FOR_REDUCE_OR(v) _Pragma("omp parallel for schedule(static) num_threads(g_threads) reduction(|:err)")
 
 /* ----------------------------------------------------------------- codecs */
 static inline uint32_t f2u(float v) { uint32_t u; memcpy(&u, &v, 4); return u; }
@@ -415,6 +416,37 @@ void po_bf16_gemm(const uint16_t* a, const uint16_t* w, uint32_t m, uint32_t n,
     for (uint32_t i = 0; i < k; ++i) acc += po_bf16_to_f32(ar[i]) * po_bf16_to_f32(wr[i]);
     out[idx] = acc;
   }
+}
+
+/* DeepSeek LM head (plugins/kernels/deepseek-v4-sm89/native/
+ * deepseek_endpoint.cu:94-115): logits[r, v] = sum_h x[r, h] * W[v, h] in
+ * the reference block's order -- 256 strided fp32 partial sums (thread t
+ * takes h = t, t + 256, ...), then the shared-memory tree halving 128, 64,
+ * ..., 1 (reduce_sum, :13-24).  Bit 64 when an x or W element read is
+ * non-finite, bit 128 when the sum is; the logit is written either way. */
+uint32_t po_lm_head(const uint16_t* x, const uint16_t* w, uint32_t rows, uint32_t vocab,
+                    uint32_t hidden, float* logits) {
+  uint32_t err = 0;
+  PO_PARALLEL_FOR_REDUCE_OR(err)
+  for (int64_t idx = 0; idx < (int64_t)rows * vocab; ++idx) {
+    const uint32_t row = (uint32_t)(idx / vocab), word = (uint32_t)(idx % vocab);
+    float part[256];
+    for (uint32_t t = 0; t < 256; ++t) {
+      float acc = 0.0f;
+      for (uint32_t h = t; h < hidden; h += 256) {
+        const float xv = po_bf16_to_f32(x[(size_t)row * hidden + h]);
+        const float wv = po_bf16_to_f32(w[(size_t)word * hidden + h]);
+        if (!isfinite(xv) || !isfinite(wv)) err |= 64u;
+        acc += xv * wv;
+      }
+      part[t] = acc;
+    }
+    for (uint32_t width = 128; width != 0; width >>= 1)
+      for (uint32_t t = 0; t < width; ++t) part[t] += part[t + width];
+    if (!isfinite(part[0])) err |= 128u;
+    logits[(size_t)row * vocab + word] = part[0];
+  }
+  return err;
 }
 
 /* ------------------------------------------------------------ elementwise */

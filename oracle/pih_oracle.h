@@ -126,6 +126,9 @@ int po_w4a16_asym_dequant(const uint32_t* qweight, const uint16_t* scales_bf16,
 /* BF16 linear as cuBLASLt computes it for GemmPlan
  * (src/backend/cuda/gemm_plan.cpp:83-198): C[m,n] = A[m,k] . W[n,k]^T with a
  * strict-k fp32 dot.  fp32 result; callers round to bf16 with RNE. */
+/* DeepSeek LM head in the reference's reduction order; returns error bits 64/128. */
+uint32_t po_lm_head(const uint16_t* x, const uint16_t* w, uint32_t rows, uint32_t vocab,
+                    uint32_t hidden, float* logits);
 void po_bf16_gemm(const uint16_t* a, const uint16_t* w, uint32_t m, uint32_t n,
                   uint32_t k, float* out);
 

@@ -4,8 +4,9 @@
 // Drop-in for plugins/kernels/deepseek-v4-sm89/kernel_pack.cpp:42-585.  The
 // table keeps the reference's order and request structs.  Linear/MoE entries
 // run the gfx950 kernels of this library; the attention, compressor,
-// indexer, hyper-connection, embedding, head and sampling entries stay in
-// the table so its size and order match, and answer UNAVAILABLE.
+// indexer, hyper-connection, embedding and sampling entries stay in the
+// table so its size and order match, and answer UNAVAILABLE; the LM head
+// runs the BF16 GEMM/GEMV.
 //
 // Shapes fixed by the reference ABI (no size field in the request): route
 // gather, expert accumulate and finalize use hidden 4096; expert and shared
@@ -25,6 +26,7 @@ namespace {
 constexpr uint32_t kAbi = PIH_DEEPSEEK_KERNELS_ABI_VERSION_V1;
 constexpr uint32_t kHidden = 4096;
 constexpr uint32_t kIntermediate = 2048;
+constexpr uint32_t kVocab = 129280;
 constexpr float kSwiGluLimit = 10.0f;
 
 const pih_kernel_pack_identity_v1 kIdentity = {
@@ -227,6 +229,44 @@ St RouterGemm(const pih_deepseek_router_gemm_launch_v1* r) {
   return LaunchBf16Gemm(a);
 }
 
+// LM head: logits f32 [rows, 129280] = x bf16 [rows, 4096] . W bf16
+// [129280, 4096]^T (reference deepseek_endpoint.cu:94-115, launcher
+// :484-497, validator deepseek_endpoint.cpp:57-66).  Error bits as the
+// reference: 128 for a non-finite logit (the logit is still written), 64
+// for a non-finite x or W element.  Decode row counts run the
+// weight-streaming GEMV, larger ones the MFMA GEMM; the fp32 sums run in
+// the kernels' order, not the reference's 256-thread tree.
+St LmHead(const pih_deepseek_lm_head_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("lm_head_request_invalid");
+  if (!r->input_bf16 || !r->weight_bf16 || !r->logits_f32 || !r->error_flag_u32 || !r->stream ||
+      r->output_rows == 0 || r->output_rows > 4096 || r->vocab_size != kVocab || r->hidden_size != kHidden ||
+      r->logits_f32 == r->input_bf16 || r->logits_f32 == r->weight_bf16)
+    return Invalid("lm_head_launch_invalid");
+  Bf16GemmArgs g;
+  g.a = Ptr<const uint16_t>(r->input_bf16);
+  g.w = Ptr<const uint16_t>(r->weight_bf16);
+  g.out = Ptr<void>(r->logits_f32);
+  g.stream = AsStream(r->stream);
+  g.m = r->output_rows;
+  g.n = r->vocab_size;
+  g.k = r->hidden_size;
+  g.out_kind = kOutF32;
+  g.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  g.nonfinite_bit = 128u;
+  St s = LaunchBf16Gemm(g);
+  if (!s.ok()) return s;
+  NonfiniteScanArgs c;
+  c.x = g.a;
+  c.w = g.w;
+  c.x_elems = (uint64_t)r->output_rows * r->hidden_size;
+  c.w_elems = (uint64_t)r->vocab_size * r->hidden_size;
+  c.error_flag = g.error_flag;
+  c.stream = g.stream;
+  c.trigger_bit = 128u;
+  c.set_bit = 64u;
+  return LaunchNonfiniteScan(c);
+}
+
 // Entries outside the linear/MoE path: present, validated, unavailable.
 #define PIH_AMD_UNAVAILABLE_ENTRY(fn, type, name)                     \
   St fn(const type* r) {                                              \
@@ -240,7 +280,6 @@ PIH_AMD_UNAVAILABLE_ENTRY(Rotary, pih_deepseek_rotary_launch_v1, "rotary")
 PIH_AMD_UNAVAILABLE_ENTRY(KvFp8Simulate, pih_deepseek_kv_fp8_simulate_launch_v1, "kv_fp8")
 PIH_AMD_UNAVAILABLE_ENTRY(Embedding, pih_deepseek_embedding_launch_v1, "embedding")
 PIH_AMD_UNAVAILABLE_ENTRY(HcHead, pih_deepseek_hc_head_launch_v1, "hc_head")
-PIH_AMD_UNAVAILABLE_ENTRY(LmHead, pih_deepseek_lm_head_launch_v1, "lm_head")
 PIH_AMD_UNAVAILABLE_ENTRY(Argmax, pih_deepseek_argmax_launch_v1, "argmax")
 PIH_AMD_UNAVAILABLE_ENTRY(StochasticSample, pih_deepseek_stochastic_sample_launch_v1, "sample")
 PIH_AMD_UNAVAILABLE_ENTRY(CompressorPooling, pih_deepseek_compressor_pooling_launch_v1, "compressor_pooling")

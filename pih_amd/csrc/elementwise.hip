@@ -13,6 +13,8 @@
 //            bf16 number, so the decode is exact.
 // All arithmetic is fp32 with no contraction (the build passes
 // -ffp-contract=off), in the reference's operation order.
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -91,6 +93,29 @@ uint32_t grid_for(uint64_t items) {
   return (uint32_t)(b > 16384 ? 16384 : b);
 }
 
+
+// Scan of bf16 operands for a non-finite element, run only when `trigger`
+// is already set in *err (so a clean call costs one flag read per block).
+// Used for the DeepSeek LM head's bit 64 (deepseek_endpoint.cu:94-115 sets
+// it when any x or W element it reads is non-finite): every logit reads its
+// whole x row and W row, and a non-finite operand makes the dot non-finite,
+// so the GEMM's non-finite-logit bit is set whenever bit 64 is due.
+__global__ __launch_bounds__(256) void nonfinite_scan_kernel(const uint4* x, uint64_t nx, const uint4* w,
+                                                             uint64_t nw, uint32_t* err, uint32_t trigger,
+                                                             uint32_t bit) {
+  if (!(__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & trigger)) return;
+  const uint64_t total = nx + nw, stride = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t bad = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const uint4 v = i < nx ? x[i] : w[i - nx];
+    const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bad |= ((q[j] & 0x7f80u) == 0x7f80u) | ((q[j] & 0x7f800000u) == 0x7f800000u);
+  }
+  if (bad) atomicOr(err, bit);
+}
+
 }  // namespace
 
 St LaunchSwiGlu(const SwiGluArgs& a) {
@@ -123,6 +148,20 @@ St LaunchMxfp4Decode(const Mxfp4DecodeArgs& a) {
   hipLaunchKernelGGL(mxfp4_decode_kernel, dim3(grid_for((uint64_t)a.rows * a.k / 2u)), dim3(256), 0,
                      a.stream, a.packed, a.scales, a.out, a.error_flag, a.rows, a.k);
   return AfterLaunch("mxfp4_decode_launch_failed");
+}
+
+St LaunchNonfiniteScan(const NonfiniteScanArgs& a) {
+  if (!a.x || !a.w || !a.error_flag || !a.stream) return Invalid("nonfinite_scan_null_argument");
+  if (a.x_elems % 8 || a.w_elems % 8 || (reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w)) % 16)
+    return Invalid("nonfinite_scan_shape_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  const uint64_t vec = (a.x_elems + a.w_elems) / 8;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>((vec + 255) / 256, 2048);
+  hipLaunchKernelGGL(nonfinite_scan_kernel, dim3(grid ? grid : 1), dim3(256), 0, a.stream,
+                     reinterpret_cast<const uint4*>(a.x), a.x_elems / 8, reinterpret_cast<const uint4*>(a.w),
+                     a.w_elems / 8, a.error_flag, a.trigger_bit, a.set_bit);
+  return AfterLaunch("nonfinite_scan_launch_failed");
 }
 
 }  // namespace pih_amd

@@ -692,8 +692,11 @@ St LaunchBf16Gemm(const Bf16GemmArgs& a) {
   uint32_t grid;
   St s = prepare(gp, grid, a.m, a.n, a.k, 1, false, a.out_kind, 0);
   if (!s.ok()) return s;
-  // no error flag in the GemmPlan contract: nothing for the kernel to report
-  gp.err = nullptr;
+  // the GemmPlan contract has no error flag; the LM head passes one for its
+  // non-finite-logit bit (the logit is stored either way)
+  gp.err = a.error_flag && a.nonfinite_bit ? a.error_flag : nullptr;
+  gp.err_nonfinite = gp.err ? a.nonfinite_bit : 0u;
+  gp.write_nonfinite = 1u;
   if (a.out_kind == kOutBf16) launch_one<kBf16, kScaleUe8m0, kOutBf16, false, false>(gp, grid, a.stream);
   else launch_one<kBf16, kScaleUe8m0, kOutF32, false, false>(gp, grid, a.stream);
   return AfterLaunch("bf16_gemm_launch_failed");

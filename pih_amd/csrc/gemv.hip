@@ -50,6 +50,7 @@ struct GemvParams {
   uint32_t* err;
   uint32_t m, n, k;
   uint32_t out_f32;
+  uint32_t nonfinite_or;  // bf16 weights: OR'd into *err for a non-finite output (0: none)
 };
 
 // K elements one wave consumes per 16-byte-per-lane load step.
@@ -245,6 +246,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
     else static_cast<uint16_t*>(p.out)[(uint64_t)mrow * p.n + col] = (uint16_t)f32_to_bf16_bits(v);
   }
   if (nonfinite && FMT != kWBf16) publish(p.err, kQwenNonFinite);
+  if (nonfinite && FMT == kWBf16 && p.nonfinite_or) atomicOr(p.err, p.nonfinite_or);
 }
 
 // ---------------------------------------------------------------------------
@@ -564,6 +566,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
   }
   if constexpr (kInt4)
     if (nonfinite) publish(p.err, kQwenNonFinite);
+  if constexpr (!kInt4)
+    if (nonfinite && p.nonfinite_or) atomicOr(p.err, p.nonfinite_or);
 }
 
 // ---------------------------------------------------------------------------
@@ -815,6 +819,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mid_kernel(GemvGroup grp, uin
   }
   if constexpr (kInt4)
     if (nonfinite) publish(p.err, kQwenNonFinite);
+  if constexpr (!kInt4)
+    if (nonfinite && p.nonfinite_or) atomicOr(p.err, p.nonfinite_or);
 }
 
 // Exact dequant of an INT4 weight to fp32: w[n, k] = (q - z) * s (asym) or
@@ -1051,6 +1057,10 @@ St LaunchBf16Gemv(const Bf16GemmArgs& a) {
   p.n = a.n;
   p.k = a.k;
   p.out_f32 = a.out_kind == kOutF32;
+  if (a.error_flag && a.nonfinite_bit) {
+    p.err = a.error_flag;
+    p.nonfinite_or = a.nonfinite_bit;
+  }
   return launch_gemv<kWBf16>(p, a.stream);
 }
 

@@ -129,6 +129,10 @@ struct Bf16GemmArgs {
   hipStream_t stream = nullptr;
   uint32_t m = 0, n = 0, k = 0;
   OutKind out_kind = kOutBf16;
+  // optional: a non-finite output is stored and ORs nonfinite_bit into
+  // *error_flag (the DeepSeek LM head's bit 128)
+  uint32_t* error_flag = nullptr;
+  uint32_t nonfinite_bit = 0;
 };
 St LaunchBf16Gemm(const Bf16GemmArgs& a);
 uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
@@ -301,5 +305,17 @@ struct Mxfp4DecodeArgs {
   uint32_t rows = 0, k = 0;
 };
 St LaunchMxfp4Decode(const Mxfp4DecodeArgs& a);
+
+// Sets set_bit in *error_flag when a bf16 element of x or w is non-finite,
+// scanning only when trigger_bit is already set (elementwise.hip).
+struct NonfiniteScanArgs {
+  const uint16_t* x = nullptr;
+  const uint16_t* w = nullptr;
+  uint64_t x_elems = 0, w_elems = 0;  // multiples of 8, 16-byte aligned pointers
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t trigger_bit = 0, set_bit = 0;
+};
+St LaunchNonfiniteScan(const NonfiniteScanArgs& a);
 
 }  // namespace pih_amd

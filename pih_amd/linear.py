@@ -225,6 +225,48 @@ class QwenMlpBlock:
         return bf16_gemm(self.h, self.wd, out=self.out)
 
 
+QWEN_VOCAB, QWEN_HIDDEN = 151936, 1024
+
+
+class QwenLmHead:
+    """The Qwen3-0.6B LM head as the reference's INT4 execution driver runs
+    it (plugins/model-qwen3/nvidia_qwen3_int4_execution_driver.cpp:16-67): a
+    bank of GemmPlans for 1..maximum_rows rows (at most 32) over the tied
+    [151936, 1024] bf16 weight with fp32 logits; ``execute`` rejects a row
+    count outside the bank.  Here every row count is the same
+    ``launch_bf16_gemm`` call (the weight-streaming GEMV, no workspace)."""
+
+    def __init__(self, maximum_rows: int):
+        if not 1 <= maximum_rows <= 32:
+            raise ValueError("NVIDIA Qwen INT4 workspace identity is invalid")
+        self.maximum_rows = maximum_rows
+
+    def execute(self, x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        if x.dim() != 2 or x.shape[0] == 0 or x.shape[0] > self.maximum_rows:
+            raise ValueError("NVIDIA Qwen INT4 LM head row count is invalid")
+        if tuple(weight.shape) != (QWEN_VOCAB, QWEN_HIDDEN) or x.shape[1] != QWEN_HIDDEN:
+            raise ValueError("Qwen LM head shape is invalid")
+        return bf16_gemm(x, weight, abi.OUTPUT_F32, out=out)
+
+
+def deepseek_lm_head(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None,
+                     flag: Optional[torch.Tensor] = None):
+    """logits f32 [rows, 129280] through the DeepSeek table's
+    ``launch_lm_head`` (plugins/kernels/deepseek-v4-sm89/native/
+    deepseek_endpoint.cu:94-115,484-497): bit 128 of the flag for a
+    non-finite logit, bit 64 for a non-finite x or W element."""
+    rows, hidden = x.shape
+    vocab = weight.shape[0]
+    if out is None:
+        out = torch.empty(rows, vocab, dtype=torch.float32, device=x.device)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.DS["lm_head"], input_bf16=ptr(x), weight_bf16=ptr(weight), logits_f32=ptr(out),
+                    error_flag_u32=ptr(flag), stream=stream_handle(), output_rows=rows, vocab_size=vocab,
+                    hidden_size=hidden)
+    _check(abi.deepseek_pack().call("launch_lm_head", r), "lm_head")
+    return out, flag
+
+
 class MoeFp8Layer:
     """The BASELINE FP8 MoE expert layer on device, one launch per stage:
     route plan -> FP8 quant of the token rows -> grouped gate/up GEMM with

@@ -609,6 +609,54 @@ def test_moe_fp8_forward_matches_token_major_composition():
     np.testing.assert_array_equal(got, want)
 
 
+# ------------------------------------------------------------ LM head
+def _bf(values):
+    return (np.asarray(values, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_lm_head_integer_brute_force():
+    """Small-integer operands: every order of the fp32 sum is exact, so the
+    logits equal the float64 product x . W^T (pins row/word indexing and
+    the transposed weight)."""
+    rng = np.random.default_rng(41)
+    x = rng.integers(-6, 7, (3, 4096))
+    w = rng.integers(-6, 7, (29, 4096))
+    got, err = oracle.lm_head(_bf(x), _bf(w))
+    assert err == 0
+    np.testing.assert_array_equal(got, (x.astype(np.float64) @ w.T.astype(np.float64)).astype(np.float32))
+
+
+def test_lm_head_reference_reduction_order():
+    """x = 1 at h = 0..254 and 2^24 at h = 255, W = 1.  In the reference's
+    block order (thread t holds h = t; tree halving 128 .. 1) the first level
+    adds 1 to 2^24, which rounds to even and loses it; every later level adds
+    an even partial sum exactly: 2^24 + 2 + 4 + ... + 128 = 2^24 + 254.  A
+    sequential sum would give 2^24 + 256 and the exact value is 2^24 + 255."""
+    x = np.zeros((1, 4096), np.float32)
+    x[0, :255] = 1.0
+    x[0, 255] = 2.0 ** 24
+    w = np.ones((2, 4096), np.float32)
+    got, err = oracle.lm_head(_bf(x), _bf(w))
+    assert err == 0
+    assert got[0, 0] == 2.0 ** 24 + 254 and got[0, 1] == 2.0 ** 24 + 254
+
+
+def test_lm_head_error_bits():
+    rng = np.random.default_rng(42)
+    x = _bf(rng.integers(-3, 4, (2, 4096)))
+    w = _bf(rng.integers(-3, 4, (5, 4096)))
+    w_inf = w.copy()
+    w_inf[3, 1000] = 0x7F80  # +inf in one weight row: that word's logits, bits 64 | 128
+    got, err = oracle.lm_head(x, w_inf)
+    assert err == 64 | 128
+    assert not np.isfinite(got[:, 3]).any() and np.isfinite(np.delete(got, 3, axis=1)).all()
+    # finite operands whose products overflow fp32: bit 128 only
+    xo = _bf(np.full((1, 4096), 2.0 ** 70, np.float32))
+    wo = _bf(np.full((1, 4096), 2.0 ** 70, np.float32))
+    got, err = oracle.lm_head(xo, wo)
+    assert err == 128 and np.isinf(got[0, 0])
+
+
 # --------------------------------------------- live reference (optional)
 @pytest.mark.skipif(not os.path.exists(oracle._REF_PATH),
                     reason="oracle/_ref not built (needs the reference checkout)")

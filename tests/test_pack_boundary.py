@@ -132,7 +132,7 @@ def test_header_validation(pack, entry, rtype):
 
 
 HOT_DS = {"fp8_activation_quant", "fp8_gemm", "grouped_fp8_gemm", "route_gather", "fp4_gemm", "expert_swiglu",
-          "expert_accumulate", "router_gemm", "shared_swiglu", "expert_finalize"}
+          "expert_accumulate", "router_gemm", "shared_swiglu", "expert_finalize", "lm_head"}
 
 
 @pytest.mark.parametrize("name", [n for n in abi.DS_ORDER if n not in HOT_DS])
