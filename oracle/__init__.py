@@ -100,6 +100,10 @@ def ref() -> Optional[C.CDLL]:
             "pr_routed_expert": (C.c_int, [P, P, U32, U32, U32, P, P, P, P, P, P, P]),
             "pr_int4_quantize": (C.c_int, [P, U64, U64, P, P]),
             "pr_learned_router": (C.c_int, [P, U32, P, P, P]),
+            "pr_qwen_int4_metadata": (C.c_int, [P, P, P, P]),
+            "pr_qwen_int4_parse": (C.c_int, [P]),
+            "pr_v41_fp4_block_to_fp8": (C.c_int, [P, P, P, P]),
+            "pr_v41_dequant_block": (C.c_int, [P, F32, U32, P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(R, name)

@@ -24,7 +24,11 @@
 #include "pih/model/deepseek_mxfp4_codec.h"
 #include "pih/model/deepseek_routed_expert_oracle.h"
 #include "pih/model/qwen3_cpu_oracle.h"
+#include "pih/model/qwen3_int4_artifact_layout.h"
+#include "pih/model/qwen3_int4_artifact_metadata.h"
 #include "qwen3_int4_reference_quantizer.h"
+#include "weight_dequantize.h"
+#include "weight_expert_convert.h"
 
 using namespace pih;
 
@@ -221,6 +225,62 @@ int pr_learned_router(const float* raw, uint32_t token_count, const float* bias,
     ids[at] = r.expert_id;
     weights[at] = r.weight;
   }
+  return 0;
+}
+
+// Qwen INT4 XINGW4A1 metadata region (1 MiB) serialised by the reference for
+// the official layout, the given roots (3 x 32 bytes) and payload digests
+// (32 bytes per payload record, in the layout's record order, aliases
+// skipped).  Writes the region to out (1 MiB) and the encoded length.
+int pr_qwen_int4_metadata(const uint8_t* roots, const uint8_t* digests, uint8_t* out, uint32_t* encoded) {
+  auto layout = QwenInt4ArtifactLayout::CreateOfficialPureW4();
+  if (!layout.ok()) return 1;
+  QwenInt4ArtifactRoots r;
+  std::memcpy(r.source_artifact.bytes.data(), roots, 32);
+  std::memcpy(r.source_binding.bytes.data(), roots + 32, 32);
+  std::memcpy(r.disposition.bytes.data(), roots + 64, 32);
+  std::vector<QwenInt4PayloadDigest> list;
+  std::size_t i = 0;
+  for (const auto& rec : layout->records()) {
+    if (rec.kind == QwenInt4ArtifactRecordKind::kAlias) continue;
+    QwenInt4PayloadDigest d;
+    d.identity = rec.identity;
+    std::memcpy(d.sha256.bytes.data(), digests + 32 * i++, 32);
+    list.push_back(std::move(d));
+  }
+  auto meta = QwenInt4ArtifactMetadata::Create(*layout, r, std::move(list));
+  if (!meta.ok()) return 1;
+  auto region = meta->serialize_fixed_region();
+  if (!region.ok()) return 1;
+  std::memcpy(out, region->data(), region->size());
+  *encoded = static_cast<uint32_t>(meta->encoded_bytes());
+  return 0;
+}
+
+// ParseAndVerify of a 1 MiB metadata region against the official layout.
+int pr_qwen_int4_parse(const uint8_t* region) {
+  auto layout = QwenInt4ArtifactLayout::CreateOfficialPureW4();
+  if (!layout.ok()) return 2;
+  auto meta = QwenInt4ArtifactMetadata::ParseAndVerify(bytes(region, QwenInt4ArtifactLayout::kMetadataBytes), *layout);
+  return meta.ok() ? 0 : 1;
+}
+
+// V4.1 expert FP4 -> FP8 32x32 block conversion (weight_expert_convert.cpp).
+int pr_v41_fp4_block_to_fp8(const uint8_t* packed, const uint8_t* scales, uint8_t* weight, uint8_t* scale) {
+  auto block = deepseek_v41::ConvertExpertFp4Block(bytes(packed, 512), bytes(scales, 32));
+  if (!block.ok()) return 1;
+  std::memcpy(weight, block->weight.data(), 1024);
+  *scale = std::to_integer<uint8_t>(block->scale);
+  return 0;
+}
+
+// V4.1 wo_a block dequantisation E4M3FN x scale -> bf16 (weight_dequantize.cpp).
+int pr_v41_dequant_block(const uint8_t* source, float scale, uint32_t block, uint16_t* out) {
+  std::vector<std::byte> dst(static_cast<std::size_t>(block) * block * 2U);
+  auto st = deepseek_v41::DequantizeWoABlock(bytes(source, static_cast<std::size_t>(block) * block), scale, block,
+                                             dst);
+  if (!st.ok()) return 1;
+  std::memcpy(out, dst.data(), dst.size());
   return 0;
 }
 

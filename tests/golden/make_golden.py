@@ -140,6 +140,45 @@ def main():
     assert R.pr_learned_router(_p(raw), rt, _p(bias), _p(rid), _p(rw)) == 0
     out.update(router_raw=raw, router_bias=bias, router_ids=rid, router_weights=rw)
 
+    # Qwen INT4 XINGW4A1 metadata region serialised by the reference for
+    # fixed roots and payload digests (the encoded prefix; the rest is zero)
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from artifact_files import golden_roots_and_digests  # noqa: E402
+
+    roots, digests = golden_roots_and_digests()
+    rb = np.frombuffer(roots, np.uint8).copy()
+    db = np.frombuffer(b"".join(digests), np.uint8).copy()
+    region = np.zeros(1 << 20, np.uint8)
+    enc = np.zeros(1, np.uint32)
+    assert R.pr_qwen_int4_metadata(_p(rb), _p(db), _p(region), _p(enc)) == 0
+    out["qwen_meta_region"] = region[:int(enc[0])].copy()
+
+    # V4.1 expert FP4 -> FP8 32x32 blocks: random codes with row scales in a
+    # narrow band, a band 12 wide (FP8 subnormals and flushes) and one with a
+    # maximum of exactly 6
+    blocks = 6
+    packed = synth.splitmix64(29, blocks * 512).astype(np.uint8).reshape(blocks, 512)
+    sc = np.empty((blocks, 32), np.uint8)
+    sc[0:2] = (120 + synth.splitmix64(30, 64) % np.uint64(4)).astype(np.uint8).reshape(2, 32)
+    sc[2:4] = (100 + synth.splitmix64(31, 64) % np.uint64(13)).astype(np.uint8).reshape(2, 32)
+    sc[4] = (synth.splitmix64(32, 32) % np.uint64(7)).astype(np.uint8)
+    sc[4, 0] = 6
+    sc[5] = 127
+    wq = np.empty((blocks, 1024), np.uint8)
+    ws = np.empty(blocks, np.uint8)
+    for b in range(blocks):
+        assert R.pr_v41_fp4_block_to_fp8(_p(packed[b]), _p(sc[b]), _p(wq[b]), _p(ws[b:b + 1])) == 0
+    out.update(v41_fp4_packed=packed, v41_fp4_scales=sc, v41_fp8_weight=wq, v41_fp8_scale=ws)
+
+    # V4.1 wo_a block dequantisation (E4M3FN x fp32 scale -> bf16), 32 and 128
+    for blk, seed, scale in ((32, 33, 0.0078125 * 1.3), (128, 34, 3.75e-3)):
+        src = synth.splitmix64(seed, blk * blk).astype(np.uint8)
+        src[(src & 0x7F) == 0x7F] = 0x3C
+        dq = np.empty(blk * blk, np.uint16)
+        assert R.pr_v41_dequant_block(_p(src), float(np.float32(scale)), blk, _p(dq)) == 0
+        out[f"v41_woa{blk}_src"], out[f"v41_woa{blk}_scale"], out[f"v41_woa{blk}_bf16"] = (
+            src, np.array([scale], np.float32), dq)
+
     path = os.path.join(HERE, "ref_vectors.npz")
     np.savez_compressed(path, **out)
     print(f"wrote {path} ({os.path.getsize(path)} bytes, {len(out)} arrays)")
