@@ -58,7 +58,18 @@
  *                          (plugins/model-deepseek-v4-flash/
  *                          deepseek_learned_router.cpp:21-94) on the device,
  *                          plus BASELINE's softmax top-k, so router scores
- *                          never travel to the host.
+ *                          never travel to the host;
+ *   launch_v41_linear      the DeepSeek V4.1 FP8 and mixed FP8/FP4 linears
+ *                          (plugins/model-deepseek-v41/linear_fp8.cu:
+ *                          82-105, validators linear_fp8.cpp:14-32,
+ *                          linear_fp4.cpp:13-29): per-32 activation quant,
+ *                          then the 32-block-scaled GEMM on MX MFMAs;
+ *   launch_v41_fp4_to_fp8  the V4.1 expert FP4 -> FP8 32x32 conversion
+ *                          (weight_expert_convert.cpp:33-100) on the device;
+ *   launch_v41_block_dequant
+ *                          the V4.1 wo_a e4m3 x block-scale -> bf16
+ *                          dequantisation (weight_dequantize.cpp:17-50,
+ *                          DequantizeWoATensor) on the device.
  *
  * Conventions are those of the reference's pack tables: one request pointer
  * in, pih_status_v1 by value out; a NULL request, wrong struct_size or wrong
@@ -321,6 +332,66 @@ typedef struct pih_amd_router_topk_launch_v1 {
   float route_scale;
 } pih_amd_router_topk_launch_v1;
 
+/* DeepSeek V4.1 linear: out bf16 [rows, N] = quant32(input bf16 [rows, K])
+ * . W^T.  weight_format 1: W e4m3 [N, K] + UE8M0 [N/32, K/32] (one per 32x32
+ * block); 2: W e2m1 [N, K/2] (even k in the low nibble) + UE8M0 [N, K/32].
+ * quantized_e4m3 [rows, K] and activation_scales UE8M0 [rows, K/32] are
+ * caller scratch the entry writes (the per-32 quant of the reference's
+ * Quantize kernel).  Every region carries its byte count, which must equal
+ * the layout's (the reference's Valid: non-zero, aligned, exact size), and
+ * no written region may overlap another region.  1 <= rows <= 4096,
+ * K and N in [1, 32768] and multiples of 32 (the reference's bounds); this
+ * pack also needs K and N multiples of 128 (every V4.1 projection is) and
+ * answers INVALID_ARGUMENT otherwise.  Error bits: 1 a non-finite input, a
+ * NaN code or a 255 scale; 2 a non-finite result (stored, as the reference
+ * stores it). */
+#define PIH_AMD_V41_WEIGHT_FP8_BLOCK32_V1 1U
+#define PIH_AMD_V41_WEIGHT_MXFP4_V1 2U
+typedef struct pih_amd_v41_linear_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t input_bf16;
+  uint64_t input_bytes;
+  uintptr_t weight;
+  uint64_t weight_bytes;
+  uintptr_t weight_scales;
+  uint64_t weight_scale_bytes;
+  uintptr_t quantized_e4m3;
+  uint64_t quantized_bytes;
+  uintptr_t activation_scales;
+  uint64_t activation_scale_bytes;
+  uintptr_t output_bf16;
+  uint64_t output_bytes;
+  uintptr_t error_flag_u32;
+  uint64_t error_flag_bytes;
+  uintptr_t stream;
+  uint32_t rows, in_features, out_features, weight_format;
+} pih_amd_v41_linear_launch_v1;
+
+/* V4.1 expert FP4 -> FP8 32x32: packed e2m1 [rows, cols/2] + UE8M0 [rows,
+ * cols/32] -> e4m3 [rows, cols] + UE8M0 [rows/32, cols/32]; rows and cols
+ * multiples of 32.  Error bits: 1 a NaN (255) row scale, 2 a block whose
+ * largest row scale is below 6 (shared scale under the E8M0 range); such
+ * blocks are left unwritten and the whole output must be discarded, as the
+ * reference rejects the tensor. */
+typedef struct pih_amd_v41_fp4_to_fp8_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t packed, scales, weight_e4m3, weight_scales, error_flag_u32, stream;
+  uint32_t rows, columns;
+} pih_amd_v41_fp4_to_fp8_launch_v1;
+
+/* V4.1 block dequantisation: e4m3 [rows, columns] x one scale per square
+ * block (block 32 or 128; scale_storage 1: UE8M0 bytes, 0 meaning 2^-127;
+ * 2: fp32) -> bf16, fp32 product rounded to nearest even.  Error bits: 1 a
+ * NaN code, 2 a 255 / non-finite / non-positive scale, 4 a non-finite
+ * product or bf16; those elements are left unwritten. */
+#define PIH_AMD_V41_SCALE_E8M0_V1 1U
+#define PIH_AMD_V41_SCALE_F32_V1 2U
+typedef struct pih_amd_v41_block_dequant_launch_v1 {
+  uint32_t struct_size, abi_version;
+  uintptr_t source_e4m3, scales, output_bf16, error_flag_u32, stream;
+  uint32_t rows, columns, block, scale_storage;
+} pih_amd_v41_block_dequant_launch_v1;
+
 typedef struct pih_amd_linear_kernels_api_v1 {
   uint32_t struct_size;
   uint32_t contract_version;
@@ -359,6 +430,10 @@ typedef struct pih_amd_linear_kernels_api_v1 {
    * DeepSeekLearnedRouter::Route (deepseek_learned_router.cpp:84-94) and the
    * scores D2H before it. */
   pih_status_v1 (*launch_router_topk)(const pih_amd_router_topk_launch_v1*);
+  /* DeepSeek V4.1 32-block formats (the three structs above). */
+  pih_status_v1 (*launch_v41_linear)(const pih_amd_v41_linear_launch_v1*);
+  pih_status_v1 (*launch_v41_fp4_to_fp8)(const pih_amd_v41_fp4_to_fp8_launch_v1*);
+  pih_status_v1 (*launch_v41_block_dequant)(const pih_amd_v41_block_dequant_launch_v1*);
 } pih_amd_linear_kernels_api_v1;
 
 #define PIH_AMD_ROUTE_PLAN_NOALLOC_MAX_SCRATCH_V1 (1ULL << 20)

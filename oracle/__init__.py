@@ -61,6 +61,11 @@ def lib() -> C.CDLL:
             "po_w4a16_asym_dequant": (C.c_int, [P, P, P, U32, U32, P]),
             "po_bf16_gemm": (None, [P, P, U32, U32, U32, P]),
             "po_lm_head": (U32, [P, P, U32, U32, U32, P]),
+            "po_v41_fp4_block_to_fp8": (C.c_int, [P, P, P, P]),
+            "po_v41_fp4_to_fp8": (C.c_int, [P, P, U32, U32, P, P]),
+            "po_v41_dequant_block": (C.c_int, [P, F32, U32, P]),
+            "po_v41_quant32": (U32, [P, U32, U32, P, P]),
+            "po_v41_linear": (U32, [P, P, P, P, U32, U32, U32, C.c_int, P]),
             "po_silu_mul": (None, [P, P, C.c_size_t, P]),
             "po_swiglu": (C.c_int, [P, P, C.c_size_t, F32, P]),
             "po_route_plan": (C.c_int, [P, P, U32, U32, U32, P, P, P, P]),
@@ -269,6 +274,52 @@ def lm_head(x_bits, w_bits):
     out = np.empty((rows, vocab), np.float32)
     err = lib().po_lm_head(_ptr(np.ascontiguousarray(x_bits)), _ptr(np.ascontiguousarray(w_bits)), rows, vocab,
                            hidden, _ptr(out))
+    return out, int(err)
+
+
+# ------------------------------------------------ DeepSeek V4.1 32-blocks
+def v41_fp4_block_to_fp8(packed, scales):
+    """One 32x32 block: (e4m3 [32, 32], shared UE8M0, status code)."""
+    w = np.empty(1024, np.uint8)
+    s = np.zeros(1, np.uint8)
+    st = lib().po_v41_fp4_block_to_fp8(_ptr(np.ascontiguousarray(packed, np.uint8)),
+                                       _ptr(np.ascontiguousarray(scales, np.uint8)), _ptr(w), _ptr(s))
+    return w.reshape(32, 32), int(s[0]), int(st)
+
+
+def v41_fp4_to_fp8(packed, scales):
+    rows, half = packed.shape
+    cols = half * 2
+    w = np.empty((rows, cols), np.uint8)
+    s = np.empty((rows // 32, cols // 32), np.uint8)
+    _check("po_v41_fp4_to_fp8", lib().po_v41_fp4_to_fp8(_ptr(np.ascontiguousarray(packed)),
+                                                        _ptr(np.ascontiguousarray(scales)), rows, cols, _ptr(w),
+                                                        _ptr(s)))
+    return w, s
+
+
+def v41_dequant_block(src, scale, block):
+    out = np.empty(block * block, np.uint16)
+    st = lib().po_v41_dequant_block(_ptr(np.ascontiguousarray(src, np.uint8)), float(np.float32(scale)), block,
+                                    _ptr(out))
+    return out, int(st)
+
+
+def v41_quant32(x_bits):
+    rows, k = x_bits.shape
+    codes = np.empty((rows, k), np.uint8)
+    scales = np.empty((rows, k // 32), np.uint8)
+    err = lib().po_v41_quant32(_ptr(np.ascontiguousarray(x_bits)), rows, k, _ptr(codes), _ptr(scales))
+    return codes, scales, int(err)
+
+
+def v41_linear(a, sa, w, sw, n, fp4):
+    """bf16 [rows, n] and error bits of the V4.1 projection."""
+    rows, k = a.shape
+    out = np.empty((rows, n), np.uint16)
+    err = lib().po_v41_linear(_ptr(np.ascontiguousarray(a)), _ptr(np.ascontiguousarray(sa)),
+                              _ptr(np.ascontiguousarray(w)), _ptr(np.ascontiguousarray(sw)), rows, n, k,
+                              1 if fp4 else 0, _ptr(out))
     return out, int(err)
 
 

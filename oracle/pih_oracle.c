@@ -449,6 +449,146 @@ uint32_t po_lm_head(const uint16_t* x, const uint16_t* w, uint32_t rows, uint32_
   return err;
 }
 
+/* ------------------------------------------ DeepSeek V4.1 32-block formats */
+/* Expert FP4 32x32 block -> FP8 e4m3 + shared UE8M0
+ * (plugins/model-deepseek-v41/weight_expert_convert.cpp:33-63): shared =
+ * max(row scale) - 6 (NaN scale 255: code 1; max < 6: code 2); value =
+ * e2m1 magnitude * 2^(row - max + 6) rounded to the nearest e4m3 code, ties
+ * to the even code; both zero codes give +0, other negatives keep the sign
+ * (also when they round to zero).  Below 2^-30 every magnitude rounds to 0;
+ * above it the float product is exact, so po_e4m3_encode applies. */
+int po_v41_fp4_block_to_fp8(const uint8_t* packed, const uint8_t* scales, uint8_t* weight, uint8_t* scale) {
+  static const float mags[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+  unsigned maximum = 0;
+  for (int r = 0; r < 32; ++r) {
+    if (scales[r] == 255) return 1;
+    if (scales[r] > maximum) maximum = scales[r];
+  }
+  if (maximum < 6) return 2;
+  *scale = (uint8_t)(maximum - 6);
+  for (int r = 0; r < 32; ++r) {
+    const int shift = (int)scales[r] - (int)maximum + 6;
+    for (int c = 0; c < 32; ++c) {
+      const unsigned nib = (packed[r * 16 + c / 2] >> ((c & 1) * 4)) & 15u;
+      const unsigned mag = nib & 7u;
+      uint8_t code = 0;
+      if (mag && shift >= -30) po_e4m3_encode(ldexpf(mags[mag], shift), &code);
+      if ((nib & 8u) && mag) code |= 0x80u;
+      weight[r * 32 + c] = code;
+    }
+  }
+  return 0;
+}
+
+/* The tensor form (ConvertExpertFp4Tensor, :64-100): packed [rows, cols/2],
+ * scales [rows, cols/32] -> e4m3 [rows, cols], UE8M0 [rows/32, cols/32];
+ * returns the first failing block's code. */
+int po_v41_fp4_to_fp8(const uint8_t* packed, const uint8_t* scales, uint32_t rows, uint32_t cols, uint8_t* weight,
+                      uint8_t* out_scales) {
+  uint8_t blk_packed[512], blk_scales[32], blk_out[1024];
+  for (uint32_t r0 = 0; r0 < rows; r0 += 32)
+    for (uint32_t g = 0; g < cols / 32; ++g) {
+      for (uint32_t r = 0; r < 32; ++r) {
+        memcpy(blk_packed + r * 16, packed + (size_t)(r0 + r) * (cols / 2) + g * 16, 16);
+        blk_scales[r] = scales[(size_t)(r0 + r) * (cols / 32) + g];
+      }
+      const int st = po_v41_fp4_block_to_fp8(blk_packed, blk_scales, blk_out, &out_scales[(size_t)(r0 / 32) * (cols / 32) + g]);
+      if (st) return st;
+      for (uint32_t r = 0; r < 32; ++r) memcpy(weight + (size_t)(r0 + r) * cols + g * 32, blk_out + r * 32, 32);
+    }
+  return 0;
+}
+
+/* wo_a block dequantisation (weight_dequantize.cpp:24-50): e4m3 x scale in
+ * fp32, bf16 round to nearest even.  Codes: 1 scale not finite and > 0,
+ * 2 NaN source code, 3 non-finite fp32 product, 4 bf16 overflow. */
+int po_v41_dequant_block(const uint8_t* src, float scale, uint32_t block, uint16_t* out) {
+  if ((block != 32 && block != 128) || !isfinite(scale) || scale <= 0.0f) return 1;
+  po_tables();
+  for (uint32_t i = 0; i < block * block; ++i) {
+    if (g_e4m3_nan[src[i]]) return 2;
+    const float v = g_e4m3[src[i]] * scale;
+    if (!isfinite(v)) return 3;
+    const uint16_t h = po_bf16_from_f32(v);
+    if (!isfinite(po_bf16_to_f32(h))) return 4;
+    out[i] = h;
+  }
+  return 0;
+}
+
+/* The V4.1 linear's activation quant (plugins/model-deepseek-v41/
+ * linear_fp8.cu:18-34), per (row, 32 k): amax of the finite values, floor
+ * 1e-4, times the fp32 constant 1/448; the exponent of that product, plus
+ * one unless it is a power of two, is the scale 2^e (byte e + 127); codes
+ * are clamp(x / 2^e, +-448) rounded to nearest even, non-finite inputs
+ * encode 0 and raise bit 1. */
+uint32_t po_v41_quant32(const uint16_t* x, uint32_t rows, uint32_t k, uint8_t* codes, uint8_t* scales) {
+  uint32_t err = 0;
+  for (size_t g = 0; g < (size_t)rows * (k / 32); ++g) {
+    float maximum = 0.0f;
+    for (int l = 0; l < 32; ++l) {
+      const float v = po_bf16_to_f32(x[g * 32 + l]);
+      if (!isfinite(v)) err |= 1u;
+      else maximum = fmaxf(maximum, fabsf(v));
+    }
+    const float scaled = fmaxf(maximum, 1e-4f) * (1.0f / 448.0f);
+    const uint32_t bits = f2u(scaled);
+    const int e = (int)((bits >> 23) & 255u) - 127 + ((bits & 0x7fffffu) != 0u);
+    scales[g] = (uint8_t)(e + 127);
+    const float scale = ldexpf(1.0f, e);
+    for (int l = 0; l < 32; ++l) {
+      const float v = po_bf16_to_f32(x[g * 32 + l]);
+      const float q = isfinite(v) ? fminf(fmaxf(v / scale, -448.0f), 448.0f) : 0.0f;
+      po_e4m3_encode(q, &codes[g * 32 + l]);
+    }
+  }
+  return err;
+}
+
+/* The V4.1 projection (linear_fp8.cu:39-76): per 32-deep group a sequential
+ * fp32 dot of the decoded operands, term = (dot * 2^(sa-127)) * 2^(sb-127),
+ * accumulated in group order; bf16 out.  sb is the 32x32 block's scale
+ * (fp4 = 0) or the weight row's per-32 scale (fp4 = 1, e2m1 weights, even
+ * k in the low nibble).  Bits: 1 a NaN operand or a 255 scale, 2 a
+ * non-finite term, accumulator or bf16 output. */
+uint32_t po_v41_linear(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint32_t rows,
+                       uint32_t n, uint32_t k, int fp4, uint16_t* out) {
+  po_tables();
+  uint32_t err = 0;
+  const uint32_t groups = k / 32;
+  PO_PARALLEL_FOR_REDUCE_OR(err)
+  for (int64_t idx = 0; idx < (int64_t)rows * n; ++idx) {
+    const uint32_t t = (uint32_t)(idx / n), col = (uint32_t)(idx % n);
+    float acc = 0.0f;
+    for (uint32_t g = 0; g < groups; ++g) {
+      float dot = 0.0f;
+      for (uint32_t i = 0; i < 32; ++i) {
+        const uint8_t ac = a[(size_t)t * k + g * 32 + i];
+        float av = g_e4m3_nan[ac] ? NAN : g_e4m3[ac], bv;
+        if (fp4) {
+          const uint8_t byte = w[(size_t)col * (k / 2) + g * 16 + i / 2];
+          bv = g_e2m1[(byte >> ((i & 1) * 4)) & 15u];
+        } else {
+          const uint8_t wc = w[(size_t)col * k + g * 32 + i];
+          bv = g_e4m3_nan[wc] ? NAN : g_e4m3[wc];
+        }
+        if (!isfinite(av) || !isfinite(bv)) err |= 1u;
+        dot += av * bv;
+      }
+      const uint8_t sab = sa[(size_t)t * groups + g];
+      const uint8_t sbb = sw[(size_t)(fp4 ? col : col / 32) * groups + g];
+      if (sab == 255 || sbb == 255) err |= 1u;
+      const float term = (dot * ldexpf(1.0f, (int)sab - 127)) * ldexpf(1.0f, (int)sbb - 127);
+      acc += term;
+      if (!isfinite(term) || !isfinite(acc)) err |= 2u;
+    }
+    const uint16_t h = po_bf16_from_f32(acc);
+    if (!isfinite(po_bf16_to_f32(h))) err |= 2u;
+    out[idx] = h;
+  }
+  return err;
+}
+
 /* ------------------------------------------------------------ elementwise */
 void po_silu_mul(const uint16_t* gate, const uint16_t* up, size_t count,
                  uint16_t* out) {

@@ -129,6 +129,14 @@ int po_w4a16_asym_dequant(const uint32_t* qweight, const uint16_t* scales_bf16,
 /* DeepSeek LM head in the reference's reduction order; returns error bits 64/128. */
 uint32_t po_lm_head(const uint16_t* x, const uint16_t* w, uint32_t rows, uint32_t vocab,
                     uint32_t hidden, float* logits);
+/* DeepSeek V4.1 32-block formats (weight_expert_convert.cpp, weight_dequantize.cpp, linear_fp8.cu). */
+int po_v41_fp4_block_to_fp8(const uint8_t* packed, const uint8_t* scales, uint8_t* weight, uint8_t* scale);
+int po_v41_fp4_to_fp8(const uint8_t* packed, const uint8_t* scales, uint32_t rows, uint32_t cols, uint8_t* weight,
+                      uint8_t* out_scales);
+int po_v41_dequant_block(const uint8_t* src, float scale, uint32_t block, uint16_t* out);
+uint32_t po_v41_quant32(const uint16_t* x, uint32_t rows, uint32_t k, uint8_t* codes, uint8_t* scales);
+uint32_t po_v41_linear(const uint8_t* a, const uint8_t* sa, const uint8_t* w, const uint8_t* sw, uint32_t rows,
+                       uint32_t n, uint32_t k, int fp4, uint16_t* out);
 void po_bf16_gemm(const uint16_t* a, const uint16_t* w, uint32_t m, uint32_t n,
                   uint32_t k, float* out);
 

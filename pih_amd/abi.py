@@ -209,6 +209,20 @@ LN["router_topk"] = _struct("RouterTopk", _hdr(*_u("scores_f32", "bias_f32", "to
                                                     "error_flag_u32", "stream"),
                                                 *_i("token_count", "expert_count", "top_k", "mode"),
                                                 ("route_scale", C.c_float)))
+_V41_BYTES = {"input_bf16": "input_bytes", "weight": "weight_bytes", "weight_scales": "weight_scale_bytes",
+              "quantized_e4m3": "quantized_bytes", "activation_scales": "activation_scale_bytes",
+              "output_bf16": "output_bytes", "error_flag_u32": "error_flag_bytes"}
+LN["v41_linear"] = _struct("V41Linear", _hdr(
+    *[f for name in ("input_bf16", "weight", "weight_scales", "quantized_e4m3", "activation_scales", "output_bf16",
+                     "error_flag_u32") for f in ((name, UPTR), (_V41_BYTES[name], U64))],
+    ("stream", UPTR), *_i("rows", "in_features", "out_features", "weight_format")))
+LN["v41_fp4_to_fp8"] = _struct("V41Fp4ToFp8", _hdr(*_u("packed", "scales", "weight_e4m3", "weight_scales",
+                                                        "error_flag_u32", "stream"), *_i("rows", "columns")))
+LN["v41_block_dequant"] = _struct("V41BlockDequant", _hdr(*_u("source_e4m3", "scales", "output_bf16",
+                                                              "error_flag_u32", "stream"),
+                                                          *_i("rows", "columns", "block", "scale_storage")))
+V41_WEIGHT_FP8_BLOCK32, V41_WEIGHT_MXFP4 = 1, 2
+V41_SCALE_E8M0, V41_SCALE_F32 = 1, 2
 LN["silu_mul"] = _struct("SiluMul", _hdr(*_u("gate_bf16", "up_bf16", "output_bf16", "stream"), ("count", U64)))
 LN["swiglu"] = _struct("SwiGlu", _hdr(*_u("gate_bf16", "up_bf16", "route_weights_f32", "output_bf16",
                                           "error_flag_u32", "stream"), *_i("rows", "cols"), ("limit", F32)))
@@ -238,7 +252,8 @@ LN_ORDER = [("query_workspace", "workspace_query"), ("launch_route_plan", "route
             ("launch_mxfp4_decode", "mxfp4_decode"), ("launch_w4a16_dequant", "w4a16_dequant"),
             ("launch_w4a16_grouped", "w4a16_grouped"), ("query_moe_layer_workspace", "moe_layer"),
             ("launch_moe_layer", "moe_layer"), ("launch_route_plan_noalloc", "route_plan"),
-            ("launch_router_topk", "router_topk")]
+            ("launch_router_topk", "router_topk"), ("launch_v41_linear", "v41_linear"),
+            ("launch_v41_fp4_to_fp8", "v41_fp4_to_fp8"), ("launch_v41_block_dequant", "v41_block_dequant")]
 LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_version", U32),
                                          ("identity", C.POINTER(Identity))] +
                  [(f, C.CFUNCTYPE(Status, C.POINTER(LN[s]))) for f, s in LN_ORDER])

@@ -23,6 +23,15 @@
 //   kBf16Fp4 A bf16; W MXFP4 dequantised exactly into bf16 in registers
 //            (every e2m1 value times 2^(s-127) is a bf16 number; one
 //            v_cvt_scalef32_pk_bf16_fp4 per byte), then bf16 MFMAs.
+//   kMx8     A e4m3 + UE8M0 per (row, 32 k); W e4m3 + UE8M0 per (32 rows,
+//            32 k): the DeepSeek V4.1 FP8 linear
+//            (plugins/model-deepseek-v41/linear_fp8.cu:39-76), on the MX
+//            instruction with both operands in the FP8 lane map (lane group g
+//            holds k [16g, 16g+16) and [64+16g, 64+16g+16)) and each lane
+//            group's scale byte covering k block g of the step (measured on
+//            gfx950: lane group g's scale applies to k [32g, 32g+32)).
+//   kMx4     as kMx8 with W e2m1 + UE8M0 per (row, 32 k) (the V4.1 mixed
+//            FP8/FP4 linear).
 //
 // Tiling: 256 threads = 4 waves, block tile 128 A rows x 128 W rows, each
 // wave 64x64 = 4x4 MFMA 16x16 tiles.  Per K step A and W tiles go through
@@ -50,7 +59,7 @@
 namespace pih_amd {
 namespace {
 
-enum Kind : int { kFp8 = 0, kFp4 = 1, kBf16 = 2, kBf16Fp4 = 3 };
+enum Kind : int { kFp8 = 0, kFp4 = 1, kBf16 = 2, kBf16Fp4 = 3, kMx8 = 4, kMx4 = 5 };
 
 constexpr int BM = 128, BN = 128, THREADS = 256, A_STEP_BYTES = 128;
 constexpr int LDS_A = A_STEP_BYTES;
@@ -82,6 +91,14 @@ struct Traits<kBf16> {
 template <>
 struct Traits<kBf16Fp4> {
   static constexpr int K_STEP = 64, B_STEP_BYTES = 32, A_ELEM = 2;
+};
+template <>
+struct Traits<kMx8> {
+  static constexpr int K_STEP = 128, B_STEP_BYTES = 128, A_ELEM = 1;
+};
+template <>
+struct Traits<kMx4> {
+  static constexpr int K_STEP = 128, B_STEP_BYTES = 64, A_ELEM = 1;
 };
 
 struct GemmParams {
@@ -192,10 +209,13 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
   constexpr int LDS_B = lds_row_bytes<B_STEP>();
   constexpr int B_CPR = B_STEP / 16;             // 16-byte chunks per W row per step
   constexpr int B_LOADS = BN * B_CPR / THREADS;  // per thread
-  constexpr bool FP8A = KIND == kFp8 || KIND == kFp4;
-  constexpr bool BSCALE_ROW = KIND == kFp4 || KIND == kBf16Fp4;  // per-row MX scales
-  constexpr bool ASCALE = KIND == kFp8 || KIND == kFp4;
+  constexpr bool MX = KIND == kMx8 || KIND == kMx4;  // per-32 scales on both operands
+  constexpr bool FP8A = KIND == kFp8 || KIND == kFp4 || MX;
+  constexpr bool BSCALE_ROW = KIND == kFp4 || KIND == kBf16Fp4 || MX;  // per-row MX scales
+  constexpr bool ASCALE = KIND == kFp8 || KIND == kFp4 || MX;
   constexpr bool E8M0_A = (KIND == kFp8 && SCALE == kScaleUe8m0) || KIND == kFp4;
+  // FP8 lane map for A (and kMx8's W): chunks lg and lg + 4 of the step
+  constexpr bool LANE_MAP_MX = KIND == kFp4 || MX;
 
   __shared__ __align__(16) uint8_t sA[2][BM * LDS_A];
   __shared__ __align__(16) uint8_t sB[2][BN * LDS_B];
@@ -269,7 +289,10 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
   }
   // per-row MX scale words (kFp4: 4 bytes per 128-deep step; kBf16Fp4: 2)
   const uint8_t* ws_row = nullptr;
-  if constexpr (BSCALE_ROW)
+  if constexpr (KIND == kMx8)  // one scale row per 32 W rows
+    ws_row = static_cast<const uint8_t*>(p.w_scale) +
+             ((uint64_t)prob * (p.n / 32) + w_row(tid < BN ? tid : 0) / 32) * (K / 32);
+  else if constexpr (BSCALE_ROW)
     ws_row = static_cast<const uint8_t*>(p.w_scale) +
              ((uint64_t)prob * p.n + w_row(tid < BN ? tid : 0)) * (K / 32);
   // FP8 block scales (128-row blocks) used by this tile
@@ -287,7 +310,16 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
     for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const v4i*>(a_ptr[i] + (uint64_t)kb * A_STEP_BYTES);
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) rb[i] = *reinterpret_cast<const v4i*>(w_ptr[i] + (uint64_t)kb * B_STEP);
-    if constexpr (ASCALE) {
+    if constexpr (MX) {
+      // four per-32 scale bytes per row and step; a 255 (NaN) scale raises
+      // the error bit and propagates through the MFMA as the reference's
+      // 2^128 term does
+      rsa = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.a_scale) + s_src * (K / 32) +
+                                               (uint64_t)kb * 4);
+      if (ff_bytes(rsa) && tid < rows) bad |= kErrScale;
+      rsb = *reinterpret_cast<const uint32_t*>(ws_row + (uint64_t)kb * 4);
+      if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
+    } else if constexpr (ASCALE) {
       if constexpr (E8M0_A) {
         // a 0xFF scale raises the scale bit; its block then runs with
         // 2^-127, so it adds (almost) nothing, as the reference skips it
@@ -310,7 +342,25 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
       rsb = *reinterpret_cast<const uint16_t*>(ws_row + (uint64_t)kb * 2);
       if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
     }
-    if constexpr (CHECK && FP8A) {
+    if constexpr (CHECK && MX) {
+      // NaN codes raise the error bit and stay NaN (the V4.1 decode gives
+      // NaN, so the output is non-finite as well)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t |= e4m3_nan_bytes((uint32_t)ra[i][q]);
+        if (t && (tid >> 3) + 32 * i < rows) bad |= kErrCode;
+      }
+      if constexpr (KIND == kMx8) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) t |= e4m3_nan_bytes((uint32_t)rb[i][q]);
+        if (t) bad |= kErrCode;
+      }
+    } else if constexpr (CHECK && FP8A) {
       // NaN codes count as 0 in the sum (and raise the code bit), as the
       // reference decodes them
 #pragma unroll
@@ -399,7 +449,11 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
         if constexpr (KIND == kFp8 || KIND == kBf16) {  // chunks 2lg, 2lg + 1
           const uint32_t o = lds_at<128>(brow, 2 * lg);
           bv[ns] = cat8(*reinterpret_cast<const v4i*>(&sB[buf][o]), *reinterpret_cast<const v4i*>(&sB[buf][o ^ 16]));
-        } else if constexpr (KIND == kFp4) {
+        } else if constexpr (KIND == kMx8) {  // FP8 lane map: chunks lg, lg + 4
+          const uint32_t o = lds_at<128>(brow, lg);
+          bv[ns] = cat8(*reinterpret_cast<const v4i*>(&sB[buf][o]), *reinterpret_cast<const v4i*>(&sB[buf][o ^ 64]));
+          bsc[ns] = (sBs[buf][brow] >> (8 * lg)) & 0xffu;
+        } else if constexpr (KIND == kFp4 || KIND == kMx4) {
           bv[ns] = cat8(*reinterpret_cast<const v4i*>(&sB[buf][lds_at<64>(brow, lg)]), v4i{0, 0, 0, 0});
           bsc[ns] = (sBs[buf][brow] >> (8 * lg)) & 0xffu;
         } else {  // kBf16Fp4: 16 nibbles = k 16*lg .. 16*lg+15 of the step
@@ -418,9 +472,9 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
         // while an FP4 lane group g holds k [32g, 32g+32) contiguously
         // (measured on gfx950); same-format operands just use the same map.
         // chunks lg and lg + 4 (kFp4) or 2lg and 2lg + 1 of the 128-byte row
-        const uint32_t ao = lds_at<A_STEP_BYTES>(arow, KIND == kFp4 ? lg : 2 * lg);
+        const uint32_t ao = lds_at<A_STEP_BYTES>(arow, LANE_MAP_MX ? lg : 2 * lg);
         const v4i a0 = *reinterpret_cast<const v4i*>(&sA[buf][ao]);
-        const v4i a1 = *reinterpret_cast<const v4i*>(&sA[buf][ao ^ (KIND == kFp4 ? 64u : 16u)]);
+        const v4i a1 = *reinterpret_cast<const v4i*>(&sA[buf][ao ^ (LANE_MAP_MX ? 64u : 16u)]);
         if constexpr (KIND == kFp8 && SCALE == kScaleF32) {
           const v4i s4 = *reinterpret_cast<const v4i*>(&sAs[buf][wm * 64 + ms * 16 + 4 * lg]);
           const v8i av = cat8(a0, a1);
@@ -449,6 +503,14 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
           for (int ns = 0; ns < 4; ++ns)
             acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv[ns], acc[ms][ns], 0, 4, 0, sab,
                                                                            0, (int)bsc[ns]);
+        } else if constexpr (MX) {
+          // lane group lg supplies the scales of k block lg of the step
+          const int sab = (int)((sAs[buf][arow] >> (8 * lg)) & 0xffu);
+          const v8i av = cat8(a0, a1);
+#pragma unroll
+          for (int ns = 0; ns < 4; ++ns)
+            acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                av, bv[ns], acc[ms][ns], 0, KIND == kMx4 ? 4 : 0, 0, sab, 0, (int)bsc[ns]);
         } else {  // bf16 A: 16 k per lane = two 16x16x32 MFMAs
 #pragma unroll
           for (int ns = 0; ns < 4; ++ns) {
@@ -700,6 +762,34 @@ St LaunchBf16Gemm(const Bf16GemmArgs& a) {
   if (a.out_kind == kOutBf16) launch_one<kBf16, kScaleUe8m0, kOutBf16, false, false>(gp, grid, a.stream);
   else launch_one<kBf16, kScaleUe8m0, kOutF32, false, false>(gp, grid, a.stream);
   return AfterLaunch("bf16_gemm_launch_failed");
+}
+
+St LaunchMx32Gemm(const Mx32GemmArgs& a) {
+  if (!a.a || !a.a_scale || !a.w || !a.w_scale || !a.out || !a.error_flag || !a.stream)
+    return Invalid("mx32_gemm_null_argument");
+  // 128-deep MX steps and 128-row W tiles
+  if (a.m == 0 || a.n == 0 || a.k == 0 || a.k % 128 || a.n % 128) return Invalid("mx32_gemm_shape_invalid");
+  GemmParams gp{};
+  gp.a = a.a;
+  gp.a_scale = a.a_scale;
+  gp.w = a.w;
+  gp.w_scale = a.w_scale;
+  gp.out = a.out;
+  gp.err = a.error_flag;
+  gp.a_rows_total = a.m;
+  gp.a_row_stride = 1;
+  // V4.1 error bits: 1 for an invalid operand or scale, 2 for a non-finite
+  // result, which is stored as the reference stores it
+  gp.err_code = 1u;
+  gp.err_scale = 1u;
+  gp.err_nonfinite = 2u;
+  gp.write_nonfinite = 1u;
+  uint32_t grid;
+  St s = prepare(gp, grid, a.m, a.n, a.k, 1, false, kOutBf16, 0);
+  if (!s.ok()) return s;
+  if (a.fp4_weight) launch_one<kMx4, kScaleUe8m0, kOutBf16, false, true>(gp, grid, a.stream);
+  else launch_one<kMx8, kScaleUe8m0, kOutBf16, false, true>(gp, grid, a.stream);
+  return AfterLaunch("mx32_gemm_launch_failed");
 }
 
 uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k) {

@@ -318,4 +318,52 @@ struct NonfiniteScanArgs {
 };
 St LaunchNonfiniteScan(const NonfiniteScanArgs& a);
 
+// ------------------------------------------- DeepSeek V4.1 32-block formats
+// (v41_formats.hip, gemm_mfma.hip; plugins/model-deepseek-v41)
+struct V41Quant32Args {
+  const uint16_t* input = nullptr;  // bf16 [rows, k]
+  uint8_t* codes = nullptr;         // e4m3 [rows, k]
+  uint8_t* scales = nullptr;        // UE8M0 [rows, k/32]
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t rows = 0, k = 0;
+};
+St LaunchV41Quant32(const V41Quant32Args& a);
+// out bf16 [m, n] = A . W^T with A e4m3 + UE8M0 per (row, 32 k) and W e4m3
+// + UE8M0 per (32 rows, 32 k) or W e2m1 + UE8M0 per (row, 32 k), on the
+// MX MFMA (each lane group's scale covers its 32-deep k block).  Error bit
+// 1: a NaN code or a 255 scale; 2: a non-finite output (stored).
+struct Mx32GemmArgs {
+  const uint8_t* a = nullptr;
+  const uint8_t* a_scale = nullptr;
+  const uint8_t* w = nullptr;
+  const uint8_t* w_scale = nullptr;
+  uint16_t* out = nullptr;
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t m = 0, n = 0, k = 0;
+  bool fp4_weight = false;
+};
+St LaunchMx32Gemm(const Mx32GemmArgs& a);
+struct V41Fp4ToFp8Args {
+  const uint8_t* packed = nullptr;  // e2m1 [rows, cols/2]
+  const uint8_t* scales = nullptr;  // UE8M0 [rows, cols/32]
+  uint8_t* weight = nullptr;        // e4m3 [rows, cols]
+  uint8_t* weight_scales = nullptr; // UE8M0 [rows/32, cols/32]
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t rows = 0, cols = 0;
+};
+St LaunchV41Fp4ToFp8(const V41Fp4ToFp8Args& a);
+struct V41BlockDequantArgs {
+  const uint8_t* source = nullptr;  // e4m3 [rows, cols]
+  const void* scales = nullptr;     // [rows/block, cols/block] UE8M0 or fp32
+  uint16_t* output = nullptr;       // bf16 [rows, cols]
+  uint32_t* error_flag = nullptr;
+  hipStream_t stream = nullptr;
+  uint32_t rows = 0, cols = 0, block = 0;
+  uint32_t scale_f32 = 0;
+};
+St LaunchV41BlockDequant(const V41BlockDequantArgs& a);
+
 }  // namespace pih_amd

@@ -104,6 +104,102 @@ St RouterTopk(const pih_amd_router_topk_launch_v1* r) {
   return LaunchRouterTopk(a);
 }
 
+// The reference's region checks (plugins/model-deepseek-v41/linear_fp8.cpp:
+// 6-13): non-zero, aligned, exactly the layout's size, no address overflow.
+bool RegionOk(uintptr_t address, uint64_t bytes, uint64_t want, unsigned align) {
+  return address && address % align == 0 && bytes == want && want <= UINTPTR_MAX - address;
+}
+bool RegionsOverlap(uintptr_t a, uint64_t na, uintptr_t b, uint64_t nb) { return a < b + nb && b < a + na; }
+
+St V41Linear(const pih_amd_v41_linear_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("v41_linear_request_invalid");
+  const bool fp4 = r->weight_format == PIH_AMD_V41_WEIGHT_MXFP4_V1;
+  if (!fp4 && r->weight_format != PIH_AMD_V41_WEIGHT_FP8_BLOCK32_V1) return Invalid("v41_linear_weight_format_invalid");
+  // linear_fp8.cpp:15-17 / linear_fp4.cpp:14-16
+  if (!r->stream || !r->rows || r->rows > 4096 || !r->in_features || r->in_features > 32768 || !r->out_features ||
+      r->out_features > 32768 || r->in_features % 32 || r->out_features % 32)
+    return Invalid("V4.1 linear requires bounded block-32 dimensions");
+  const uint64_t m = r->rows, k = r->in_features, n = r->out_features;
+  const uint64_t wbytes = fp4 ? n * k / 2 : n * k, wsbytes = fp4 ? n * (k / 32) : (n / 32) * (k / 32);
+  if (!RegionOk(r->input_bf16, r->input_bytes, m * k * 2, 2) || !RegionOk(r->weight, r->weight_bytes, wbytes, 1) ||
+      !RegionOk(r->weight_scales, r->weight_scale_bytes, wsbytes, 1) ||
+      !RegionOk(r->quantized_e4m3, r->quantized_bytes, m * k, 1) ||
+      !RegionOk(r->activation_scales, r->activation_scale_bytes, m * (k / 32), 1) ||
+      !RegionOk(r->output_bf16, r->output_bytes, m * n * 2, 2) ||
+      !RegionOk(r->error_flag_u32, r->error_flag_bytes, 4, 4))
+    return Invalid("V4.1 linear buffer layout invalid");
+  const uintptr_t reads[3][2] = {{r->input_bf16, r->input_bytes}, {r->weight, r->weight_bytes},
+                                 {r->weight_scales, r->weight_scale_bytes}};
+  const uintptr_t writes[4][2] = {{r->quantized_e4m3, r->quantized_bytes},
+                                  {r->activation_scales, r->activation_scale_bytes},
+                                  {r->output_bf16, r->output_bytes},
+                                  {r->error_flag_u32, r->error_flag_bytes}};
+  for (int i = 0; i < 4; ++i) {
+    for (int j = 0; j < 3; ++j)
+      if (RegionsOverlap(writes[i][0], writes[i][1], reads[j][0], reads[j][1]))
+        return Invalid("V4.1 linear overwrites an input");
+    for (int j = 0; j < i; ++j)
+      if (RegionsOverlap(writes[i][0], writes[i][1], writes[j][0], writes[j][1]))
+        return Invalid("V4.1 linear writable alias");
+  }
+  // the MX MFMA tiles take 128-deep steps over 128-row W tiles
+  if (k % 128 || n % 128) return Invalid("v41_linear_requires_128_multiples");
+  V41Quant32Args q;
+  q.input = Ptr<const uint16_t>(r->input_bf16);
+  q.codes = Ptr<uint8_t>(r->quantized_e4m3);
+  q.scales = Ptr<uint8_t>(r->activation_scales);
+  q.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  q.stream = AsStream(r->stream);
+  q.rows = r->rows;
+  q.k = r->in_features;
+  St s = LaunchV41Quant32(q);
+  if (!s.ok()) return s;
+  Mx32GemmArgs g;
+  g.a = q.codes;
+  g.a_scale = q.scales;
+  g.w = Ptr<const uint8_t>(r->weight);
+  g.w_scale = Ptr<const uint8_t>(r->weight_scales);
+  g.out = Ptr<uint16_t>(r->output_bf16);
+  g.error_flag = q.error_flag;
+  g.stream = q.stream;
+  g.m = r->rows;
+  g.n = r->out_features;
+  g.k = r->in_features;
+  g.fp4_weight = fp4;
+  return LaunchMx32Gemm(g);
+}
+
+St V41Fp4ToFp8(const pih_amd_v41_fp4_to_fp8_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("v41_fp4_to_fp8_request_invalid");
+  V41Fp4ToFp8Args a;
+  a.packed = Ptr<const uint8_t>(r->packed);
+  a.scales = Ptr<const uint8_t>(r->scales);
+  a.weight = Ptr<uint8_t>(r->weight_e4m3);
+  a.weight_scales = Ptr<uint8_t>(r->weight_scales);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.rows = r->rows;
+  a.cols = r->columns;
+  return LaunchV41Fp4ToFp8(a);
+}
+
+St V41BlockDequant(const pih_amd_v41_block_dequant_launch_v1* r) {
+  if (!HeaderOk(r, kAbi)) return Invalid("v41_block_dequant_request_invalid");
+  if (r->scale_storage != PIH_AMD_V41_SCALE_E8M0_V1 && r->scale_storage != PIH_AMD_V41_SCALE_F32_V1)
+    return Invalid("v41_dequant_scale_storage_invalid");
+  V41BlockDequantArgs a;
+  a.source = Ptr<const uint8_t>(r->source_e4m3);
+  a.scales = Ptr<const void>(r->scales);
+  a.output = Ptr<uint16_t>(r->output_bf16);
+  a.error_flag = Ptr<uint32_t>(r->error_flag_u32);
+  a.stream = AsStream(r->stream);
+  a.rows = r->rows;
+  a.cols = r->columns;
+  a.block = r->block;
+  a.scale_f32 = r->scale_storage == PIH_AMD_V41_SCALE_F32_V1 ? 1u : 0u;
+  return LaunchV41BlockDequant(a);
+}
+
 St Fp8Quant(const pih_amd_fp8_quant_launch_v1* r) {
   if (!HeaderOk(r, kAbi) || !ScaleFmtOk(r->scale_format)) return Invalid("fp8_quant_request_invalid");
   Fp8QuantArgs a;
@@ -394,12 +490,15 @@ PIH_AMD_CONTAINED(CQueryMoeLayer, QueryMoeLayer, pih_amd_moe_layer_launch_v1)
 PIH_AMD_CONTAINED(CMoeLayer, MoeLayer, pih_amd_moe_layer_launch_v1)
 PIH_AMD_CONTAINED(CRoutePlanNoAlloc, RoutePlanNoAlloc, pih_amd_route_plan_launch_v1)
 PIH_AMD_CONTAINED(CRouterTopk, RouterTopk, pih_amd_router_topk_launch_v1)
+PIH_AMD_CONTAINED(CV41Linear, V41Linear, pih_amd_v41_linear_launch_v1)
+PIH_AMD_CONTAINED(CV41Fp4ToFp8, V41Fp4ToFp8, pih_amd_v41_fp4_to_fp8_launch_v1)
+PIH_AMD_CONTAINED(CV41BlockDequant, V41BlockDequant, pih_amd_v41_block_dequant_launch_v1)
 
 const pih_amd_linear_kernels_api_v1 kContract = {
     sizeof(pih_amd_linear_kernels_api_v1), kAbi, &kIdentity, &CQueryWorkspace, &CRoutePlan,
     &CFp8Quant, &CFp8Gemm, &CMoeFp8Gemm, &CMoeMxfp4Gemm, &CMoeCombine, &CBf16Gemm, &CW4a16,
     &CSiluMul, &CSwiGlu, &CMxfp4Decode, &CW4a16Dequant, &CW4a16Grouped, &CQueryMoeLayer, &CMoeLayer,
-    &CRoutePlanNoAlloc, &CRouterTopk};
+    &CRoutePlanNoAlloc, &CRouterTopk, &CV41Linear, &CV41Fp4ToFp8, &CV41BlockDequant};
 
 pih_status_v1 BindOrigin(const char* path) noexcept {
   return ToAbi(path && path[0] == '/' ? Ok() : Invalid("bind_origin_path_not_absolute"));

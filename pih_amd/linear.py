@@ -386,3 +386,65 @@ class MoeLayer:
                         error_flag_u32=ptr(self.flag), stream=stream_handle(), **self.fields)
         _check(_ln().call("launch_moe_layer", r), "moe_layer")
         return self.out
+
+
+# ------------------------------------------------ DeepSeek V4.1 32-block formats
+def v41_linear(x: torch.Tensor, weight: torch.Tensor, weight_scales: torch.Tensor, weight_format: int,
+               out: Optional[torch.Tensor] = None, quantized: Optional[torch.Tensor] = None,
+               activation_scales: Optional[torch.Tensor] = None, flag: Optional[torch.Tensor] = None):
+    """The V4.1 FP8 (32x32 weight blocks) or mixed FP8/FP4 linear
+    (plugins/model-deepseek-v41/linear_fp8.cu:82-105) through
+    ``launch_v41_linear``: per-32 activation quant into ``quantized`` /
+    ``activation_scales`` (allocated when None), then the MX GEMM; returns
+    (out bf16 [rows, N], quantized, activation_scales, flag)."""
+    rows, k = x.shape
+    n = weight.shape[0]
+    dev = x.device
+    if out is None:
+        out = torch.empty(rows, n, dtype=torch.bfloat16, device=dev)
+    if quantized is None:
+        quantized = torch.empty(rows, k, dtype=torch.uint8, device=dev)
+    if activation_scales is None:
+        activation_scales = torch.empty(rows, k // 32, dtype=torch.uint8, device=dev)
+    flag = error_flag() if flag is None else flag
+    nbytes = lambda t: t.numel() * t.element_size()  # noqa: E731
+    r = abi.request(abi.LN["v41_linear"], input_bf16=ptr(x), input_bytes=nbytes(x), weight=ptr(weight),
+                    weight_bytes=nbytes(weight), weight_scales=ptr(weight_scales),
+                    weight_scale_bytes=nbytes(weight_scales), quantized_e4m3=ptr(quantized),
+                    quantized_bytes=nbytes(quantized), activation_scales=ptr(activation_scales),
+                    activation_scale_bytes=nbytes(activation_scales), output_bf16=ptr(out),
+                    output_bytes=nbytes(out), error_flag_u32=ptr(flag), error_flag_bytes=4,
+                    stream=stream_handle(), rows=rows, in_features=k, out_features=n, weight_format=weight_format)
+    _check(_ln().call("launch_v41_linear", r), "v41_linear")
+    return out, quantized, activation_scales, flag
+
+
+def v41_fp4_to_fp8(packed: torch.Tensor, scales: torch.Tensor, flag: Optional[torch.Tensor] = None):
+    """V4.1 expert FP4 -> FP8 32x32 conversion on the device
+    (weight_expert_convert.cpp:33-100): (e4m3 [rows, cols], UE8M0 [rows/32,
+    cols/32], flag)."""
+    rows, half = packed.shape
+    cols = half * 2
+    w = torch.empty(rows, cols, dtype=torch.uint8, device=packed.device)
+    s = torch.empty(rows // 32, cols // 32, dtype=torch.uint8, device=packed.device)
+    flag = error_flag() if flag is None else flag
+    r = abi.request(abi.LN["v41_fp4_to_fp8"], packed=ptr(packed), scales=ptr(scales), weight_e4m3=ptr(w),
+                    weight_scales=ptr(s), error_flag_u32=ptr(flag), stream=stream_handle(), rows=rows, columns=cols)
+    _check(_ln().call("launch_v41_fp4_to_fp8", r), "v41_fp4_to_fp8")
+    return w, s, flag
+
+
+def v41_block_dequant(source: torch.Tensor, scales: torch.Tensor, block: int, out: Optional[torch.Tensor] = None,
+                      flag: Optional[torch.Tensor] = None):
+    """e4m3 [rows, cols] x per-block scale (uint8 UE8M0 or float32 tensor)
+    -> bf16 (weight_dequantize.cpp:17-50, DequantizeWoATensor)."""
+    rows, cols = source.shape
+    if out is None:
+        out = torch.empty(rows, cols, dtype=torch.bfloat16, device=source.device)
+    flag = error_flag() if flag is None else flag
+    storage = abi.V41_SCALE_F32 if scales.dtype == torch.float32 else abi.V41_SCALE_E8M0
+    r = abi.request(abi.LN["v41_block_dequant"], source_e4m3=ptr(source), scales=ptr(scales), output_bf16=ptr(out),
+                    error_flag_u32=ptr(flag), stream=stream_handle(), rows=rows, columns=cols, block=block,
+                    scale_storage=storage)
+    _check(_ln().call("launch_v41_block_dequant", r), "v41_block_dequant")
+    return out, flag

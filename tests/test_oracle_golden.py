@@ -693,3 +693,124 @@ def test_against_live_reference_library():
                                w2.ctypes.data_as(P)) == 0
     np.testing.assert_array_equal(ids1, ids2)
     np.testing.assert_array_equal(w1.view(np.uint32), w2.view(np.uint32))
+
+
+# --------------------------------------------------- V4.1 32-block formats
+def test_v41_fp4_to_fp8_reference_vectors(gold):
+    """ConvertExpertFp4Block of the reference (compiled from its sources):
+    narrow and 12-wide row-scale bands, a maximum of exactly 6, all 127."""
+    for b in range(gold["v41_fp4_packed"].shape[0]):
+        w, s, st = oracle.v41_fp4_block_to_fp8(gold["v41_fp4_packed"][b], gold["v41_fp4_scales"][b])
+        assert st == 0 and s == gold["v41_fp8_scale"][b]
+        np.testing.assert_array_equal(w.ravel(), gold["v41_fp8_weight"][b])
+
+
+def test_v41_fp4_to_fp8_closed_forms():
+    """All row scales equal: shift = 6, every e2m1 magnitude m becomes
+    m * 64 (exact in e4m3: 32, 64, 96, 128, 192, 256, 384); the negative zero
+    nibble gives +0; a row 7 below the maximum (shift -1) maps 0.5 to 0.25
+    and 6 to 3; one 12 below (shift -6) maps 0.5 to the subnormal 2^-7 (code
+    4) and 6 to 0.09375 (code 0x1C); shared scale = max - 6; errors for 255
+    and max < 6."""
+    nib = np.arange(16, dtype=np.uint8)
+    row = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)  # 16 nibbles 0..15 then again
+    packed = np.tile(np.concatenate([row, row]), 32)
+    scales = np.full(32, 120, np.uint8)
+    w, s, st = oracle.v41_fp4_block_to_fp8(packed, scales)
+    assert st == 0 and s == 114
+    vals = [oracle.e4m3_decode(int(c)) for c in w[0, :16]]
+    assert vals == [0.0, 32.0, 64.0, 96.0, 128.0, 192.0, 256.0, 384.0,
+                    0.0, -32.0, -64.0, -96.0, -128.0, -192.0, -256.0, -384.0]
+    assert w[0, 8] == 0x00  # e2m1 -0 -> +0
+    scales[5], scales[6] = 113, 108
+    w, s, st = oracle.v41_fp4_block_to_fp8(packed, scales)
+    assert st == 0 and s == 114
+    assert oracle.e4m3_decode(int(w[5, 1])) == 0.25 and oracle.e4m3_decode(int(w[5, 7])) == 3.0
+    assert w[6, 1] == 0x04 and w[6, 7] == 0x1C and w[6, 9] == 0x84
+    bad = scales.copy()
+    bad[9] = 255
+    assert oracle.v41_fp4_block_to_fp8(packed, bad)[2] == 1
+    assert oracle.v41_fp4_block_to_fp8(packed, np.full(32, 5, np.uint8))[2] == 2
+
+
+def test_v41_dequant_reference_vectors(gold):
+    for blk in (32, 128):
+        out, st = oracle.v41_dequant_block(gold[f"v41_woa{blk}_src"], gold[f"v41_woa{blk}_scale"][0], blk)
+        assert st == 0
+        np.testing.assert_array_equal(out, gold[f"v41_woa{blk}_bf16"])
+    src = np.full(32 * 32, 0x38, np.uint8)  # 1.0
+    out, st = oracle.v41_dequant_block(src, 0.375, 32)
+    assert st == 0 and (out == 0x3EC0).all()  # bf16(0.375)
+    src[7] = 0x7F
+    assert oracle.v41_dequant_block(src, 0.375, 32)[1] == 2
+    assert oracle.v41_dequant_block(np.full(1024, 0x7E, np.uint8), 2.0 ** 120, 32)[1] == 3  # 448 * 2^120
+    assert oracle.v41_dequant_block(src, 0.0, 32)[1] == 1
+
+
+def test_v41_quant32_closed_forms():
+    """1/448 lies in [2^-9, 2^-8), so a group with amax 1 takes e = -8 (byte
+    119) and 1.0 encodes as 256 = 0x78; an all-zero group uses the 1e-4 floor:
+    1e-4/448 in [2^-23, 2^-22) -> byte 105; non-finite inputs raise bit 1,
+    encode 0 and do not enter the maximum."""
+    x = np.zeros((2, 64), np.float32)
+    x[0, :32] = 1.0
+    x[0, 32:] = 0.0
+    x[1, :32] = -1.0
+    x[1, 3] = np.inf
+    x[1, 32:] = np.linspace(-3.0, 3.0, 32, dtype=np.float32)
+    codes, scales, err = oracle.v41_quant32(oracle.f32_to_bf16_bits(x))
+    assert scales[0].tolist() == [119, 105] and (codes[0, :32] == 0x78).all() and (codes[0, 32:] == 0).all()
+    assert err == 1 and codes[1, 3] == 0 and scales[1, 0] == 119 and codes[1, 0] == 0xF8
+    # 3/448 in [2^-8, 2^-7): e = -7, 3.0 * 128 = 384 = 0x7C
+    assert scales[1, 1] == 120 and codes[1, 63] == 0x7C and codes[1, 32] == 0xFC
+
+
+def _v41_operands(seed, rows, n, k, fp4):
+    rng = np.random.default_rng(seed)
+    a_int = rng.integers(-4, 5, (rows, k))
+    a = np.array([oracle.e4m3_encode(float(v)) for v in a_int.ravel()], np.uint8).reshape(rows, k)
+    sa = rng.integers(124, 131, (rows, k // 32)).astype(np.uint8)
+    if fp4:
+        codes = rng.integers(0, 16, (n, k)).astype(np.uint8)
+        w = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+        table = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, 0, -.5, -1, -1.5, -2, -3, -4, -6])
+        wv = table[codes]
+        sw = rng.integers(124, 131, (n, k // 32)).astype(np.uint8)
+        sw_full = np.repeat(sw, 32, axis=1)
+    else:
+        w_int = rng.integers(-4, 5, (n, k))
+        w = np.array([oracle.e4m3_encode(float(v)) for v in w_int.ravel()], np.uint8).reshape(n, k)
+        wv = w_int.astype(np.float64)
+        sw = rng.integers(124, 131, (n // 32, k // 32)).astype(np.uint8)
+        sw_full = np.repeat(np.repeat(sw, 32, axis=0), 32, axis=1)
+    return a, sa, w, sw, a_int.astype(np.float64), wv, sw_full
+
+
+@pytest.mark.parametrize("fp4", [False, True])
+def test_v41_linear_float64_brute_force(fp4):
+    """Small integers / e2m1 values with power-of-two scales: every term and
+    partial sum is exact in fp32, so the output is the float64 sum
+    sum_k a x 2^(sa-127) x w x 2^(sw-127) rounded once to bf16; the scale of
+    W element (n, k) comes from block (n/32, k/32) (FP8) or row n (FP4)."""
+    rows, n, k = 3, 64, 128
+    a, sa, w, sw, af, wf, swf = _v41_operands(77 + fp4, rows, n, k, fp4)
+    got, err = oracle.v41_linear(a, sa, w, sw, n, fp4)
+    assert err == 0
+    ascale = np.exp2(np.repeat(sa, 32, axis=1).astype(np.float64) - 127)
+    wscale = np.exp2(swf.astype(np.float64) - 127)
+    want = (af * ascale) @ (wf * wscale).T
+    np.testing.assert_array_equal(got, oracle.f32_to_bf16_bits(want.astype(np.float32)))
+
+
+def test_v41_linear_error_bits():
+    rows, n, k = 2, 32, 64
+    a, sa, w, sw, *_ = _v41_operands(90, rows, n, k, False)
+    a2 = a.copy()
+    a2[1, 5] = 0x7F  # NaN code: bit 1, the output row is NaN (bit 2)
+    out, err = oracle.v41_linear(a2, sa, w, sw, n, False)
+    assert err == 3 and np.isnan(oracle.bf16_bits_to_f32(out[1])).all()
+    sa2 = sa.copy()
+    sa2[0, 1] = 255  # NaN scale: bit 1 and an infinite term
+    assert oracle.v41_linear(a, sa2, w, sw, n, False)[1] == 3
+    sa3 = np.full_like(sa, 254)  # finite operands, terms overflow: bit 2 only
+    assert oracle.v41_linear(a, sa3, w, np.full_like(sw, 254), n, False)[1] == 2
