@@ -154,3 +154,43 @@ def test_silu_mul_code_object(co):
     # at most one bf16 ulp from the reference formula
     diff = np.abs(got.astype(np.int32) - ref.astype(np.int32))
     assert diff.max() <= 1
+
+
+@pytest.mark.parametrize("m,n,k,seed", [(3, 1024, 1024, 0), (1, 2048, 1024, 0x51A7), (2, 1024, 1024, 0x62B8),
+                                        (3, 1024, 2048, 0x73C9), (7, 3072, 1024, 0x84DA),
+                                        (17, 1024, 3072, 0x95EB)])
+def test_w4a16_compat_reference_fixture(co, m, n, k, seed):
+    """The reference's own fixture matrix for this kernel
+    (src/backend/cuda/qwen_int4_cuda_fixture.cpp:87-140,291,296-302): exact
+    sums, so the outputs must equal the expected bf16 values bit for bit
+    (exact zero sums as +0, see tests/qwen_int4_fixture.py)."""
+    from tests import qwen_int4_fixture as fx
+
+    x, q, s, expected = fx.case(m, n, k, seed)
+    got, flag = _run_w4a16(co, x, q, s, m, n, k)
+    assert flag == 0
+    np.testing.assert_array_equal(got, expected)
+
+
+@pytest.mark.parametrize("m,n,k,seed", [(3, 1024, 1024, 0), (7, 3072, 1024, 0x84DA), (17, 1024, 3072, 0x95EB)])
+def test_w4a16_entry_reference_fixture(co, m, n, k, seed):
+    """The same fixture through the linear pack's launch_w4a16_gemm
+    (symmetric format)."""
+    import torch
+
+    from pih_amd import abi
+    from pih_amd.device import ptr
+    from tests import qwen_int4_fixture as fx
+
+    _, stream = co
+    x, q, s, expected = fx.case(m, n, k, seed)
+    xd, qd, sd = to_dev(x), to_dev(q), to_dev(s)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    r = abi.request(abi.LN["w4a16"], input_bf16=ptr(xd), qweight=ptr(qd), scales=ptr(sd), zeros=0,
+                    output_bf16=ptr(out), workspace=0, workspace_bytes=0, error_flag_u32=ptr(flag),
+                    stream=stream.cuda_stream, m=m, n=n, k=k, format=abi.W4A16_SYMMETRIC)
+    assert abi.linear_pack().call("launch_w4a16_gemm", r).code == abi.OK
+    stream.synchronize()
+    assert int(flag.item()) == 0
+    np.testing.assert_array_equal(to_host(out), expected)

@@ -814,3 +814,17 @@ def test_v41_linear_error_bits():
     assert oracle.v41_linear(a, sa2, w, sw, n, False)[1] == 3
     sa3 = np.full_like(sa, 254)  # finite operands, terms overflow: bit 2 only
     assert oracle.v41_linear(a, sa3, w, np.full_like(sw, 254), n, False)[1] == 2
+
+
+# ------------------------------------------------ reference INT4 fixture
+@pytest.mark.parametrize("m,n,k,seed", [(3, 1024, 1024, 0), (1, 2048, 1024, 0x51A7), (2, 1024, 1024, 0x62B8),
+                                        (3, 1024, 2048, 0x73C9), (7, 3072, 1024, 0x84DA),
+                                        (17, 1024, 3072, 0x95EB)])
+def test_w4a16_sym_reference_fixture(m, n, k, seed):
+    """The reference's closed-form INT4 fixture
+    (src/backend/cuda/qwen_int4_cuda_fixture.cpp:87-140,291,296-302):
+    po_w4a16_sym equals its expected bf16 outputs bit for bit."""
+    from tests import qwen_int4_fixture as fx
+
+    x, packed, scales, expected = fx.case(m, n, k, seed)
+    np.testing.assert_array_equal(oracle.w4a16_sym(x, packed, scales), expected)
