@@ -38,24 +38,54 @@
 // 9 % but ran 3 % slower than M-fastest groups of 32).
 #include <type_traits>
 
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
 namespace pih_amd {
 namespace {
 
-constexpr int BM = 128, BN = 256, NTH = 512, LDS_ROW = 128, GROUP_M = 32, STAGES = 3;
-
+constexpr int BM = 128, BN = 256, LDS_ROW = 128, GROUP_M = 32, STAGES = 3;
+// eight waves (2 x 4, one 64 x 64 output block each)
+constexpr int NCW = 8, NTH = 64 * NCW;
+constexpr uint32_t A_BYTES = BM * LDS_ROW, W_BYTES = BN * LDS_ROW, SA_BYTES = 512, SW_BYTES = 256;
+constexpr uint32_t STAGE = A_BYTES + W_BYTES + SA_BYTES + SW_BYTES, DUMMY_BYTES = 256;
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
 // [6:4], lgkmcnt [11:8]; an all-ones field does not wait)
 constexpr int kWaitVm7 = 0x0F77;     // vmcnt(7)
 constexpr int kWaitVm0 = 0x0F70;     // vmcnt(0)
-constexpr int kWaitLgkm0 = 0xC07F;   // lgkmcnt(0)
 
-// 16 bytes per lane from global memory straight into LDS: lane l's bytes
-// land at lds + 16 l (lds is wave-uniform; it goes to M0)
-__device__ __forceinline__ void dma16(const void* src, void* lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+// LDS byte address of a __shared__ object
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+
+// Global -> LDS DMA of 16 (dma16) or 4 (dma4) bytes per lane: lane l's data
+// lands at LDS byte lds + 16 l (resp. 4 l); lds is wave-uniform and goes to
+// M0.  Issued as inline asm so that the compiler, which cannot tell which
+// LDS bytes a DMA writes, adds no conservative vmcnt waits before LDS reads;
+// the kernel waits for them explicitly (s_waitcnt vmcnt + s_barrier).  M0 is
+// written here only; nothing else in these kernels uses it.
+// The address is a wave-uniform base (SGPRs) plus a per-lane 32-bit offset,
+// or (dma4v) a per-lane 64-bit address.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off), "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off), "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void dma4v(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src) : "memory");
+}
+
+// a pointer the caller knows to be wave-uniform, as SGPRs
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
 }
 
 // byte offset of 16-byte chunk c of tile row r (XOR-swizzled slots)
@@ -209,23 +239,14 @@ __device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, u
 
 template <int SCALE, int OUT>
 __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
-  // One LDS variable per stage and operand: the compiler's wait insertion
-  // tells DMA into one stage from reads of another only across distinct
-  // variables (otherwise it waits for every load in flight before any LDS
-  // access).
-  __shared__ __align__(16) uint8_t sA0[BM * LDS_ROW], sA1[BM * LDS_ROW], sA2[BM * LDS_ROW];
-  __shared__ __align__(16) uint8_t sB0[BN * LDS_ROW], sB1[BN * LDS_ROW], sB2[BN * LDS_ROW];
-  // A-row scales of a stage: row wm*64 + rb*16 + l at [wm*64 + l*4 + rb]
-  __shared__ __align__(16) uint32_t sSa0[BM], sSa1[BM], sSa2[BM];
-  __shared__ __align__(16) uint32_t sSw0[2], sSw1[2], sSw2[2];
-  auto sA = [&](int st) -> uint8_t* { return st == 0 ? sA0 : st == 1 ? sA1 : sA2; };
-  auto sB = [&](int st) -> uint8_t* { return st == 0 ? sB0 : st == 1 ? sB1 : sB2; };
-  auto sSa = [&](int st) -> uint32_t* { return st == 0 ? sSa0 : st == 1 ? sSa1 : sSa2; };
-  auto sSw = [&](int st) -> uint32_t* { return st == 0 ? sSw0 : st == 1 ? sSw1 : sSw2; };
+  // Stage s at smem + s * STAGE: A tile, W tile, A-row scales, W scales.
+  __shared__ __align__(16) uint8_t smem[STAGES * STAGE + DUMMY_BYTES];
+  const uint32_t lds0 = lds_addr(smem);
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
-  const uint32_t wm = __builtin_amdgcn_readfirstlane(wave >> 2), wn = __builtin_amdgcn_readfirstlane(wave & 3);
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t wm = (wv >> 2) & 1u, wn = wv & 3u;
   constexpr bool kSwi = OUT == kOutSwiGlu || OUT == kOutSwiGluFp8;  // gate/up pairs in the tile
 
   uint32_t expert, row0, rows, nt;
@@ -251,14 +272,12 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
     return src;
   };
-  const uint64_t sa_off = a_source(tid & (BM - 1)) * KB;
-
   // W tile row R: for SwiGLU, wave block R >> 6 holds 32 gate rows (R & 63
   // below 32) and the 32 matching up rows, so each wave owns gate/up pairs
   auto w_row = [&](uint32_t R) -> uint32_t {
     if constexpr (kSwi) {
-      const uint32_t wv = R >> 6, j = (R & 63) >> 4, rr = R & 15;
-      const uint32_t base = nt * 128 + wv * 32 + (j & 1) * 16 + rr;
+      const uint32_t wb = R >> 6, j = (R & 63) >> 4, rr = R & 15;
+      const uint32_t base = nt * 128 + wb * 32 + (j & 1) * 16 + rr;
       return j >= 2 ? p.n / 2 + base : base;
     } else {
       const uint32_t row = nt * BN + R;
@@ -275,63 +294,77 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     wblk0 = min(2 * nt, p.n / 128 - 1);
     wblk1 = min(2 * nt + 1, p.n / 128 - 1);
   }
-  const uint64_t ws0_off = ((uint64_t)expert * (p.n / 128) + wblk0) * KB;
-  const uint64_t ws1_off = ((uint64_t)expert * (p.n / 128) + wblk1) * KB;
+  constexpr uint32_t ESZ = SCALE == kScaleUe8m0 ? 1 : 4;
+  const uint64_t ws_off[2] = {((uint64_t)expert * (p.n / 128) + wblk0) * KB,
+                              ((uint64_t)expert * (p.n / 128) + wblk1) * KB};
+
+  // Operand tiles move global -> LDS by DMA
+  // (global_load_lds_dwordx4): an instruction lands lane l's 16 bytes at
+  // byte 16 l of a wave-uniform 1 KB window, i.e. tile row 8q + (l >> 3),
+  // slot l & 7 of window q, so lane l fetches chunk (l & 7) ^ ((row >> 1) & 7)
+  // of that row (full 128-byte lines per 8 lanes).  Wave w fills A rows
+  // [16w, 16w + 16) and W rows [32w, 32w + 32) of a stage.
+  const uint32_t lrow = lane >> 3, lslot = lane & 7;
+  // byte offsets from the operand bases (A: a_rows_total * K and W: n * K
+  // per expert stay below 2^32, which the launcher checks)
+  uint32_t a_off[2], w_off[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t R = 16 * wv + 8 * i + lrow;
+    a_off[i] = (uint32_t)(a_source(R) * K) + ((lslot ^ ((R >> 1) & 7u)) << 4);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t R = 32 * wv + 8 * i + lrow;
+    w_off[i] = w_row(R) * K + ((lslot ^ ((R >> 1) & 7u)) << 4);
+  }
+  // Scales (one dword DMA per wave and step, so every compute wave issues
+  // seven loads per step): waves 0 and 1 fetch the A-row scales of rows
+  // 64w + (l & 3) * 16 + (l >> 2) into word 64w + l of the stage's scale
+  // block (a lane's four A-row scales are then one 16-byte read); wave 2
+  // the two W block scales (lane l: block l & 1); waves 3..7 repeat wave
+  // 2's load into the scratch word.  UE8M0 bytes come in their aligned
+  // dword and are picked out by byte offset.
+  const uint8_t* s_src;
+  uint32_t s_lds;
+  if (wv < 2) {
+    const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2));
+    s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB * ESZ;
+    s_lds = A_BYTES + W_BYTES + 256 * wv;
+  } else {
+    s_src = static_cast<const uint8_t*>(p.w_scale) + ws_off[lane & 1] * ESZ;
+    s_lds = A_BYTES + W_BYTES + SA_BYTES;
+  }
+  s_lds = __builtin_amdgcn_readfirstlane(s_lds);
+  const bool s_scratch = wv > 2;
+  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(wv * 2048), w_lds = __builtin_amdgcn_readfirstlane(A_BYTES + wv * 4096);
+  auto issue = [&](uint32_t stage, uint32_t kb) __attribute__((always_inline)) {
+    const uint32_t base = lds0 + stage * STAGE;
+    const uint8_t* ab = uniform_ptr(p.a + (uint64_t)kb * 128);
+    const uint8_t* wb = uniform_ptr(w_base + (uint64_t)kb * 128);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(ab, a_off[i], base + a_lds + i * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(wb, w_off[i], base + w_lds + i * 1024);
+    // scales: a per-lane pointer (UE8M0 bytes come in their aligned dword)
+    uintptr_t sp = reinterpret_cast<uintptr_t>(s_src) + (uint64_t)kb * ESZ;
+    if constexpr (ESZ == 1) sp &= ~uintptr_t(3);
+    dma4v(reinterpret_cast<const void*>(sp), s_scratch ? lds0 + STAGES * STAGE : base + s_lds);
+  };
+
+  // byte offsets of this lane's UE8M0 A scales (rows wm*64 + r*16 + lr) and
+  // of the W block scales within their aligned dwords, at k step 0
+  uint32_t a_byte0[4] = {0, 0, 0, 0}, w_byte0[2] = {0, 0};
+  if constexpr (ESZ == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      a_byte0[r] = (uint32_t)((reinterpret_cast<uintptr_t>(p.a_scale) + a_source(wm * 64 + r * 16 + lr) * KB) & 3u);
+    w_byte0[0] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + ws_off[0]) & 3u);
+    w_byte0[1] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + ws_off[1]) & 3u);
+  }
   // live 16-row blocks of this wave's 64-row half
   const uint32_t rb_live =
       __builtin_amdgcn_readfirstlane(rows > wm * 64 ? min(4u, (rows - wm * 64 + 15) / 16) : 0u);
-
-  // Operand tiles move global -> LDS by DMA (global_load_lds_dwordx4): an
-  // instruction lands lane l's 16 bytes at byte 16 l of a wave-uniform 1 KB
-  // window, i.e. tile row 8q + (l >> 3), slot l & 7 of window q, so lane l
-  // fetches chunk (l & 7) ^ ((row >> 1) & 7) of that row (full 128-byte lines
-  // per 8 lanes).  Wave w fills A rows [16w, 16w + 16) and W rows
-  // [32w, 32w + 32) of a stage.
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(wave);
-  const uint32_t lrow = lane >> 3, lslot = lane & 7;
-  const uint8_t* a_src[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t R = 16 * wave + 8 * i + lrow;
-    a_src[i] = p.a + a_source(R) * K + ((lslot ^ ((R >> 1) & 7u)) << 4);
-  }
-  const uint8_t* w_src[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t R = 32 * wave + 8 * i + lrow;
-    w_src[i] = w_base + (uint64_t)w_row(R) * K + ((lslot ^ ((R >> 1) & 7u)) << 4);
-  }
-  // Scales ride in registers: thread t < 128 loads the A scale of tile row
-  // t, threads 128 and 129 the two W block scales, every other thread the
-  // A scale of row t & 127 again, so each thread issues exactly seven
-  // vector loads per step (the wait counts below rely on it).
-  constexpr uint32_t ESZ = SCALE == kScaleUe8m0 ? 1 : 4;
-  const uint8_t* s_src = static_cast<const uint8_t*>(p.a_scale) + sa_off * ESZ;
-  if (tid == BM) s_src = static_cast<const uint8_t*>(p.w_scale) + ws0_off * ESZ;
-  if (tid == BM + 1) s_src = static_cast<const uint8_t*>(p.w_scale) + ws1_off * ESZ;
-  uint32_t sreg[STAGES];
-  auto issue = [&](int stage, uint32_t kb) {
-    const uint64_t o = (uint64_t)kb * 128;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      dma16(a_src[i] + o, sA(stage) + wv * 2048 + i * 1024);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(w_src[i] + o, sB(stage) + wv * 4096 + i * 1024);
-    if constexpr (SCALE == kScaleUe8m0) sreg[stage] = s_src[kb];
-    else sreg[stage] = reinterpret_cast<const uint32_t*>(s_src)[kb];
-  };
-  auto sstore = [&](int stage) {
-    if (tid < BM) {
-      sSa(stage)[(tid >> 6) * 64 + (tid & 15) * 4 + ((tid >> 4) & 3)] = sreg[stage];
-      if constexpr (SCALE == kScaleUe8m0)
-        if (sreg[stage] == 0xffu && tid < rows) bad |= kErrScale;
-    } else if (tid < BM + 2) {
-      sSw(stage)[tid - BM] = sreg[stage];
-      if constexpr (SCALE == kScaleUe8m0)
-        if (sreg[stage] == 0xffu) bad |= kErrScale;
-    }
-  };
 
   v4f acc[4][4];  // [W block nb][A block rb]
 #pragma unroll
@@ -339,8 +372,13 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int stage) {
-    if (rb_live == 0) return;
+  auto compute = [&](auto STG, uint32_t kb, auto FULL) __attribute__((always_inline)) {
+    constexpr uint32_t stage = decltype(STG)::value;
+    constexpr bool kFull = decltype(FULL)::value;
+    if (!kFull && rb_live == 0) return;
+    const uint8_t* sA = smem + stage * STAGE;
+    const uint8_t* sB = sA + A_BYTES;
+    const uint32_t* sS = reinterpret_cast<const uint32_t*>(sB + W_BYTES);
     // operand fragments: lane (lr, lg) holds row lr, bytes [16lg, 16lg+16)
     // and [64+16lg, 64+16lg+16) of the step (the same map for both); the
     // fragment rows start at multiples of 16, so the slot of chunk lg is
@@ -349,32 +387,36 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     v8i wf[4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const uint8_t* pb = sB(stage) + (wn * 64 + nb * 16 + lr) * LDS_ROW;
+      const uint8_t* pb = sB + (wn * 64 + nb * 16 + lr) * LDS_ROW;
       wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb + rd0), *reinterpret_cast<const v4i*>(pb + (rd0 ^ 64)));
     }
-    const v4i sa4 = *reinterpret_cast<const v4i*>(sSa(stage) + wm * 64 + lr * 4);
-    const uint32_t sw0 = sSw(stage)[kSwi ? 0 : (wn >> 1)];
-    const uint32_t sw1 = sSw(stage)[kSwi ? 1 : (wn >> 1)];
+    const v4i sa4 = *reinterpret_cast<const v4i*>(sS + wm * 64 + lr * 4);
+    // W block scales of this wave's columns: SwiGLU gate (block 0) and up
+    // (block 1); otherwise the 128-row block holding columns wn*64 ..
+    constexpr bool kSw = kSwi;
+    const uint32_t wsel0 = kSw ? 0u : (wn >> 1), wsel1 = kSw ? 1u : (wn >> 1);
+    const uint32_t sw0 = sS[128 + wsel0], sw1 = sS[128 + wsel1];
     auto a_frag = [&](int r) -> v8i {
-      const uint8_t* pa = sA(stage) + (wm * 64 + r * 16 + lr) * LDS_ROW;
+      const uint8_t* pa = sA + (wm * 64 + r * 16 + lr) * LDS_ROW;
       return cat8(*reinterpret_cast<const v4i*>(pa + rd0), *reinterpret_cast<const v4i*>(pa + (rd0 ^ 64)));
     };
+    auto live = [&](int r) { return kFull || r < (int)rb_live; };
     if constexpr (SCALE == kScaleF32) {
       // fp32 scales: each MFMA starts from zero and its result is added
       // with one FMA per output.  Software-pipelined: the four MFMAs of A
       // block r + 1 are issued before the FMAs of block r, so those read
       // results that finished while the next MFMAs ran (consuming a result
       // right after its MFMA stalls the wave for the MFMA's latency).
+      const float fw0 = __uint_as_float(sw0), fw1 = __uint_as_float(sw1);
       auto mfma4 = [&](const v8i& af, v4f (&t)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
           t[nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[nb], af, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
                                                                    127, 0, 127);
       };
-      auto fma4 = [&](auto R, const v4f (&t)[4]) __attribute__((always_inline)) {
-        constexpr int r = decltype(R)::value;
+      auto fma4 = [&](int r, const v4f (&t)[4]) __attribute__((always_inline)) {
         const float sa = __uint_as_float((uint32_t)sa4[r]);
-        const float c0 = sa * __uint_as_float(sw0), c1 = sa * __uint_as_float(sw1);
+        const float c0 = sa * fw0, c1 = sa * fw1;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
           const float c = (kSwi && nb >= 2) ? c1 : c0;
@@ -382,40 +424,51 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
           for (int i = 0; i < 4; ++i) acc[nb][r][i] = __builtin_fmaf(t[nb][i], c, acc[nb][r][i]);
         }
       };
-      using I0 = std::integral_constant<int, 0>;
-      using I1 = std::integral_constant<int, 1>;
-      using I2 = std::integral_constant<int, 2>;
-      using I3 = std::integral_constant<int, 3>;
+      // A fragments are read one block ahead
       v4f tA[4], tB[4];
-      const v8i af0 = a_frag(0), af1 = a_frag(1);
-      mfma4(af0, tA);
+      v8i af = a_frag(0), afn = a_frag(1);
+      mfma4(af, tA);
       __builtin_amdgcn_sched_barrier(0);
-      if (rb_live > 1) mfma4(af1, tB);
-      const v8i af2 = a_frag(2), af3 = a_frag(3);
-      fma4(I0{}, tA);
+      af = a_frag(2);
+      if (live(1)) mfma4(afn, tB);
       __builtin_amdgcn_sched_barrier(0);
-      if (rb_live > 2) mfma4(af2, tA);
-      if (rb_live > 1) fma4(I1{}, tB);
+      fma4(0, tA);
+      afn = a_frag(3);
       __builtin_amdgcn_sched_barrier(0);
-      if (rb_live > 3) mfma4(af3, tB);
-      if (rb_live > 2) fma4(I2{}, tA);
+      if (live(2)) mfma4(af, tA);
       __builtin_amdgcn_sched_barrier(0);
-      if (rb_live > 3) fma4(I3{}, tB);
+      if (live(1)) fma4(1, tB);
+      __builtin_amdgcn_sched_barrier(0);
+      if (live(3)) mfma4(afn, tB);
+      __builtin_amdgcn_sched_barrier(0);
+      if (live(2)) fma4(2, tA);
+      __builtin_amdgcn_sched_barrier(0);
+      if (live(3)) fma4(3, tB);
     } else {
       // UE8M0 scales ride in the MFMA's E8M0 operands and the MFMAs chain on
-      // the accumulator
+      // the accumulator; a 255 scale raises the scale bit and runs as 0
+      // (2^-127), contributing nothing, as the reference skips the block
+      const uint32_t wsh0 = 8 * ((w_byte0[wsel0] + kb) & 3u), wsh1 = 8 * ((w_byte0[wsel1] + kb) & 3u);
+      uint32_t wsb0 = (sw0 >> wsh0) & 0xffu, wsb1 = (sw1 >> wsh1) & 0xffu;
+      if (wsb0 == 0xffu || wsb1 == 0xffu) bad |= kErrScale;
+      wsb0 = wsb0 == 0xffu ? 0u : wsb0;
+      wsb1 = wsb1 == 0xffu ? 0u : wsb1;
       auto mma = [&](int r, const v8i& af) {
-        const int sb = (int)sa4[r];
+        uint32_t sb = ((uint32_t)sa4[r] >> (8 * ((a_byte0[r] + kb) & 3u))) & 0xffu;
+        if (sb == 0xffu) {
+          bad |= kErrScale;
+          sb = 0;
+        }
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
           acc[nb][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wf[nb], af, acc[nb][r], 0, 0, 0, (int)((kSwi && nb >= 2) ? sw1 : sw0), 0, sb);
+              wf[nb], af, acc[nb][r], 0, 0, 0, (int)((kSwi && nb >= 2) ? wsb1 : wsb0), 0, (int)sb);
       };
       // A fragments one block ahead (at most four LDS reads in flight)
       v8i af = a_frag(0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        if (r < (int)rb_live) {
+        if (live(r)) {
           const v8i afn = a_frag(r < 3 ? r + 1 : 3);
           mma(r, af);
           af = afn;
@@ -425,29 +478,32 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
   };
 
-  // Three LDS stages, loads two steps ahead.  Step j: wait until at most
-  // the seven loads of step j + 1 are in flight (step j's tiles and scale
-  // registers have landed), publish step j's scales, barrier (every wave's
-  // DMA for step j is visible and step j - 1's compute is done, so its stage
-  // may be refilled), issue step j + 2 into that stage, compute step j.
-  // Loads past the last step re-read it into a stage that is never used.
+  // Three LDS stages, loads two steps ahead.  The loads issued at step j are
+  // the seven DMAs of step j + 2.  Step j: wait until at most seven loads
+  // are in flight (step j + 1's: step j's tiles and scales have landed),
+  // barrier (every wave's DMA for step j is visible and step j - 1's compute
+  // is done, so its stage may be refilled), issue, compute step j.  Loads
+  // past the last step re-read it (into a stage that is never used).  The
+  // loads are issued by inline asm, so the compiler adds no waits of its
+  // own.  (A per-step L2 prefetch of a later step, one 4-byte load per lane
+  // and line, measured slower: the tiles already hit L2 about nine times in
+  // ten, and the extra load lengthens every wait.)
   const uint32_t last = KB - 1;
   issue(0, 0);
   issue(1, min(1u, last));
-#define PIH_MOE_STEP(J, TAIL)                                           \
-  {                                                                     \
-    const uint32_t j = kb + (J);                                        \
-    if ((TAIL) && j >= KB) goto done;                                   \
-    __builtin_amdgcn_s_waitcnt(kWaitVm7);                               \
-    sstore((J) % 3);                                                    \
-    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);                             \
-    __builtin_amdgcn_s_barrier();                                       \
-    issue(((J) + 2) % 3, min(j + 2, last));                             \
-    compute((J) % 3);                                                   \
+  // Six steps per trip (stages fixed at compile time, so every LDS address
+  // is a per-lane base plus an immediate); whole tiles (all 128 A rows) run
+  // a compute without per-block guards.
+  auto run = [&](auto FULL) __attribute__((always_inline)) {
+#define PIH_MOE_STEP(J, TAIL)                                                                        \
+  {                                                                                                  \
+    const uint32_t j = kb + (J);                                                                     \
+    if ((TAIL) && j >= KB) return;                                                                   \
+    __builtin_amdgcn_s_waitcnt(kWaitVm7);                                                            \
+    __builtin_amdgcn_s_barrier();                                                                    \
+    issue(((J) + 2) % 3, min(j + 2, last));                                                          \
+    compute(std::integral_constant<uint32_t, (J) % 3>{}, j, FULL);                                   \
   }
-  {
-    // six steps per trip: only the first LDS accesses after the loop
-    // header get a conservative full wait from the compiler
     uint32_t kb = 0;
     for (; kb + 6 < KB; kb += 6) {
       PIH_MOE_STEP(0, false)
@@ -463,9 +519,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     PIH_MOE_STEP(3, true)
     PIH_MOE_STEP(4, true)
     PIH_MOE_STEP(5, true)
-  }
 #undef PIH_MOE_STEP
-done:
+  };
+  if (rb_live == 4) run(std::true_type{});
+  else run(std::false_type{});
   // no DMA may still target this block's LDS when its waves end
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
@@ -656,6 +713,9 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
   const uint64_t mt = (uint64_t)a.m / BM + (a.problems < a.m ? a.problems : a.m);
   const uint64_t total = mt * mp.n_tiles;
   if (total == 0 || total > 0x7fffffffull - 8) return Invalid("fp8_gemm_grid_too_large");
+  // the tile loads address A and one expert's W by 32-bit byte offsets
+  if ((uint64_t)a.a_rows_total * a.k > 0xffffffffull || (uint64_t)a.n * a.k > 0xffffffffull)
+    return Invalid("fp8_moe_gemm_operand_too_large");
   const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
   St s = RequireCleanLastError();
   if (!s.ok()) return s;
