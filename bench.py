@@ -26,6 +26,7 @@ sample of the same routed rows.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -199,16 +200,26 @@ QWEN8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4
 
 
 def _timed(torch, fn, iters: int):
-    """Mean ms per call of fn(i) measured with HIP events on the launch stream."""
+    """Mean ms per call of fn(i) measured with HIP events on the launch stream.
+    The Python garbage collector is off meanwhile: the eager decode loops
+    launch from Python, and a collection pass inside the timed region
+    (measured: one ~50 ms stall in 30 passes) idles the GPU."""
     s = torch.cuda.current_stream()
     fn(0)
     s.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(s)
-    for i in range(iters):
-        fn(i)
-    ev1.record(s)
-    ev1.synchronize()
+    gc_was_on = gc.isenabled()
+    gc.collect()
+    gc.disable()
+    try:
+        ev0.record(s)
+        for i in range(iters):
+            fn(i)
+        ev1.record(s)
+        ev1.synchronize()
+    finally:
+        if gc_was_on:
+            gc.enable()
     return ev0.elapsed_time(ev1) / iters
 
 

@@ -262,9 +262,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
 //   * a wave loads its own slice of x (rows < M, its K run) first, then its
 //     first U steps of W, then writes x to a wave-private LDS area: waiting
 //     for x leaves W in flight, and no block barrier precedes the math;
-//   * the group scales of a batch arrive in one vector load (U bf16 / fp16
-//     values of the lane's row) and the zero points in one u32, instead of
-//     two scalar-per-step loads that cost more than the nibble math;
+//   * the group scales of a batch arrive in vector loads (U bf16 / fp16
+//     values of the lane's row) and the zero points in one or two u32,
+//     instead of two scalar-per-step loads that cost more than the nibble
+//     math;
+//   * even U: W arrives as whole 128-byte lines and turns into the MFMA
+//     layout through one wave-private LDS tile, reused pair after pair (one
+//     tile instead of U / 2 lets 4 rather than 3 blocks of 4 waves share a
+//     CU: Qwen3-8B gate+up at m = 1, 13.1 -> 11.6 us);
 //   * INT4: the 32 nibbles of a lane's 16-byte piece become bf16 (128 + u)
 //     values with two masks and four v_perm per 8 nibbles (x is staged in
 //     the matching k order), four MFMAs give sum_k x (128 + u), and the
@@ -312,14 +317,21 @@ template <int U>
 struct ScaleVec {
   uint32_t w[(U + 1) / 2];
   __device__ __forceinline__ void load(const uint16_t* p) {
-    if constexpr (U == 8) {
-      const v4i v = *reinterpret_cast<const v4i*>(p);
-      w[0] = v[0], w[1] = v[1], w[2] = v[2], w[3] = v[3];
-    } else if constexpr (U == 4) {
-      const uint2 v = *reinterpret_cast<const uint2*>(p);
-      w[0] = v.x, w[1] = v.y;
-    } else if constexpr (U == 2) {
-      w[0] = *reinterpret_cast<const uint32_t*>(p);
+    if constexpr (U % 8 == 0) {
+#pragma unroll
+      for (int i = 0; i < U / 8; ++i) {
+        const v4i v = reinterpret_cast<const v4i*>(p)[i];
+        w[4 * i] = v[0], w[4 * i + 1] = v[1], w[4 * i + 2] = v[2], w[4 * i + 3] = v[3];
+      }
+    } else if constexpr (U % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < U / 4; ++i) {
+        const uint2 v = reinterpret_cast<const uint2*>(p)[i];
+        w[2 * i] = v.x, w[2 * i + 1] = v.y;
+      }
+    } else if constexpr (U % 2 == 0) {
+#pragma unroll
+      for (int i = 0; i < U / 2; ++i) w[i] = reinterpret_cast<const uint32_t*>(p)[i];
     } else {
       w[0] = *p;
     }
@@ -335,7 +347,7 @@ constexpr uint32_t kWTileRow = 144, kWTile = 16 * kWTileRow;
 
 template <int FMT>
 constexpr uint32_t small_m_lds(uint32_t m, uint32_t spw, uint32_t waves, uint32_t u) {
-  const uint32_t wtile = u % 2 == 0 ? u / 2 * kWTile : 0;
+  const uint32_t wtile = u % 2 == 0 ? kWTile : 0;
   return waves * (wtile + m * spw * step_k<FMT>() * 2 + (FMT != kWBf16 ? spw * 16 * 4 : 0)) + waves * 4 * 64 * 4;
 }
 
@@ -349,7 +361,7 @@ struct GemvGroup {
   uint32_t count;
 };
 
-template <int FMT, int WAVES, int U>
+template <int FMT, int WAVES, int U, bool ONE_ROW>
 __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uint32_t spw) {
   extern __shared__ __align__(16) uint8_t smem[];
   // this block's problem: selected field by field with constant indices
@@ -365,7 +377,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
   const uint32_t block = blockIdx.x - grp.block_start[pi];
   constexpr bool kInt4 = FMT != kWBf16;
   constexpr uint32_t SK = step_k<FMT>();
-  constexpr int XR = 8;  // x chunks per lane loaded ahead of the weights (M * spw * 16 <= 512)
+  // x chunks per lane loaded ahead of the weights: M * spw * 16 <= 512, or
+  // (ONE_ROW: m = 1 and the wave's run is one batch) spw * SK / 8 <= 64 * XR
+  constexpr int XR = ONE_ROW ? (U + 3) / 4 : 8;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
   const uint32_t n0 = block * 16, nrow = n0 + lr;
@@ -378,7 +392,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
   // 64 B per step) through an LDS tile.  Loading the MFMA layout directly
   // touches 16 half lines per instruction and streamed ~17 % slower.
   constexpr bool kT = U % 2 == 0;
-  constexpr uint32_t kWBytes = kT ? U / 2 * kWTile : 0;
+  constexpr uint32_t kWBytes = kT ? kWTile : 0;
   // wave-private LDS: W tiles, x[M][span] bf16, then (INT4) row sums [spw][16]
   const uint32_t wave_bytes = kWBytes + M * span * 2 + (kInt4 ? spw * 16 * 4 : 0);
   uint8_t* wt = smem + wave * wave_bytes;
@@ -405,12 +419,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
   // ---- first batch of W, its scales and zero points
   v4i wv[U];
   ScaleVec<U> sv;
-  uint32_t zw = 0;
+  uint32_t zw = 0, zw1 = 0;
+  constexpr bool kTwoZeroWords = 8 % U != 0;  // a batch may span two words of 8 zero points
   // scales and zero points go first: loads complete in issue order, so the
   // math of step 0 then waits only for W[0], not for the whole batch
   auto issue = [&](uint32_t sb) {
     if constexpr (kInt4) sv.load(p.scales + (uint64_t)nrow * G + sb);
-    if constexpr (FMT == kWAsym) zw = p.zeros[(uint64_t)nrow * zwords + sb / 8];
+    if constexpr (FMT == kWAsym) {
+      zw = p.zeros[(uint64_t)nrow * zwords + sb / 8];
+      if constexpr (kTwoZeroWords) zw1 = p.zeros[(uint64_t)nrow * zwords + min(sb / 8 + 1, zwords - 1)];
+    }
     if constexpr (kT) {
       // load 2q + h: rows n0 + 8h + lane / 8, bytes [64 (sb + 2q), +128) of
       // the row, 16 of them per lane
@@ -439,7 +457,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
   // u + 1) through the LDS tile into the MFMA layout of steps u and u + 1.
   auto to_mfma_layout = [&](int u) {
     if constexpr (kT) {
-      uint8_t* tile = wt + (u / 2) * kWTile;
+      uint8_t* tile = wt;  // one tile per wave: a wave's LDS accesses complete in order
       *reinterpret_cast<v4i*>(tile + (lane / 8) * kWTileRow + (lane % 8) * 16) = wv[u];
       *reinterpret_cast<v4i*>(tile + (8 + lane / 8) * kWTileRow + (lane % 8) * 16) = wv[u + 1];
       wv[u] = *reinterpret_cast<const v4i*>(tile + lr * kWTileRow + lg * 16);
@@ -511,7 +529,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
           zero = 8;
         } else {
           sc = bf16_bits_to_f32(sv.bits(u));
-          zero = (int)((zw >> (4 * (st % 8))) & 0xfu);
+          const uint32_t zword = kTwoZeroWords && (st / 8 != sb / 8) ? zw1 : zw;
+          zero = (int)((zword >> (4 * (st % 8))) & 0xfu);
         }
         if (!(sc > 0.0f) || !__builtin_isfinite(sc)) bad = bad ? bad : kQwenBadScale;
         uint32_t wd[4] = {(uint32_t)wv[u][0], (uint32_t)wv[u][1], (uint32_t)wv[u][2], (uint32_t)wv[u][3]};
@@ -533,8 +552,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_lds_kernel(GemvGroup grp, uin
                                                        __builtin_bit_cast(v8bf, qb[i]), pq, 0, 0, 0);
         // rows >= M (copies of row M - 1, stale row sums) are never stored
         const float zc = 128.0f + (float)zero;
+        // m = 1: only MFMA row 0 (acc[0] of lanes 0..15) is ever stored
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = __builtin_fmaf(__builtin_fmaf(-zc, xsv[i], pq[i]), sc, acc[i]);
+        for (int i = 0; i < (ONE_ROW ? 1 : 4); ++i)
+          acc[i] = __builtin_fmaf(__builtin_fmaf(-zc, xsv[i], pq[i]), sc, acc[i]);
       }
     }
   };
@@ -876,33 +897,53 @@ void launch_mt(const GemvParams& p, int waves, hipStream_t s) {
   else hipLaunchKernelGGL((gemv_kernel<FMT, MT, 16>), grid, dim3(1024), 0, s, p);
 }
 
-template <int FMT, int WAVES, int U>
+template <int FMT, int WAVES, int U, bool ONE_ROW>
 St launch_lds(const GemvGroup& g, uint32_t spw, hipStream_t s) {
   const uint32_t lds = small_m_lds<FMT>(g.prob[0].m, spw, WAVES, U);
   static bool raised = false;  // LDS above 64 KB must be allowed once per kernel
   if (lds > 65536 && !raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_lds_kernel<FMT, WAVES, U>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_lds_kernel<FMT, WAVES, U, ONE_ROW>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
       return Internal("gemv_lds_attribute_failed");
     raised = true;
   }
-  hipLaunchKernelGGL((gemv_lds_kernel<FMT, WAVES, U>), dim3(g.block_start[g.count]), dim3(WAVES * 64), lds, s, g,
-                     spw);
+  hipLaunchKernelGGL((gemv_lds_kernel<FMT, WAVES, U, ONE_ROW>), dim3(g.block_start[g.count]), dim3(WAVES * 64), lds, s,
+                     g, spw);
   return AfterLaunch("gemv_launch_failed");
 }
 
 // Waves per block and steps per batch for the LDS kernel: the waves split
-// the K steps evenly (WAVES divides steps); among 4, 8, 12 and 16 waves take
-// the first that gives the grid >= 2048 waves (m = 1) or at most 4 steps per
-// wave (m >= 2: each wave stages m rows of x for its run before its first
-// step, so shorter runs measured faster, e.g. 16.7 vs 19.6 us for Qwen3-8B
-// gate+up at m = 4), else the largest that divides; U is the largest of 8,
-// 4, 2, 1 dividing the steps per wave.  Returns false when no split divides
-// the steps.
+// the K steps evenly (WAVES divides steps).
+//   INT4, m = 1: the most of 4, 8, 12 waves whose grid still fits one
+//     resident round (<= 4096 waves: 16 per CU on 256 CUs), each wave's run
+//     one batch of 1, 2, 4, 6, 8 or 12 steps, so every load of the launch is
+//     issued before any wave waits (Qwen3-8B down, K = 12288: 12 waves x 8
+//     steps measured 7.7 us against 8.6 us for 8 waves x 12 steps in three
+//     batches of 4; 16 waves x 6 steps ran as fast but spills registers).
+//   Otherwise: the first of 4, 8, 12, 16 that gives the grid >= 2048 waves
+//     (m = 1) or at most 4 steps per wave (m >= 2: each wave stages m rows
+//     of x for its run before its first step, so shorter runs measured
+//     faster, e.g. 16.7 vs 19.6 us for Qwen3-8B gate+up at m = 4), else the
+//     largest that divides; U is the largest of 8, 4, 2, 1 dividing the
+//     steps per wave.
+// Returns false when no split divides the steps.
 template <int FMT>
 bool pick_lds_split(uint32_t rowblks, uint32_t k, uint32_t m, int& waves, uint32_t& spw, int& u) {
   const uint32_t steps = k / step_k<FMT>();
   waves = 0;
+  if (FMT != kWBf16 && m == 1) {
+    for (int w : {4, 8, 12}) {
+      const uint32_t run = steps / (uint32_t)w;
+      if (steps % (uint32_t)w || (run != 1 && run != 2 && run != 4 && run != 6 && run != 8 && run != 12)) continue;
+      if (waves && rowblks * (uint32_t)w > 4096) break;
+      waves = w;
+    }
+    if (waves) {
+      spw = steps / waves;
+      u = (int)spw;
+      return true;
+    }
+  }
   for (int w : {4, 8, 12, 16}) {
     if (steps % (uint32_t)w) continue;
     waves = w;
@@ -916,10 +957,19 @@ bool pick_lds_split(uint32_t rowblks, uint32_t k, uint32_t m, int& waves, uint32
 
 template <int FMT, int WAVES>
 St launch_lds_u(const GemvGroup& g, uint32_t spw, int u, hipStream_t s) {
-  if (u == 8) return launch_lds<FMT, WAVES, 8>(g, spw, s);
-  if (u == 4) return launch_lds<FMT, WAVES, 4>(g, spw, s);
-  if (u == 2) return launch_lds<FMT, WAVES, 2>(g, spw, s);
-  return launch_lds<FMT, WAVES, 1>(g, spw, s);
+  const bool one = g.prob[0].m == 1 && spw == (uint32_t)u;
+  if constexpr (FMT != kWBf16) {
+    // batches of 12 and 6 steps come only from the INT4 m = 1 rule (one
+    // batch per wave, at most 12 waves: 16 waves of 6 or 12 steps spill)
+    if constexpr (WAVES <= 12) {
+      if (u == 12) return launch_lds<FMT, WAVES, 12, true>(g, spw, s);
+      if (u == 6) return launch_lds<FMT, WAVES, 6, true>(g, spw, s);
+    }
+  }
+  if (u == 8) return one ? launch_lds<FMT, WAVES, 8, true>(g, spw, s) : launch_lds<FMT, WAVES, 8, false>(g, spw, s);
+  if (u == 4) return one ? launch_lds<FMT, WAVES, 4, true>(g, spw, s) : launch_lds<FMT, WAVES, 4, false>(g, spw, s);
+  if (u == 2) return one ? launch_lds<FMT, WAVES, 2, true>(g, spw, s) : launch_lds<FMT, WAVES, 2, false>(g, spw, s);
+  return launch_lds<FMT, WAVES, 1, false>(g, spw, s);
 }
 
 // The small-M path for a group (every problem has the same m and k);
