@@ -68,6 +68,17 @@ __device__ __forceinline__ uint32_t e4m3_quant4(const float* v, float scale) {
   return (uint32_t)w;
 }
 
+// e4m3_quant4 with the scale given as its exact reciprocal (a power of two):
+// codes of v[0..3] * inv.
+__device__ __forceinline__ uint32_t e4m3_quant4_mul(const float* v, float inv) {
+  float q[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q[i] = fminf(fmaxf(v[i] * inv, -448.0f), 448.0f);
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w, true);
+  return (uint32_t)w;
+}
+
 __device__ __forceinline__ uint32_t e4m3_encode(float v) {
   const uint32_t raw = __float_as_uint(v);
   const uint32_t sign = (raw >> 24) & 0x80u;

@@ -195,6 +195,10 @@ struct RoutePlanArgs {
   uint32_t tokens = 0, topk = 0, experts = 0;
 };
 St LaunchRoutePlan(const RoutePlanArgs& a);
+// The route plan whose first launch also quantizes the token activations
+// (quant: input [tokens, k] bf16, no row gather, same stream and error flag)
+// -- the MoE layer's activation quant without a launch of its own.
+St LaunchRoutePlanWithQuant(const RoutePlanArgs& a, const Fp8QuantArgs& quant);
 uint64_t RoutePlanWorkspaceBytes(uint32_t tokens, uint32_t topk, uint32_t experts);
 // LaunchRoutePlan with the pack's own per-device scratch array instead of a
 // caller workspace (a.workspace and a.workspace_bytes must be 0); plans

@@ -6,8 +6,12 @@
 // (deepseek_expert_subwave_plan.cpp:32-101).  Here every stage is one launch
 // over all experts, enqueued back to back on the caller's stream with no
 // host synchronisation:
-//   route plan -> activation quant -> grouped gate/up GEMM (+ SwiGLU x route
+//   route plan + activation quant -> grouped gate/up GEMM (+ SwiGLU x route
 //   weight) -> intermediate quant -> grouped down GEMM -> ordered combine.
+// The activation quant does not depend on the routing, so its blocks ride in
+// the route plan's first launch (the route-mask blocks first); it is not a
+// prologue of the gate/up GEMM because every token row feeds top_k experts
+// times n / 256 tiles there and would be quantised that many times over.
 // FP8 weights fold the intermediate quant into the gate/up epilogue (one
 // launch and the bf16 intermediate's write and read fewer); it quantises the
 // bf16-rounded SwiGLU values with the quant entry's arithmetic, so the
@@ -117,9 +121,8 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
   rp.tokens = a.tokens;
   rp.topk = a.topk;
   rp.experts = a.experts;
-  if (!(s = LaunchRoutePlan(rp)).ok()) return s;
 
-  auto quant = [&](const uint16_t* in, uint32_t rows, uint32_t k, uint64_t codes, uint64_t scales) {
+  auto quant_args = [&](const uint16_t* in, uint32_t rows, uint32_t k, uint64_t codes, uint64_t scales) {
     Fp8QuantArgs q;
     q.input = in;
     q.codes = at(codes);
@@ -130,9 +133,12 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
     q.k = k;
     q.input_rows = rows;
     q.fmt = act_fmt;
-    return LaunchFp8Quant(q);
+    return q;
   };
-  if (c.quant_x && !(s = quant(a.x, a.tokens, a.hidden, c.xq, c.xs)).ok()) return s;
+  // the token activations are quantized by the route plan's first launch
+  if (c.quant_x) s = LaunchRoutePlanWithQuant(rp, quant_args(a.x, a.tokens, a.hidden, c.xq, c.xs));
+  else s = LaunchRoutePlan(rp);
+  if (!s.ok()) return s;
 
   // gate/up: logical row r reads token row_token[r]; SwiGLU x route weight
   auto gemm = [&](bool gate_up) -> St {
@@ -190,7 +196,7 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
     return LaunchFp4Gemm(g);
   };
   if (!(s = gemm(true)).ok()) return s;
-  if (!fp8 && c.quant_mid && !(s = quant(mid, R, a.inter, c.mq, c.ms)).ok()) return s;
+  if (!fp8 && c.quant_mid && !(s = LaunchFp8Quant(quant_args(mid, R, a.inter, c.mq, c.ms))).ok()) return s;
   if (!(s = gemm(false)).ok()) return s;
 
   CombineArgs cb;

@@ -20,6 +20,7 @@
 #include <mutex>
 
 #include "device_common.hpp"
+#include "fp8_quant_device.hpp"
 #include "kernels.hpp"
 
 // Scratch of the no-allocation route plan (LaunchRoutePlanNoAlloc): the
@@ -61,41 +62,84 @@ __device__ __forceinline__ uint32_t route_expert(const uint32_t* ids, const floa
   return e;
 }
 
-__global__ __launch_bounds__(kChunk) void route_mask_kernel(const uint32_t* ids, const float* weights,
-                                                            unsigned long long* masks,
-                                                            uint32_t* err, uint32_t tokens,
-                                                            uint32_t topk, uint32_t experts) {
-  __shared__ unsigned long long s_mask[kMaxExperts];
-  const uint32_t lane = threadIdx.x, chunk = blockIdx.x;
-  for (uint32_t e = lane; e < experts; e += kChunk) s_mask[e] = 0ull;
+// Chunk `chunk` of 64 tokens: the 64-bit token mask of every expert, built
+// with LDS atomics (order independent) by the block's waves, wave w taking
+// the routes j = w, w + waves, ...; s_mask holds `experts` words.
+__device__ __forceinline__ void route_mask_chunk(const uint32_t* ids, const float* weights, unsigned long long* masks,
+                                                 unsigned long long* s_mask, uint32_t* err, uint32_t chunk,
+                                                 uint32_t tokens, uint32_t topk, uint32_t experts) {
+  const uint32_t lane = threadIdx.x & (kChunk - 1), wave = threadIdx.x / kChunk, waves = blockDim.x / kChunk;
+  for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) s_mask[e] = 0ull;
   __syncthreads();
   const uint32_t t = chunk * kChunk + lane;
   uint32_t bad = 0;
   if (t < tokens) {
-    for (uint32_t j = 0; j < topk; ++j) {
+    for (uint32_t j = wave; j < topk; j += waves) {
       const uint32_t e = route_expert(ids, weights, t, j, topk, experts, bad);
       if (e != kNoRow) atomicOr(&s_mask[e], 1ull << lane);
     }
   }
   __syncthreads();
-  for (uint32_t e = lane; e < experts; e += kChunk) masks[(uint64_t)chunk * experts + e] = s_mask[e];
+  for (uint32_t e = threadIdx.x; e < experts; e += blockDim.x) masks[(uint64_t)chunk * experts + e] = s_mask[e];
   if (bad) atomicOr(err, bad);
 }
 
-// One block: per expert, chunk bases by a serial walk over chunks, then a
-// block-wide exclusive scan of the per-expert totals.
+__global__ __launch_bounds__(256) void route_mask_kernel(const uint32_t* ids, const float* weights,
+                                                         unsigned long long* masks, uint32_t* err, uint32_t tokens,
+                                                         uint32_t topk, uint32_t experts) {
+  extern __shared__ unsigned long long s_mask[];
+  route_mask_chunk(ids, weights, masks, s_mask, err, blockIdx.x, tokens, topk, experts);
+}
+
+// The MoE layer's first launch: blocks [0, chunks) build the route masks,
+// the blocks after them quantize the token activations (quant_groups over
+// the remaining blocks) -- two independent jobs in one launch, the route
+// blocks first so the plan's next launch can start as soon as possible.
+template <int FMT>
+__global__ __launch_bounds__(256) void route_mask_quant_kernel(const uint32_t* ids, const float* weights,
+                                                               unsigned long long* masks, uint32_t* err,
+                                                               uint32_t tokens, uint32_t topk, uint32_t experts,
+                                                               uint32_t chunks, const uint16_t* x, uint8_t* codes,
+                                                               void* scales, uint32_t hidden) {
+  extern __shared__ unsigned long long s_mask[];
+  if (blockIdx.x < chunks) {
+    route_mask_chunk(ids, weights, masks, s_mask, err, blockIdx.x, tokens, topk, experts);
+    return;
+  }
+  const uint64_t seg0 = ((uint64_t)(blockIdx.x - chunks) * blockDim.x + threadIdx.x) >> 4;
+  const uint64_t seg_step = ((uint64_t)(gridDim.x - chunks) * blockDim.x) >> 4;
+  const uint32_t bad = quant_groups<FMT, false>(x, nullptr, codes, scales, tokens, hidden, tokens, seg0, seg_step);
+  if (bad) atomicOr(err, bad);
+}
+
+// One block, one thread per expert: chunk bases by a walk over the chunks
+// (the masks of 16 chunks loaded before they are summed, so the walk waits
+// on memory once per 16 chunks), then a block-wide exclusive scan of the
+// per-expert totals.
 __global__ __launch_bounds__(kMaxExperts) void route_scan_kernel(const unsigned long long* masks,
                                                                  uint32_t* bases,
                                                                  uint32_t* offsets,
                                                                  uint32_t chunks,
                                                                  uint32_t experts) {
+  constexpr uint32_t kBatch = 16;
   __shared__ uint32_t s_scan[kMaxExperts];
   const uint32_t e = threadIdx.x;
   uint32_t total = 0;
   if (e < experts) {
-    for (uint32_t c = 0; c < chunks; ++c) {
-      bases[(uint64_t)c * experts + e] = total;
-      total += (uint32_t)__popcll(masks[(uint64_t)c * experts + e]);
+    for (uint32_t c0 = 0; c0 < chunks; c0 += kBatch) {
+      // unconditional loads (past the end: the last chunk again, not
+      // counted); a load under a branch would be waited for on the spot
+      unsigned long long mk[kBatch];
+#pragma unroll
+      for (uint32_t i = 0; i < kBatch; ++i) mk[i] = masks[(uint64_t)min(c0 + i, chunks - 1) * experts + e];
+      uint32_t pc[kBatch];
+#pragma unroll
+      for (uint32_t i = 0; i < kBatch; ++i) pc[i] = c0 + i < chunks ? (uint32_t)__popcll(mk[i]) : 0u;
+#pragma unroll
+      for (uint32_t i = 0; i < kBatch; ++i) {
+        if (c0 + i < chunks) bases[(uint64_t)(c0 + i) * experts + e] = total;
+        total += pc[i];
+      }
     }
   }
   s_scan[e] = total;
@@ -110,26 +154,27 @@ __global__ __launch_bounds__(kMaxExperts) void route_scan_kernel(const unsigned 
   if (e == experts - 1) offsets[experts] = s_scan[e];
 }
 
-__global__ __launch_bounds__(kChunk) void route_scatter_kernel(
+// One thread per route (t, j): its row is offset + chunk base + the number
+// of earlier tokens of its chunk that chose the same expert.
+__global__ __launch_bounds__(256) void route_scatter_kernel(
     const uint32_t* ids, const float* weights, const unsigned long long* masks,
     const uint32_t* bases, const uint32_t* offsets, uint32_t* row_token, float* row_weight,
     uint32_t* token_rows, uint32_t tokens, uint32_t topk, uint32_t experts) {
-  const uint32_t lane = threadIdx.x, chunk = blockIdx.x;
-  const uint32_t t = chunk * kChunk + lane;
-  if (t >= tokens) return;
+  const uint64_t r = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= (uint64_t)tokens * topk) return;
+  const uint32_t t = (uint32_t)(r / topk), j = (uint32_t)(r % topk);
+  const uint32_t chunk = t / kChunk, lane = t % kChunk;
   const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
-  uint32_t bad = 0;
-  for (uint32_t j = 0; j < topk; ++j) {
-    const uint32_t e = route_expert(ids, weights, t, j, topk, experts, bad);
-    uint32_t row = kNoRow;
-    if (e != kNoRow) {
-      const unsigned long long m = masks[(uint64_t)chunk * experts + e];
-      row = offsets[e] + bases[(uint64_t)chunk * experts + e] + (uint32_t)__popcll(m & below);
-      row_token[row] = t;
-      row_weight[row] = weights[(uint64_t)t * topk + j];
-    }
-    token_rows[(uint64_t)t * topk + j] = row;
+  uint32_t bad = 0;  // reported by the mask pass
+  const uint32_t e = route_expert(ids, weights, t, j, topk, experts, bad);
+  uint32_t row = kNoRow;
+  if (e != kNoRow) {
+    const unsigned long long m = masks[(uint64_t)chunk * experts + e];
+    row = offsets[e] + bases[(uint64_t)chunk * experts + e] + (uint32_t)__popcll(m & below);
+    row_token[row] = t;
+    row_weight[row] = weights[r];
   }
+  token_rows[r] = row;
 }
 
 // dst[r, :] = src[idx[r], :], 16 bytes per lane.
@@ -286,7 +331,11 @@ uint64_t RoutePlanWorkspaceBytes(uint32_t tokens, uint32_t topk, uint32_t expert
   return ((mask_bytes + 255) / 256) * 256 + base_bytes;
 }
 
-St LaunchRoutePlan(const RoutePlanArgs& a) {
+namespace {
+
+// The plan's three launches; with `quant`, the first launch also quantizes
+// the token activations (route_mask_quant_kernel).
+St EnqueueRoutePlan(const RoutePlanArgs& a, const Fp8QuantArgs* quant) {
   if (!a.topk_ids || !a.topk_weights || !a.expert_offsets || !a.row_token || !a.row_weight ||
       !a.token_rows || !a.workspace || !a.error_flag || !a.stream)
     return Invalid("route_plan_null_argument");
@@ -295,22 +344,51 @@ St LaunchRoutePlan(const RoutePlanArgs& a) {
     return Invalid("route_plan_shape_invalid");
   if (a.workspace_bytes < RoutePlanWorkspaceBytes(a.tokens, a.topk, a.experts))
     return Invalid("route_plan_workspace_too_small");
+  if (quant) {
+    if (!quant->input || !quant->codes || !quant->scales || quant->rows) return Invalid("fp8_quant_null_argument");
+    if (quant->row_count != a.tokens || quant->k == 0 || quant->k % 128u) return Invalid("fp8_quant_shape_invalid");
+    if (quant->fmt != kScaleF32 && quant->fmt != kScaleUe8m0) return Invalid("fp8_quant_scale_format_invalid");
+  }
   const uint32_t chunks = (a.tokens + kChunk - 1) / kChunk;
   const uint64_t mask_bytes = (uint64_t)chunks * a.experts * 8ull;
   auto* masks = static_cast<unsigned long long*>(a.workspace);
   auto* bases = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(a.workspace) +
                                             ((mask_bytes + 255) / 256) * 256);
+  const uint32_t lds = a.experts * 8u;
   St clean = RequireCleanLastError();
   if (!clean.ok()) return clean;
-  hipLaunchKernelGGL(route_mask_kernel, dim3(chunks), dim3(kChunk), 0, a.stream, a.topk_ids,
-                     a.topk_weights, masks, a.error_flag, a.tokens, a.topk, a.experts);
+  if (!quant) {
+    hipLaunchKernelGGL(route_mask_kernel, dim3(chunks), dim3(256), lds, a.stream, a.topk_ids, a.topk_weights, masks,
+                       a.error_flag, a.tokens, a.topk, a.experts);
+  } else {
+    const uint32_t grid = chunks + QuantBlocks((uint64_t)quant->row_count * (quant->k / 128u));
+    if (quant->fmt == kScaleUe8m0)
+      hipLaunchKernelGGL(route_mask_quant_kernel<kScaleUe8m0>, dim3(grid), dim3(256), lds, a.stream, a.topk_ids,
+                         a.topk_weights, masks, a.error_flag, a.tokens, a.topk, a.experts, chunks, quant->input,
+                         quant->codes, quant->scales, quant->k);
+    else
+      hipLaunchKernelGGL(route_mask_quant_kernel<kScaleF32>, dim3(grid), dim3(256), lds, a.stream, a.topk_ids,
+                         a.topk_weights, masks, a.error_flag, a.tokens, a.topk, a.experts, chunks, quant->input,
+                         quant->codes, quant->scales, quant->k);
+  }
   const uint32_t scan_threads = ((a.experts + 63) / 64) * 64;
   hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(scan_threads), 0, a.stream, masks, bases,
                      a.expert_offsets, chunks, a.experts);
-  hipLaunchKernelGGL(route_scatter_kernel, dim3(chunks), dim3(kChunk), 0, a.stream, a.topk_ids,
-                     a.topk_weights, masks, bases, a.expert_offsets, a.row_token, a.row_weight,
+  const uint64_t routes = (uint64_t)a.tokens * a.topk;
+  hipLaunchKernelGGL(route_scatter_kernel, dim3((uint32_t)((routes + 255) / 256)), dim3(256), 0, a.stream,
+                     a.topk_ids, a.topk_weights, masks, bases, a.expert_offsets, a.row_token, a.row_weight,
                      a.token_rows, a.tokens, a.topk, a.experts);
   return AfterLaunch("route_plan_launch_failed");
+}
+
+}  // namespace
+
+St LaunchRoutePlan(const RoutePlanArgs& a) { return EnqueueRoutePlan(a, nullptr); }
+
+St LaunchRoutePlanWithQuant(const RoutePlanArgs& a, const Fp8QuantArgs& quant) {
+  if (!quant.error_flag || quant.error_flag != a.error_flag || quant.stream != a.stream)
+    return Invalid("route_plan_quant_mismatch");
+  return EnqueueRoutePlan(a, &quant);
 }
 
 namespace {
