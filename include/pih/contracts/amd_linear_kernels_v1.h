@@ -253,7 +253,9 @@ typedef struct pih_amd_w4a16_grouped_launch_v1 {
  * route plan -> activation quant -> grouped gate/up GEMM with the SwiGLU x
  * route-weight epilogue -> intermediate quant -> grouped down GEMM ->
  * ordered combine (+ shared).  The output equals launching those entries
- * one by one in that order.
+ * one by one in that order; fewer launches run (the activation quant rides
+ * in the route plan's first launch, and with FP8 weights the intermediate
+ * quant in the gate/up epilogue).
  * FP8 weights: w13 e4m3 [E][2I][H] (gate rows, then up rows), w13_scale
  *   [E][2I/128][H/128], w2 e4m3 [E][H][I], w2_scale [E][H/128][I/128];
  *   scale_format applies to weights and activations.
