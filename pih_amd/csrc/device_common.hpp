@@ -68,6 +68,26 @@ __device__ __forceinline__ uint32_t e4m3_quant4(const float* v, float scale) {
   return (uint32_t)w;
 }
 
+// e4m3_quant4 for an fp32 scale with inv = 1 / scale (one IEEE division per
+// group instead of one per value): q0 = v * inv, the remainder v - q0 * scale
+// exactly by an FMA, q = q0 + remainder * inv (Markstein's correction step,
+// IBM J. Res. Dev. 34(1), 1990), sign of v kept for v = -0.  q can differ
+// from v / scale in the last fp32 bit, but for every bf16 v with |v| <= amax
+// and scale = max(amax, 1e-4) / 448, amax any positive bf16, the e4m3 code
+// is the same (an exhaustive check over all 1.07e9 pairs is in the tests).
+__device__ __forceinline__ uint32_t e4m3_quant4_recip(const float* v, float scale, float inv) {
+  float q[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float q0 = v[i] * inv;
+    const float rem = __builtin_fmaf(-q0, scale, v[i]);
+    q[i] = fminf(fmaxf(__builtin_copysignf(__builtin_fmaf(rem, inv, q0), v[i]), -448.0f), 448.0f);
+  }
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], w, true);
+  return (uint32_t)w;
+}
+
 // e4m3_quant4 with the scale given as its exact reciprocal (a power of two):
 // codes of v[0..3] * inv.
 __device__ __forceinline__ uint32_t e4m3_quant4_mul(const float* v, float inv) {

@@ -11,7 +11,8 @@
 // round-to-nearest-even.  A non-finite input sets bit 1 and counts as zero
 // magnitude (reference kernel behaviour); an exponent outside UE8M0 sets
 // bit 2 and uses scale 1.
-// fp32 form: s = max(amax,1e-4)/448, codes = e4m3(clamp(x/s, +-448)).
+// fp32 form: s = max(amax,1e-4)/448, codes = e4m3(clamp(x/s, +-448)); x/s
+// through e4m3_quant4_recip (same codes as the division for every input).
 //
 // One 16-lane segment owns one 128-column group (8 bf16 per lane, one
 // 16-byte load), so the amax reduction is four xor-shuffles; a segment
@@ -107,8 +108,9 @@ __device__ __forceinline__ uint32_t quant_groups(const uint16_t* __restrict__ in
         packed[0] = e4m3_quant4_mul(v, inv);
         packed[1] = e4m3_quant4_mul(v + 4, inv);
       } else {
-        packed[0] = e4m3_quant4(v, scale);
-        packed[1] = e4m3_quant4(v + 4, scale);
+        const float inv = 1.0f / scale;
+        packed[0] = e4m3_quant4_recip(v, scale, inv);
+        packed[1] = e4m3_quant4_recip(v + 4, scale, inv);
       }
       *reinterpret_cast<uint2*>(codes + (uint64_t)row[i] * k + kg[i] * 128u + sub * 8u) =
           make_uint2(packed[0], packed[1]);

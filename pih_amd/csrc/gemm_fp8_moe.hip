@@ -575,7 +575,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       if (rr >= rows) continue;
       float amax = fmaxf(fmaxf(s_amax[rr][0], s_amax[rr][1]), fmaxf(s_amax[rr][2], s_amax[rr][3]));
       amax = fmaxf(amax, 1.0e-4f);
-      float scale;
+      float scale, inv;  // inv: the exact 2^-e (UE8M0) or 1 / scale (fp32)
       const uint64_t g = (uint64_t)(row0 + rr) * groups + nt;
       if constexpr (SCALE == kScaleUe8m0) {
         int e = ue8m0_exponent(amax);
@@ -584,15 +584,19 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
           e = 0;
         }
         scale = ldexpf(1.0f, e);
+        inv = ldexpf(1.0f, -e);
         if (wn == 0 && lg == 0) static_cast<uint8_t*>(p.out_scale)[g] = (uint8_t)(e + 127);
       } else {
         scale = amax / 448.0f;
+        inv = 1.0f / scale;
         if (wn == 0 && lg == 0) static_cast<float*>(p.out_scale)[g] = scale;
       }
       uint8_t* dst = static_cast<uint8_t*>(p.out) + (uint64_t)(row0 + rr) * p.out_row_stride + nt * 128 + wn * 32 +
                      4 * lg;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) *reinterpret_cast<uint32_t*>(dst + h * 16) = e4m3_quant4(vq[r][h], scale);
+      for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<uint32_t*>(dst + h * 16) =
+            SCALE == kScaleUe8m0 ? e4m3_quant4_mul(vq[r][h], inv) : e4m3_quant4_recip(vq[r][h], scale, inv);
     }
   }
 #pragma unroll
