@@ -17,9 +17,10 @@
 //     (global_load_lds_dwordx4: no staging registers, no ds_write), as dense
 //     128-byte rows whose 16-byte chunk c sits in slot c ^ ((row >> 1) & 7):
 //     the 16 rows of one operand-fragment read hit 64 distinct banks;
-//   * three LDS stages (144 KB), loads issued two steps ahead, one barrier
-//     per step; the waits are explicit vmcnt counts (seven loads per thread
-//     and step), because the compiler does not order LDS reads after DMA;
+//   * three LDS stages (149 KB), loads issued two steps ahead, one barrier
+//     per step; the DMAs are inline asm and the waits explicit vmcnt counts
+//     (seven loads per wave and step), so the compiler adds no waits of its
+//     own before LDS reads;
 //   * the output is computed transposed, C^T = W . A^T: the MFMA's first
 //     operand is a 16-row W block and its second a 16-row A block, so a lane
 //     owns four consecutive output columns of one row.  That makes the fp32
@@ -37,7 +38,6 @@
 // an 8 M x 4 N grouping of the multi-tile ones cut the L2-miss bytes by
 // 9 % but ran 3 % slower than M-fastest groups of 32).
 #include <type_traits>
-
 
 #include "device_common.hpp"
 #include "kernels.hpp"
