@@ -294,7 +294,12 @@ pih_status_v1 VerifyPayloads(const uint8_t* file, const Layout& L, const Parsed&
   };
   const unsigned hw = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
   std::vector<std::thread> pool;
-  for (unsigned t = 1; t < hw; ++t) pool.emplace_back(work);
+  try {
+    for (unsigned t = 1; t < hw; ++t) pool.emplace_back(work);
+  } catch (...) {
+    // fewer threads than asked for: the records are shared out by the
+    // atomic counter, so the ones started (and this one) cover them all
+  }
   work();
   for (auto& t : pool) t.join();
   if (bad.load() == 1) return Precond("canonical payload checksum mismatch");
