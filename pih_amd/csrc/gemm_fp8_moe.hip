@@ -53,6 +53,9 @@ constexpr uint32_t STAGE = A_BYTES + W_BYTES + SA_BYTES + SW_BYTES, DUMMY_BYTES 
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
 // [6:4], lgkmcnt [11:8]; an all-ones field does not wait)
 constexpr int kWaitVm7 = 0x0F77;     // vmcnt(7)
+constexpr int kWaitVm6 = 0x0F76;     // vmcnt(6)
+// operand kinds: e4m3 with block scales, or bf16 (no scales)
+enum : int { kOpFp8 = 0, kOpBf16 = 1 };
 constexpr int kWaitVm0 = 0x0F70;     // vmcnt(0)
 
 // LDS byte address of a __shared__ object
@@ -103,6 +106,10 @@ struct MoeParams {
   uint32_t* err;
   void* out_scale;  // kOutSwiGluFp8: [rows, n / 256] group scales
   uint32_t m, n, k, experts, a_rows_total;
+  // dense: one problem of m rows, ceil(m / 128) M tiles (no offsets, no
+  // gather); 0 for MoE segments
+  uint32_t dense_m_tiles;
+  uint32_t write_nonfinite;  // store a non-finite result (and flag it)
   uint64_t out_row_stride;
   uint32_t n_tiles;
   float limit;
@@ -237,7 +244,26 @@ __device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, u
   return true;
 }
 
-template <int SCALE, int OUT>
+// Dense form: tile t of the M x N tile grid, each XCD (blocks b % 8) walking
+// one contiguous range, M-fastest in groups of GROUP_M so that concurrent
+// tiles share their W tile in L2.
+__device__ bool dense_tile(const MoeParams& p, uint32_t& row0, uint32_t& rows, uint32_t& nt) {
+  const uint32_t MT = p.dense_m_tiles, NTL = p.n_tiles;
+  const uint64_t T = (uint64_t)MT * NTL;
+  const uint32_t per = (uint32_t)((T + 7) / 8);
+  const uint32_t xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const uint64_t t = (uint64_t)xcd * per + jj;
+  if (jj >= per || t >= T) return false;
+  const uint32_t mg = (uint32_t)(t / ((uint64_t)GROUP_M * NTL));
+  const uint32_t gsize = min((uint32_t)GROUP_M, MT - mg * GROUP_M);
+  const uint32_t r = (uint32_t)(t - (uint64_t)mg * GROUP_M * NTL);
+  row0 = (mg * GROUP_M + r % gsize) * BM;
+  nt = r / gsize;
+  rows = min((uint32_t)BM, p.m - row0);
+  return true;
+}
+
+template <int OP, int SCALE, int OUT>
 __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // Stage s at smem + s * STAGE: A tile, W tile, A-row scales, W scales.
   __shared__ __align__(16) uint8_t smem[STAGES * STAGE + DUMMY_BYTES];
@@ -249,14 +275,20 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   const uint32_t wm = (wv >> 2) & 1u, wn = wv & 3u;
   constexpr bool kSwi = OUT == kOutSwiGlu || OUT == kOutSwiGluFp8;  // gate/up pairs in the tile
 
-  uint32_t expert, row0, rows, nt;
-  if (!moe_tile(p, expert, row0, rows, nt)) return;
+  uint32_t expert = 0, row0, rows, nt;
+  if (p.dense_m_tiles) {
+    if (!dense_tile(p, row0, rows, nt)) return;
+  } else if (!moe_tile(p, expert, row0, rows, nt)) {
+    return;
+  }
   expert = __builtin_amdgcn_readfirstlane(expert);
   row0 = __builtin_amdgcn_readfirstlane(row0);
   rows = __builtin_amdgcn_readfirstlane(rows);
   nt = __builtin_amdgcn_readfirstlane(nt);
 
-  const uint32_t K = p.k, KB = K / 128;
+  // a K step is 128 bytes of a row: 128 e4m3 or 64 bf16 values
+  constexpr bool kBf = OP == kOpBf16;
+  const uint32_t K = p.k, RB = kBf ? 2 * K : K, KB = RB / 128;
   uint32_t bad = 0;
 
   // Rows past the tile's end (and rejected gather indices) read A row 0:
@@ -284,7 +316,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       return row < p.n ? row : p.n - 1;
     }
   };
-  const uint8_t* w_base = p.w + (uint64_t)expert * p.n * K;
+  const uint8_t* w_base = p.w + (uint64_t)expert * p.n * RB;
   // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
   uint32_t wblk0, wblk1;
   if constexpr (kSwi) {
@@ -305,18 +337,18 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // of that row (full 128-byte lines per 8 lanes).  Wave w fills A rows
   // [16w, 16w + 16) and W rows [32w, 32w + 32) of a stage.
   const uint32_t lrow = lane >> 3, lslot = lane & 7;
-  // byte offsets from the operand bases (A: a_rows_total * K and W: n * K
-  // per expert stay below 2^32, which the launcher checks)
+  // byte offsets from the operand bases (A: a_rows_total rows and W: n rows
+  // per expert stay below 2^32 bytes, which the launcher checks)
   uint32_t a_off[2], w_off[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const uint32_t R = 16 * wv + 8 * i + lrow;
-    a_off[i] = (uint32_t)(a_source(R) * K) + ((lslot ^ ((R >> 1) & 7u)) << 4);
+    a_off[i] = (uint32_t)(a_source(R) * RB) + ((lslot ^ ((R >> 1) & 7u)) << 4);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t R = 32 * wv + 8 * i + lrow;
-    w_off[i] = w_row(R) * K + ((lslot ^ ((R >> 1) & 7u)) << 4);
+    w_off[i] = w_row(R) * RB + ((lslot ^ ((R >> 1) & 7u)) << 4);
   }
   // Scales (one dword DMA per wave and step, so every compute wave issues
   // seven loads per step): waves 0 and 1 fetch the A-row scales of rows
@@ -324,16 +356,19 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // block (a lane's four A-row scales are then one 16-byte read); wave 2
   // the two W block scales (lane l: block l & 1); waves 3..7 repeat wave
   // 2's load into the scratch word.  UE8M0 bytes come in their aligned
-  // dword and are picked out by byte offset.
-  const uint8_t* s_src;
-  uint32_t s_lds;
-  if (wv < 2) {
-    const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2));
-    s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB * ESZ;
-    s_lds = A_BYTES + W_BYTES + 256 * wv;
-  } else {
-    s_src = static_cast<const uint8_t*>(p.w_scale) + ws_off[lane & 1] * ESZ;
-    s_lds = A_BYTES + W_BYTES + SA_BYTES;
+  // dword and are picked out by byte offset.  bf16 operands have no scales
+  // (six loads per step).
+  const uint8_t* s_src = nullptr;
+  uint32_t s_lds = 0;
+  if constexpr (!kBf) {
+    if (wv < 2) {
+      const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2));
+      s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB * ESZ;
+      s_lds = A_BYTES + W_BYTES + 256 * wv;
+    } else {
+      s_src = static_cast<const uint8_t*>(p.w_scale) + ws_off[lane & 1] * ESZ;
+      s_lds = A_BYTES + W_BYTES + SA_BYTES;
+    }
   }
   s_lds = __builtin_amdgcn_readfirstlane(s_lds);
   const bool s_scratch = wv > 2;
@@ -347,9 +382,11 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(wb, w_off[i], base + w_lds + i * 1024);
     // scales: a per-lane pointer (UE8M0 bytes come in their aligned dword)
-    uintptr_t sp = reinterpret_cast<uintptr_t>(s_src) + (uint64_t)kb * ESZ;
-    if constexpr (ESZ == 1) sp &= ~uintptr_t(3);
-    dma4v(reinterpret_cast<const void*>(sp), s_scratch ? lds0 + STAGES * STAGE : base + s_lds);
+    if constexpr (!kBf) {
+      uintptr_t sp = reinterpret_cast<uintptr_t>(s_src) + (uint64_t)kb * ESZ;
+      if constexpr (ESZ == 1) sp &= ~uintptr_t(3);
+      dma4v(reinterpret_cast<const void*>(sp), s_scratch ? lds0 + STAGES * STAGE : base + s_lds);
+    }
   };
 
   // byte offsets of this lane's UE8M0 A scales (rows wm*64 + r*16 + lr) and
@@ -401,7 +438,32 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       return cat8(*reinterpret_cast<const v4i*>(pa + rd0), *reinterpret_cast<const v4i*>(pa + (rd0 ^ 64)));
     };
     auto live = [&](int r) { return kFull || r < (int)rb_live; };
-    if constexpr (SCALE == kScaleF32) {
+    if constexpr (kBf) {
+      // bf16: the 128-byte step is 64 k; the fragment's first 16 bytes (k
+      // 8lg .. 8lg+7) feed one 16x16x32 MFMA and its last 16 (k 32+8lg ..)
+      // the second, the same split for both operands
+      auto mma = [&](int r, const v8i& af) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          const v4i w0{wf[nb][0], wf[nb][1], wf[nb][2], wf[nb][3]}, w1{wf[nb][4], wf[nb][5], wf[nb][6], wf[nb][7]};
+          const v4i a0{af[0], af[1], af[2], af[3]}, a1{af[4], af[5], af[6], af[7]};
+          acc[nb][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w0),
+                                                               __builtin_bit_cast(v8bf, a0), acc[nb][r], 0, 0, 0);
+          acc[nb][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, w1),
+                                                               __builtin_bit_cast(v8bf, a1), acc[nb][r], 0, 0, 0);
+        }
+      };
+      v8i af = a_frag(0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (live(r)) {
+          const v8i afn = a_frag(r < 3 ? r + 1 : 3);
+          mma(r, af);
+          af = afn;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if constexpr (SCALE == kScaleF32) {
       // fp32 scales: each MFMA starts from zero and its result is added
       // with one FMA per output.  Software-pipelined: the four MFMAs of A
       // block r + 1 are issued before the FMAs of block r, so those read
@@ -499,7 +561,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   {                                                                                                  \
     const uint32_t j = kb + (J);                                                                     \
     if ((TAIL) && j >= KB) return;                                                                   \
-    __builtin_amdgcn_s_waitcnt(kWaitVm7);                                                            \
+    __builtin_amdgcn_s_waitcnt(kBf ? kWaitVm6 : kWaitVm7);                                           \
     __builtin_amdgcn_s_barrier();                                                                    \
     issue(((J) + 2) % 3, min(j + 2, last));                                                          \
     compute(std::integral_constant<uint32_t, (J) % 3>{}, j, FULL);                                   \
@@ -648,8 +710,9 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
                          __builtin_isfinite(v[3]);
         if constexpr (OUT == kOutF32) {
           float* dst = static_cast<float*>(p.out) + orow + col;
-          if (fin || !p.err_nonfinite) {
+          if (fin || !p.err_nonfinite || p.write_nonfinite) {
             *reinterpret_cast<v4f*>(dst) = v;
+            if (!fin) bad |= kErrNonFinite;
           } else {
             bad |= kErrNonFinite;
             for (int i = 0; i < 4; ++i)
@@ -657,9 +720,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
           }
         } else {
           uint16_t* dst = static_cast<uint16_t*>(p.out) + orow + col;
-          if (fin || !p.err_nonfinite) {
+          if (fin || !p.err_nonfinite || p.write_nonfinite) {
             *reinterpret_cast<uint2*>(dst) = uint2{f32_to_bf16_bits(v[0]) | (f32_to_bf16_bits(v[1]) << 16),
                                                    f32_to_bf16_bits(v[2]) | (f32_to_bf16_bits(v[3]) << 16)};
+            if (!fin) bad |= kErrNonFinite;
           } else {
             bad |= kErrNonFinite;
             for (int i = 0; i < 4; ++i)
@@ -676,13 +740,20 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   }
 }
 
-template <int SCALE>
+template <int OP, int SCALE>
 void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out) {
-  if (out == kOutSwiGlu) hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutSwiGlu>), dim3(grid), dim3(NTH), 0, s, mp);
-  else if (out == kOutSwiGluFp8)
-    hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutSwiGluFp8>), dim3(grid), dim3(NTH), 0, s, mp);
-  else if (out == kOutF32) hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutF32>), dim3(grid), dim3(NTH), 0, s, mp);
-  else hipLaunchKernelGGL((fp8_moe_gemm_kernel<SCALE, kOutBf16>), dim3(grid), dim3(NTH), 0, s, mp);
+  if constexpr (OP == kOpFp8) {
+    if (out == kOutSwiGlu) {
+      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGlu>), dim3(grid), dim3(NTH), 0, s, mp);
+      return;
+    }
+    if (out == kOutSwiGluFp8) {
+      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGluFp8>), dim3(grid), dim3(NTH), 0, s, mp);
+      return;
+    }
+  }
+  if (out == kOutF32) hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutF32>), dim3(grid), dim3(NTH), 0, s, mp);
+  else hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutBf16>), dim3(grid), dim3(NTH), 0, s, mp);
 }
 
 }  // namespace
@@ -723,9 +794,50 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
   const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
   St s = RequireCleanLastError();
   if (!s.ok()) return s;
-  if (a.scale_fmt == kScaleF32) launch_out<kScaleF32>(mp, grid, a.stream, a.out_kind);
-  else launch_out<kScaleUe8m0>(mp, grid, a.stream, a.out_kind);
+  if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind);
+  else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind);
   return AfterLaunch("fp8_moe_gemm_launch_failed");
+}
+
+St LaunchBigTileGemm(const BigTileArgs& a) {
+  const bool bf = a.bf16;
+  if (!a.a || !a.w || !a.out || !a.stream || (!bf && (!a.a_scale || !a.w_scale || !a.error_flag)))
+    return Invalid("big_tile_gemm_null_argument");
+  if (a.m == 0 || a.n == 0 || a.k == 0 || a.n % 128 || a.k % (bf ? 64 : 128))
+    return Invalid("big_tile_gemm_shape_invalid");
+  if (a.out_kind != kOutBf16 && a.out_kind != kOutF32) return Invalid("big_tile_gemm_output_type_invalid");
+  const uint64_t rb = bf ? 2ull * a.k : a.k;
+  // the tile loads address A and W by 32-bit byte offsets
+  if ((uint64_t)a.m * rb > 0xffffffffull || (uint64_t)a.n * rb > 0xffffffffull)
+    return Invalid("big_tile_gemm_operand_too_large");
+  MoeParams mp{};
+  mp.a = static_cast<const uint8_t*>(a.a);
+  mp.a_scale = a.a_scale;
+  mp.w = static_cast<const uint8_t*>(a.w);
+  mp.w_scale = a.w_scale;
+  mp.out = a.out;
+  mp.err = a.error_flag;
+  mp.m = a.m;
+  mp.n = a.n;
+  mp.k = a.k;
+  mp.experts = 1;
+  mp.a_rows_total = a.m;
+  mp.dense_m_tiles = (a.m + BM - 1) / BM;
+  mp.out_row_stride = a.n;
+  mp.n_tiles = (a.n + BN - 1) / BN;
+  mp.err_code = a.error_flag ? a.err_code_bit : 0u;
+  mp.err_scale = a.error_flag ? a.err_scale_bit : 0u;
+  mp.err_nonfinite = a.error_flag ? a.err_nonfinite_bit : 0u;
+  mp.write_nonfinite = a.write_nonfinite ? 1u : 0u;
+  const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles;
+  if (total > 0x7fffffffull - 8) return Invalid("big_tile_gemm_grid_too_large");
+  const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  St s = RequireCleanLastError();
+  if (!s.ok()) return s;
+  if (bf) launch_out<kOpBf16, kScaleF32>(mp, grid, a.stream, a.out_kind);
+  else if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind);
+  else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind);
+  return AfterLaunch("big_tile_gemm_launch_failed");
 }
 
 }  // namespace pih_amd

@@ -745,6 +745,28 @@ St LaunchBf16Gemm(const Bf16GemmArgs& a) {
   if (a.out_kind != kOutBf16 && a.out_kind != kOutF32) return Invalid("bf16_gemm_output_type_invalid");
   if (a.m <= 64) return LaunchBf16Gemv(a);
   if (a.n % 128 || a.k % 64) return Invalid("bf16_gemm_shape_invalid");
+  if (BigTileWorthIt(a.m, a.n) && (uint64_t)a.m * a.k * 2 <= 0xffffffffull &&
+      (uint64_t)a.n * a.k * 2 <= 0xffffffffull) {
+    BigTileArgs b;
+    b.a = a.a;
+    b.w = a.w;
+    b.out = a.out;
+    b.stream = a.stream;
+    b.m = a.m;
+    b.n = a.n;
+    b.k = a.k;
+    b.bf16 = true;
+    b.out_kind = a.out_kind;
+    // the GemmPlan contract has no error flag; the LM head passes one for
+    // its non-finite-logit bit (the logit is stored either way)
+    if (a.error_flag && a.nonfinite_bit) {
+      b.error_flag = a.error_flag;
+      b.err_code_bit = b.err_scale_bit = 0u;
+      b.err_nonfinite_bit = a.nonfinite_bit;
+    }
+    b.write_nonfinite = true;
+    return LaunchBigTileGemm(b);
+  }
   GemmParams gp{};
   gp.a = reinterpret_cast<const uint8_t*>(a.a);
   gp.w = reinterpret_cast<const uint8_t*>(a.w);

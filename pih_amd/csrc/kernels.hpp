@@ -135,6 +135,31 @@ struct Bf16GemmArgs {
   uint32_t nonfinite_bit = 0;
 };
 St LaunchBf16Gemm(const Bf16GemmArgs& a);
+
+// Dense GEMM on the MoE kernel's 128 x 256 tiles (gemm_fp8_moe.hip), one
+// problem with contiguous rows: out [m, n] = A [m, k] . W [n, k]^T, either
+// e4m3 with 128x128 block scales (fp32 or UE8M0, no NaN-code handling) or
+// bf16.  n % 128 == 0, k % 128 (e4m3) or % 64 (bf16) == 0.
+struct BigTileArgs {
+  const void* a = nullptr;
+  const void* a_scale = nullptr;
+  const void* w = nullptr;
+  const void* w_scale = nullptr;
+  void* out = nullptr;
+  uint32_t* error_flag = nullptr;  // optional for bf16
+  hipStream_t stream = nullptr;
+  uint32_t m = 0, n = 0, k = 0;
+  bool bf16 = false;
+  ScaleFmt scale_fmt = kScaleF32;
+  OutKind out_kind = kOutBf16;
+  uint32_t err_code_bit = 1u, err_scale_bit = 2u, err_nonfinite_bit = 4u;
+  bool write_nonfinite = false;
+};
+St LaunchBigTileGemm(const BigTileArgs& a);
+// the big-tile path pays when its tiles fill the CUs
+inline bool BigTileWorthIt(uint32_t m, uint32_t n) {
+  return m >= 256 && (uint64_t)((m + 127) / 128) * ((n + 255) / 256) >= 256;
+}
 uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k);
 // decode shapes (m <= 64): the weight-streaming GEMV with split-K
 St LaunchBf16Gemv(const Bf16GemmArgs& a);
