@@ -116,7 +116,39 @@ __global__ __launch_bounds__(256) void nonfinite_scan_kernel(const uint4* x, uin
   if (bad) atomicOr(err, bit);
 }
 
+// e4m3 NaN codes (0x7F / 0xFF bytes) anywhere in two byte buffers: the big
+// tile FP8 path's test (16 bytes per load, the tails byte by byte).
+__global__ __launch_bounds__(256) void nan_code_scan_kernel(const uint8_t* a, uint64_t na, const uint8_t* w,
+                                                            uint64_t nw, uint32_t* err, uint32_t bit) {
+  const uint64_t va = na / 16, vw = nw / 16, total = va + vw, stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint64_t t0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint32_t bad = 0;
+  for (uint64_t i = t0; i < total; i += stride) {
+    const uint4 v = i < va ? reinterpret_cast<const uint4*>(a)[i] : reinterpret_cast<const uint4*>(w)[i - va];
+    bad |= e4m3_nan_bytes(v.x) | e4m3_nan_bytes(v.y) | e4m3_nan_bytes(v.z) | e4m3_nan_bytes(v.w);
+  }
+  if (t0 < 16) {
+    for (uint64_t i = va * 16 + t0; i < na; i += 16) bad |= e4m3_nan_bytes(a[i]);
+    for (uint64_t i = vw * 16 + t0; i < nw; i += 16) bad |= e4m3_nan_bytes(w[i]);
+  }
+  if (bad) atomicOr(err, bit);
+}
+
 }  // namespace
+
+St LaunchNanCodeScan(const NanCodeScanArgs& a) {
+  if (!a.a || !a.w || !a.error_flag || !a.stream || !a.bit) return Invalid("nan_code_scan_null_argument");
+  if ((reinterpret_cast<uintptr_t>(a.a) | reinterpret_cast<uintptr_t>(a.w)) % 16)
+    return Invalid("nan_code_scan_alignment_invalid");
+  St clean = RequireCleanLastError();
+  if (!clean.ok()) return clean;
+  const uint64_t vec = (a.a_bytes + a.w_bytes) / 16;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>((vec + 255) / 256, 4096);
+  hipLaunchKernelGGL(nan_code_scan_kernel, dim3(grid ? grid : 1), dim3(256), 0, a.stream,
+                     static_cast<const uint8_t*>(a.a), a.a_bytes, static_cast<const uint8_t*>(a.w), a.w_bytes,
+                     a.error_flag, a.bit);
+  return AfterLaunch("nan_code_scan_launch_failed");
+}
 
 St LaunchSwiGlu(const SwiGluArgs& a) {
   if (!a.gate || !a.up || !a.out || !a.error_flag || !a.stream) return Invalid("swiglu_null_argument");

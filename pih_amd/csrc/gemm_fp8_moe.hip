@@ -110,6 +110,8 @@ struct MoeParams {
   // gather); 0 for MoE segments
   uint32_t dense_m_tiles;
   uint32_t write_nonfinite;  // store a non-finite result (and flag it)
+  const uint32_t* skip_if;   // every block exits at once if (*skip_if & skip_bit)
+  uint32_t skip_bit;
   uint64_t out_row_stride;
   uint32_t n_tiles;
   float limit;
@@ -275,6 +277,8 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   const uint32_t wm = (wv >> 2) & 1u, wn = wv & 3u;
   constexpr bool kSwi = OUT == kOutSwiGlu || OUT == kOutSwiGluFp8;  // gate/up pairs in the tile
 
+  // the masked bit is not changed while this kernel runs: one value for every thread
+  if (p.skip_if && (__hip_atomic_load(p.skip_if, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & p.skip_bit)) return;
   uint32_t expert = 0, row0, rows, nt;
   if (p.dense_m_tiles) {
     if (!dense_tile(p, row0, rows, nt)) return;
@@ -829,6 +833,8 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.err_scale = a.error_flag ? a.err_scale_bit : 0u;
   mp.err_nonfinite = a.error_flag ? a.err_nonfinite_bit : 0u;
   mp.write_nonfinite = a.write_nonfinite ? 1u : 0u;
+  mp.skip_if = a.skip_if;
+  mp.skip_bit = a.skip_bit;
   const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles;
   if (total > 0x7fffffffull - 8) return Invalid("big_tile_gemm_grid_too_large");
   const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);

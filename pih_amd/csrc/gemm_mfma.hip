@@ -120,6 +120,11 @@ struct GemmParams {
   float limit;
   uint32_t err_code, err_scale, err_nonfinite;
   uint32_t write_nonfinite;  // store a non-finite result as well as flagging it
+  // when set, the kernel runs only if (*run_if & run_bit) != 0 (the checking
+  // half of the big-tile dense FP8 path: it works only when the code scan
+  // found a NaN code, and the big-tile kernel then steps aside)
+  const uint32_t* run_if;
+  uint32_t run_bit;
 };
 
 // Expert lookup for MoE tile g: returns false when g is past the last tile.
@@ -225,6 +230,8 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1, lr = lane & 15, lg = lane >> 4;
 
+  // the scan (or an earlier call) set the bit before this launch began
+  if (p.run_if && !(__hip_atomic_load(p.run_if, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & p.run_bit)) return;
   const uint32_t tile = xcd_chunked_tile(blockIdx.x, gridDim.x);
   if (tile >= p.tiles_total) return;
   const uint32_t mtot = MOE ? p.tiles_total / p.n_tiles : p.problems * p.m_tiles_per;
@@ -658,6 +665,50 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
   if (a.moe && !a.offsets) return Invalid("fp8_gemm_offsets_missing");
   if (a.a_rows_total == 0) return Invalid("fp8_gemm_a_rows_invalid");
   if (a.moe && !a.check_codes) return LaunchFp8MoeGemm(a);
+  // One large dense problem: the MoE kernel's big tiles.  Those do not
+  // decode NaN codes as zeros, so with check_codes a scan first raises the
+  // code bit if A or W holds one; the big-tile kernel then exits at once
+  // and the checking 128 x 128 kernel enqueued after it (which otherwise
+  // exits at once) computes the result.  The bit may also have been set
+  // before the call: the checking kernel then runs, with the same result.
+  const bool dense1 = !a.moe && a.problems == 1 && !a.a_gather && a.a_row_stride == 1 && a.a_prob_row == 0 &&
+                      a.out_prob_col == 0 && (a.out_row_stride == 0 || a.out_row_stride == a.n) &&
+                      (a.out_kind == kOutBf16 || a.out_kind == kOutF32) && a.a_rows_total >= a.m &&
+                      BigTileWorthIt(a.m, a.n) && (uint64_t)a.m * a.k <= 0xffffffffull &&
+                      (uint64_t)a.n * a.k <= 0xffffffffull;
+  if (dense1) {
+    BigTileArgs b;
+    b.a = a.a;
+    b.a_scale = a.a_scale;
+    b.w = a.w;
+    b.w_scale = a.w_scale;
+    b.out = a.out;
+    b.error_flag = a.error_flag;
+    b.stream = a.stream;
+    b.m = a.m;
+    b.n = a.n;
+    b.k = a.k;
+    b.scale_fmt = a.scale_fmt;
+    b.out_kind = a.out_kind;
+    b.err_code_bit = a.err_code_bit;
+    b.err_scale_bit = a.err_scale_bit;
+    b.err_nonfinite_bit = a.err_nonfinite_bit;
+    b.write_nonfinite = a.write_nonfinite;
+    if (!a.check_codes || !a.err_code_bit) return LaunchBigTileGemm(b);
+    NanCodeScanArgs sc;
+    sc.a = a.a;
+    sc.a_bytes = (uint64_t)a.m * a.k;
+    sc.w = a.w;
+    sc.w_bytes = (uint64_t)a.n * a.k;
+    sc.error_flag = a.error_flag;
+    sc.bit = a.err_code_bit;
+    sc.stream = a.stream;
+    St s = LaunchNanCodeScan(sc);
+    if (!s.ok()) return s;
+    b.skip_if = a.error_flag;
+    b.skip_bit = a.err_code_bit;
+    if (!(s = LaunchBigTileGemm(b)).ok()) return s;
+  }
   if (!a.moe && a.m <= kSmallMRows && (a.out_kind == kOutBf16 || a.out_kind == kOutF32)) {
     // a few activation rows: weight streaming over 16-row blocks
     bool taken = false;
@@ -683,6 +734,10 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
   gp.err_scale = a.err_scale_bit;
   gp.err_nonfinite = a.err_nonfinite_bit;
   gp.write_nonfinite = a.write_nonfinite ? 1u : 0u;
+  if (dense1) {  // the checking half (a.check_codes here)
+    gp.run_if = a.error_flag;
+    gp.run_bit = a.err_code_bit;
+  }
   uint32_t grid;
   St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, a.out_row_stride);
   if (!s.ok()) return s;

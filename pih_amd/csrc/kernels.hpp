@@ -154,8 +154,25 @@ struct BigTileArgs {
   OutKind out_kind = kOutBf16;
   uint32_t err_code_bit = 1u, err_scale_bit = 2u, err_nonfinite_bit = 4u;
   bool write_nonfinite = false;
+  // when set, every block exits at once if (*skip_if & skip_bit) != 0
+  const uint32_t* skip_if = nullptr;
+  uint32_t skip_bit = 0;
 };
 St LaunchBigTileGemm(const BigTileArgs& a);
+
+// ORs `bit` into *error_flag when A or W holds an e4m3 NaN code (0x7F or
+// 0xFF byte) -- the test the big-tile FP8 path runs before it trusts the
+// MFMA to see no NaN codes (elementwise.hip).
+struct NanCodeScanArgs {
+  const void* a = nullptr;
+  uint64_t a_bytes = 0;
+  const void* w = nullptr;
+  uint64_t w_bytes = 0;
+  uint32_t* error_flag = nullptr;
+  uint32_t bit = 0;
+  hipStream_t stream = nullptr;
+};
+St LaunchNanCodeScan(const NanCodeScanArgs& a);
 // the big-tile path pays when its tiles fill the CUs
 inline bool BigTileWorthIt(uint32_t m, uint32_t n) {
   return m >= 256 && (uint64_t)((m + 127) / 128) * ((n + 255) / 256) >= 256;

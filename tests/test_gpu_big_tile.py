@@ -1,0 +1,162 @@
+"""Dense GEMMs on the MoE kernel's 128 x 256 tiles (large single problems).
+
+* DeepSeek `launch_fp8_gemm` (UE8M0 scales) and the linear pack's
+  `launch_fp8_gemm` (fp32 scales) at shapes whose tile grid fills the GPU:
+  sampled rows against the oracle.
+* The reference decodes an e4m3 NaN code as 0 and raises bit 1
+  (deepseek_fp8_gemm.cu:11-17); the big-tile kernel does not decode codes, so
+  a scan raises the bit first and the big-tile kernel steps aside for the
+  checking 128 x 128 kernel.  Checked with a NaN code planted in A and one in
+  W (the rows they reach against the oracle, which zeroes them), and with
+  the bit already set before the call (the checking kernel computes it all).
+* BF16 `launch_bf16_gemm` at M = 1024 and 2048 (prefill sizes) with bf16
+  and fp32 output against the fp32-accumulate oracle.
+
+Tolerance: max_rel <= 1e-2 (normwise), cosine >= 0.9999 (tests/helpers.py).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from pih_amd import abi, synth
+from tests.helpers import assert_close, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def eng():
+    import torch
+
+    from pih_amd.device import engine_stream
+
+    oracle.set_threads(min(16, __import__("os").cpu_count() or 1))
+    with engine_stream() as s:
+        yield s
+        torch.cuda.synchronize()
+
+
+def _codes(seed, shape):
+    """e4m3 codes without NaN codes (0x7F / 0xFF skipped)."""
+    c = (synth.splitmix64(seed, int(np.prod(shape))) % np.uint64(254)).astype(np.uint8)
+    return np.where(c >= 0x7F, c + 1, c).astype(np.uint8).reshape(shape)
+
+
+def _ds_fp8(a, sa, w, sw, m, n, k, flag_init=0):
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    flag = torch.full((1,), flag_init, dtype=torch.int32, device="cuda")
+    ad, sad, wd, swd = to_dev(a), to_dev(sa), to_dev(w), to_dev(sw)
+    r = abi.request(abi.DS["fp8_gemm"], activation_e4m3=ptr(ad), activation_scale_bits=ptr(sad),
+                    weight_e4m3=ptr(wd), weight_scale_bits=ptr(swd), output=ptr(out), error_flag=ptr(flag),
+                    stream=stream_handle(), m=m, n=n, k=k, output_type=1)
+    st = abi.deepseek_pack().call("launch_fp8_gemm", r)
+    assert st.code == abi.OK, st
+    torch.cuda.synchronize()
+    return oracle.bf16_bits_to_f32(to_host(out)), int(flag.item()) & 0xFFFFFFFF
+
+
+def _ue8m0_operands(m, n, k, seed):
+    a = _codes(synth.config_seed(5, seed), (m, k))
+    w = _codes(synth.config_seed(5, seed + 1), (n, k))
+    sa = (118 + synth.splitmix64(seed + 2, m * (k // 128)) % np.uint64(6)).astype(np.uint8).reshape(m, k // 128)
+    sw = (112 + synth.splitmix64(seed + 3, (n // 128) * (k // 128)) % np.uint64(6)).astype(np.uint8)
+    return a, sa, w, sw.reshape(n // 128, k // 128)
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 2048), (2048, 4096, 8192), (4096, 2048, 1024)])
+def test_deepseek_fp8_gemm_big_tile(eng, m, n, k):
+    a, sa, w, sw = _ue8m0_operands(m, n, k, 100 + k)
+    got, flag = _ds_fp8(a, sa, w, sw, m, n, k)
+    assert flag == 0
+    rows = np.unique(np.linspace(0, m - 1, 24).astype(np.int64))
+    ref = oracle.fp8_gemm_ue8m0(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows]), w, sw)
+    assert_close(got[rows], ref, f"big-tile fp8 {m}x{n}x{k}")
+
+
+def test_nan_codes_take_the_checking_kernel(eng):
+    m, n, k = 2048, 4096, 1024
+    a, sa, w, sw = _ue8m0_operands(m, n, k, 300)
+    a[5, 77] = 0x7F   # NaN code in A (row 5)
+    w[1000, 300] = 0xFF  # NaN code in W (column 1000 of every row)
+    got, flag = _ds_fp8(a, sa, w, sw, m, n, k)
+    assert flag & 1, flag
+    rows = np.array([0, 5, 6, 1023, 2047])
+    # the oracle rejects NaN codes; the kernel's decode reads them as 0
+    a0, w0 = a.copy(), w.copy()
+    a0[5, 77] = 0
+    w0[1000, 300] = 0
+    ref = oracle.fp8_gemm_ue8m0(np.ascontiguousarray(a0[rows]), np.ascontiguousarray(sa[rows]), w0, sw)
+    assert np.isfinite(got[rows]).all()
+    assert_close(got[rows], ref, "nan codes as zero")
+
+
+def test_code_bit_already_set(eng):
+    """A flag that already holds bit 1 (a poisoned lane) sends the call to
+    the checking kernel; the result is the same."""
+    m, n, k = 2048, 4096, 1024
+    a, sa, w, sw = _ue8m0_operands(m, n, k, 400)
+    clean, flag0 = _ds_fp8(a, sa, w, sw, m, n, k)
+    assert flag0 == 0
+    again, flag1 = _ds_fp8(a, sa, w, sw, m, n, k, flag_init=1)
+    assert flag1 == 1
+    rows = np.unique(np.linspace(0, m - 1, 16).astype(np.int64))
+    ref = oracle.fp8_gemm_ue8m0(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows]), w, sw)
+    assert_close(again[rows], ref, "checking kernel")
+    assert_close(clean[rows], ref, "big-tile kernel")
+
+
+@pytest.mark.parametrize("out_type", [1, 2])
+def test_linear_fp8_gemm_big_tile_f32_scales(eng, out_type):
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    m, n, k = 2048, 4096, 2048
+    a = _codes(synth.config_seed(5, 500), (m, k))
+    w = _codes(synth.config_seed(5, 501), (n, k))
+    rng = np.random.default_rng(502)
+    sa = (rng.uniform(0.5, 2.0, (m, k // 128)) / 448).astype(np.float32)
+    sw = (rng.uniform(0.5, 2.0, (n // 128, k // 128)) / 448).astype(np.float32)
+    dt = torch.bfloat16 if out_type == abi.OUTPUT_BF16 else torch.float32
+    out = torch.empty(m, n, dtype=dt, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ad, sad, wd, swd = to_dev(a), to_dev(sa), to_dev(w), to_dev(sw)
+    r = abi.request(abi.LN["fp8_gemm"], activation_e4m3=ptr(ad), activation_scale=ptr(sad), weight_e4m3=ptr(wd),
+                    weight_scale=ptr(swd), output=ptr(out), error_flag_u32=ptr(flag), stream=stream_handle(),
+                    m=m, n=n, k=k, scale_format=abi.SCALE_F32, output_type=out_type)
+    st = abi.linear_pack().call("launch_fp8_gemm", r)
+    assert st.code == abi.OK, st
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 0
+    host = to_host(out)
+    got = oracle.bf16_bits_to_f32(host) if out_type == abi.OUTPUT_BF16 else host
+    rows = np.unique(np.linspace(0, m - 1, 24).astype(np.int64))
+    ref = oracle.fp8_gemm_f32(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows]), w, sw)
+    assert_close(got[rows], ref, f"big-tile fp8 f32-scale out {out_type}")
+
+
+@pytest.mark.parametrize("m,n,k,out_type", [(1024, 8192, 1024, 1), (2048, 4096, 1536, 2)])
+def test_bf16_gemm_big_tile(eng, m, n, k, out_type):
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    x = synth.bf16_normal(synth.config_seed(5, 600 + m), (m, k))
+    w = synth.bf16_normal(synth.config_seed(5, 601 + n), (n, k), std=0.02)
+    dt = torch.bfloat16 if out_type == abi.OUTPUT_BF16 else torch.float32
+    out = torch.empty(m, n, dtype=dt, device="cuda")
+    xd, wd = to_dev(x), to_dev(w)
+    r = abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xd), w_bf16=ptr(wd), output=ptr(out), workspace=0,
+                    workspace_bytes=0, stream=stream_handle(), m=m, n=n, k=k, output_type=out_type)
+    st = abi.linear_pack().call("launch_bf16_gemm", r)
+    assert st.code == abi.OK, st
+    torch.cuda.synchronize()
+    host = to_host(out)
+    got = oracle.bf16_bits_to_f32(host) if out_type == abi.OUTPUT_BF16 else host
+    rows = np.unique(np.linspace(0, m - 1, 24).astype(np.int64))
+    ref = oracle.bf16_gemm(np.ascontiguousarray(x[rows]), w)
+    assert_close(got[rows], ref, f"big-tile bf16 {m}x{n}x{k}")
