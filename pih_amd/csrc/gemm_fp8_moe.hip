@@ -106,9 +106,13 @@ struct MoeParams {
   uint32_t* err;
   void* out_scale;  // kOutSwiGluFp8: [rows, n / 256] group scales
   uint32_t m, n, k, experts, a_rows_total;
-  // dense: one problem of m rows, ceil(m / 128) M tiles (no offsets, no
-  // gather); 0 for MoE segments
+  // dense: `experts` strided problems of m rows each, ceil(m / 128) M tiles
+  // per problem (no offsets, no gather; A row i of problem q is
+  // i * a_row_stride + q * a_prob_row, its output row starts at
+  // i * out_row_stride + q * out_prob_col); 0 for MoE segments
   uint32_t dense_m_tiles;
+  uint32_t a_row_stride, a_prob_row;
+  uint64_t out_prob_col;
   uint32_t write_nonfinite;  // store a non-finite result (and flag it)
   const uint32_t* skip_if;   // every block exits at once if (*skip_if & skip_bit)
   uint32_t skip_bit;
@@ -246,16 +250,18 @@ __device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, u
   return true;
 }
 
-// Dense form: tile t of the M x N tile grid, each XCD (blocks b % 8) walking
-// one contiguous range, M-fastest in groups of GROUP_M so that concurrent
-// tiles share their W tile in L2.
-__device__ bool dense_tile(const MoeParams& p, uint32_t& row0, uint32_t& rows, uint32_t& nt) {
+// Dense form: tile t of the problems x M x N tile grid (problem-major),
+// each XCD (blocks b % 8) walking one contiguous range, M-fastest in groups
+// of GROUP_M so that concurrent tiles share their W tile in L2.
+__device__ bool dense_tile(const MoeParams& p, uint32_t& prob, uint32_t& row0, uint32_t& rows, uint32_t& nt) {
   const uint32_t MT = p.dense_m_tiles, NTL = p.n_tiles;
-  const uint64_t T = (uint64_t)MT * NTL;
+  const uint64_t per_prob = (uint64_t)MT * NTL, T = per_prob * p.experts;
   const uint32_t per = (uint32_t)((T + 7) / 8);
   const uint32_t xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
-  const uint64_t t = (uint64_t)xcd * per + jj;
-  if (jj >= per || t >= T) return false;
+  const uint64_t tt = (uint64_t)xcd * per + jj;
+  if (jj >= per || tt >= T) return false;
+  prob = (uint32_t)(tt / per_prob);
+  const uint64_t t = tt - (uint64_t)prob * per_prob;
   const uint32_t mg = (uint32_t)(t / ((uint64_t)GROUP_M * NTL));
   const uint32_t gsize = min((uint32_t)GROUP_M, MT - mg * GROUP_M);
   const uint32_t r = (uint32_t)(t - (uint64_t)mg * GROUP_M * NTL);
@@ -281,7 +287,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   if (p.skip_if && (__hip_atomic_load(p.skip_if, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & p.skip_bit)) return;
   uint32_t expert = 0, row0, rows, nt;
   if (p.dense_m_tiles) {
-    if (!dense_tile(p, row0, rows, nt)) return;
+    if (!dense_tile(p, expert, row0, rows, nt)) return;
   } else if (!moe_tile(p, expert, row0, rows, nt)) {
     return;
   }
@@ -301,7 +307,9 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   auto a_source = [&](uint32_t r) -> uint64_t {
     if (r >= rows) return 0;
     const uint32_t logical = row0 + r;
-    const uint64_t src = p.a_gather ? p.a_gather[logical] : logical;
+    const uint64_t src = p.dense_m_tiles ? (uint64_t)logical * p.a_row_stride + (uint64_t)expert * p.a_prob_row
+                         : p.a_gather     ? p.a_gather[logical]
+                                          : logical;
     if (src >= p.a_rows_total) {
       bad |= kErrCode;
       return 0;
@@ -669,7 +677,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   for (int r = 0; r < 4 && OUT != kOutSwiGluFp8; ++r) {
     const uint32_t rr = wm * 64 + r * 16 + lr;
     if (rr >= rows) continue;
-    const uint64_t orow = (uint64_t)(row0 + rr) * p.out_row_stride;
+    const uint64_t orow = (uint64_t)(row0 + rr) * p.out_row_stride + (uint64_t)expert * p.out_prob_col;
     if constexpr (OUT == kOutSwiGlu) {
       const float rwt = p.row_weight ? p.row_weight[row0 + rr] : 1.0f;
 #pragma unroll
@@ -810,9 +818,11 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   if (a.m == 0 || a.n == 0 || a.k == 0 || a.n % 128 || a.k % (bf ? 64 : 128))
     return Invalid("big_tile_gemm_shape_invalid");
   if (a.out_kind != kOutBf16 && a.out_kind != kOutF32) return Invalid("big_tile_gemm_output_type_invalid");
+  if (a.problems == 0) return Invalid("big_tile_gemm_shape_invalid");
   const uint64_t rb = bf ? 2ull * a.k : a.k;
-  // the tile loads address A and W by 32-bit byte offsets
-  if ((uint64_t)a.m * rb > 0xffffffffull || (uint64_t)a.n * rb > 0xffffffffull)
+  const uint64_t a_rows = a.a_rows_total ? a.a_rows_total : (uint64_t)a.m * a.problems;
+  // the tile loads address A and one problem's W by 32-bit byte offsets
+  if (a_rows > 0xffffffffull || a_rows * rb > 0xffffffffull || (uint64_t)a.n * rb > 0xffffffffull)
     return Invalid("big_tile_gemm_operand_too_large");
   MoeParams mp{};
   mp.a = static_cast<const uint8_t*>(a.a);
@@ -824,10 +834,13 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.m = a.m;
   mp.n = a.n;
   mp.k = a.k;
-  mp.experts = 1;
-  mp.a_rows_total = a.m;
+  mp.experts = a.problems;
+  mp.a_rows_total = (uint32_t)a_rows;
   mp.dense_m_tiles = (a.m + BM - 1) / BM;
-  mp.out_row_stride = a.n;
+  mp.a_row_stride = a.a_row_stride;
+  mp.a_prob_row = a.a_prob_row;
+  mp.out_row_stride = a.out_row_stride ? a.out_row_stride : a.n;
+  mp.out_prob_col = a.out_prob_col;
   mp.n_tiles = (a.n + BN - 1) / BN;
   mp.err_code = a.error_flag ? a.err_code_bit : 0u;
   mp.err_scale = a.error_flag ? a.err_scale_bit : 0u;
@@ -835,7 +848,7 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.write_nonfinite = a.write_nonfinite ? 1u : 0u;
   mp.skip_if = a.skip_if;
   mp.skip_bit = a.skip_bit;
-  const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles;
+  const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles * a.problems;
   if (total > 0x7fffffffull - 8) return Invalid("big_tile_gemm_grid_too_large");
   const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
   St s = RequireCleanLastError();

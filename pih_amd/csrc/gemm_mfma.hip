@@ -671,11 +671,13 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
   // and the checking 128 x 128 kernel enqueued after it (which otherwise
   // exits at once) computes the result.  The bit may also have been set
   // before the call: the checking kernel then runs, with the same result.
-  const bool dense1 = !a.moe && a.problems == 1 && !a.a_gather && a.a_row_stride == 1 && a.a_prob_row == 0 &&
-                      a.out_prob_col == 0 && (a.out_row_stride == 0 || a.out_row_stride == a.n) &&
-                      (a.out_kind == kOutBf16 || a.out_kind == kOutF32) && a.a_rows_total >= a.m &&
-                      BigTileWorthIt(a.m, a.n) && (uint64_t)a.m * a.k <= 0xffffffffull &&
-                      (uint64_t)a.n * a.k <= 0xffffffffull;
+  // (With check_codes only one problem of contiguous rows: the scan then
+  // covers exactly the bytes the GEMM reads.)
+  const bool contiguous1 = a.problems == 1 && a.a_row_stride == 1 && a.a_prob_row == 0 && a.out_prob_col == 0 &&
+                           (a.out_row_stride == 0 || a.out_row_stride == a.n) && a.a_rows_total >= a.m;
+  const bool dense1 = !a.moe && !a.a_gather && (a.out_kind == kOutBf16 || a.out_kind == kOutF32) &&
+                      (contiguous1 || !a.check_codes) && BigTileWorthIt(a.m, a.n * a.problems) &&
+                      (uint64_t)a.a_rows_total * a.k <= 0xffffffffull && (uint64_t)a.n * a.k <= 0xffffffffull;
   if (dense1) {
     BigTileArgs b;
     b.a = a.a;
@@ -688,6 +690,12 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
     b.m = a.m;
     b.n = a.n;
     b.k = a.k;
+    b.problems = a.problems;
+    b.a_rows_total = a.a_rows_total;
+    b.a_row_stride = a.a_row_stride;
+    b.a_prob_row = a.a_prob_row;
+    b.out_row_stride = a.out_row_stride;
+    b.out_prob_col = a.out_prob_col;
     b.scale_fmt = a.scale_fmt;
     b.out_kind = a.out_kind;
     b.err_code_bit = a.err_code_bit;

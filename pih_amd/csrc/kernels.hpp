@@ -136,8 +136,8 @@ struct Bf16GemmArgs {
 };
 St LaunchBf16Gemm(const Bf16GemmArgs& a);
 
-// Dense GEMM on the MoE kernel's 128 x 256 tiles (gemm_fp8_moe.hip), one
-// problem with contiguous rows: out [m, n] = A [m, k] . W [n, k]^T, either
+// Dense GEMM on the MoE kernel's 128 x 256 tiles (gemm_fp8_moe.hip), one or
+// more strided problems: out [m, n] = A [m, k] . W [n, k]^T, either
 // e4m3 with 128x128 block scales (fp32 or UE8M0, no NaN-code handling) or
 // bf16.  n % 128 == 0, k % 128 (e4m3) or % 64 (bf16) == 0.
 struct BigTileArgs {
@@ -149,6 +149,11 @@ struct BigTileArgs {
   uint32_t* error_flag = nullptr;  // optional for bf16
   hipStream_t stream = nullptr;
   uint32_t m = 0, n = 0, k = 0;
+  // strided problems (W [problems][n][k]): A row i of problem q is
+  // i * a_row_stride + q * a_prob_row (< a_rows_total, 0 = m * problems);
+  // its output row starts at i * out_row_stride (0 = n) + q * out_prob_col
+  uint32_t problems = 1, a_rows_total = 0, a_row_stride = 1, a_prob_row = 0;
+  uint64_t out_row_stride = 0, out_prob_col = 0;
   bool bf16 = false;
   ScaleFmt scale_fmt = kScaleF32;
   OutKind out_kind = kOutBf16;

@@ -325,12 +325,14 @@ def _grouped(x, w, sw, t, g, ng, kg):
     return to_host(aq), to_host(out), _flag(flag)
 
 
-def test_grouped_fp8_gemm_reference_geometry(eng):
+@pytest.mark.parametrize("t", [64, 512])
+def test_grouped_fp8_gemm_reference_geometry(eng, t):
     """The attention wo_a geometry of the reference (G = 8, N_g = 1024,
     K_g = 4096; deepseek_attention_dense_primitives_test.cpp:93-106) at 64
-    tokens: quantised activations bit-exact, every output against the
-    oracle."""
-    t, g, ng, kg = 64, 8, 1024, 4096
+    tokens (the 128 x 128 kernel) and 512 (the big-tile kernel's strided
+    problems): quantised activations bit-exact, the outputs of every token
+    (64) or of 24 sampled tokens (512) against the oracle."""
+    g, ng, kg = 8, 1024, 4096
     x = synth.bf16_normal(synth.config_seed(4, 12000), (t * g, kg))
     w = _codes(synth.config_seed(4, 12001), (g * ng, kg))
     sw = (112 + synth.splitmix64(12002, g * (ng // 128) * (kg // 128)) % np.uint64(6)).astype(np.uint8)
@@ -339,26 +341,29 @@ def test_grouped_fp8_gemm_reference_geometry(eng):
     assert flag == 0
     xq, xs = oracle.fp8_quant_ue8m0(oracle.bf16_bits_to_f32(x))
     np.testing.assert_array_equal(aq, xq)
-    ref = np.empty((t, g * ng), np.float32)
+    toks = np.arange(t) if t <= 64 else np.unique(np.linspace(0, t - 1, 24).astype(np.int64))
+    ref = np.empty((len(toks), g * ng), np.float32)
     for gi in range(g):
-        rows = np.arange(t) * g + gi
+        rows = toks * g + gi
         ref[:, gi * ng:(gi + 1) * ng] = oracle.fp8_gemm_ue8m0(
             np.ascontiguousarray(xq[rows]), np.ascontiguousarray(xs[rows]),
             np.ascontiguousarray(w[gi * ng:(gi + 1) * ng]), np.ascontiguousarray(sw[gi * ng // 128:(gi + 1) * ng // 128]))
-    assert_close(oracle.bf16_bits_to_f32(out), ref, "grouped fp8 8/1024/4096")
+    assert_close(oracle.bf16_bits_to_f32(out)[toks], ref, f"grouped fp8 8/1024/4096 at {t} tokens")
 
 
-def test_grouped_fp8_gemm_stores_nonfinite(eng):
+@pytest.mark.parametrize("t,ng", [(2, 128), (256, 1024)])
+def test_grouped_fp8_gemm_stores_nonfinite(eng, t, ng):
     """As the reference's grouped kernel does (deepseek_attention_dense_
     primitives.cu:247-249): a non-finite sum raises 2048 and its bf16 value
-    is stored; finite elements are untouched by it."""
-    t, g, ng, kg = 2, 8, 128, 128
+    is stored; finite elements are untouched by it (small-M kernel at 2
+    tokens, big-tile kernel at 256 tokens x 1024 columns)."""
+    g, kg = 8, 128
     x = synth.bf16_normal(synth.config_seed(4, 12100), (t * g, kg))
     x[:, 0] = 0x4380  # 256.0 in every row: group amax >= 256
     w = np.zeros((g * ng, kg), np.uint8)
     w[:, 0] = 0x7E  # 448
     sw = np.full((g * ng // 128, kg // 128), 127, np.uint8)
-    sw[3, 0] = 254  # group 3: 2^127 scale, the sum overflows
+    sw[3 * ng // 128:4 * ng // 128, 0] = 254  # group 3: 2^127 scale, the sum overflows
     _, out, flag = _grouped(x, w, sw, t, g, ng, kg)
     assert flag == 2048
     vals = oracle.bf16_bits_to_f32(out).reshape(t, g, ng)
