@@ -9,10 +9,14 @@
 // With a few activation rows the work is a weight stream, and the 128x128
 // tiles of gemm_mfma.hip give such a call N/128 blocks (8 for N = 1024): a
 // handful of CUs each walking all of K.  Here a block owns 16 weight rows
-// and its waves split K into runs of at most SPW 128-deep steps, so N/16
-// blocks x up to 16 waves cover the GPU:
-//   * every load of a wave (its W run, the activation rows, the scales) is
-//     issued before the first wait: the W fragments in the MFMA operand
+// and one chunk of up to 64 activation rows (grid z), and its waves split K
+// into runs of at most SPW 128-deep steps, so N/16 blocks x chunks x up to
+// 16 waves cover the GPU (a chunk past the first streams its weight rows
+// again, mostly from L2 and MALL, as the blocks of one weight block run
+// side by side):
+//   * every load of a wave's batch of SPW steps (its W run, the activation
+//     rows, the scales; one batch unless K is long for the wave count) is
+//     issued before the batch's first wait: the W fragments in the MFMA operand
 //     layout (FP8: lane (lr, lg) holds row lr, bytes [16lg, +16) and
 //     [64 + 16lg, +16) of the step; FP4: bytes [16lg, +16) of the row's 64),
 //     non-temporal;
@@ -28,6 +32,8 @@
 // activation rows out of range -> err_code, UE8M0 0xFF -> err_scale, a
 // non-finite result -> err_nonfinite (the element is stored only when
 // write_nonfinite is set, as the reference's grouped kernel does).
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -53,12 +59,14 @@ struct SmallParams {
   uint32_t err_code, err_scale, err_nonfinite;
 };
 
-template <int WF, int SCALE, int WAVES, int MT, int SPW>
+// BATCHED: a wave's run may be longer than SPW steps and is walked in
+// batches of SPW; otherwise the host guarantees one batch.
+template <int WF, int SCALE, int WAVES, int MT, int SPW, bool BATCHED>
 __global__ __launch_bounds__(WAVES * 64) void small_m_gemm_kernel(SmallParams p) {
   extern __shared__ __align__(16) float red[];  // [WAVES][MT][4][64]
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t lr = lane & 15, lg = lane >> 4;
-  const uint32_t prob = blockIdx.y, n0 = blockIdx.x * 16;
+  const uint32_t prob = blockIdx.y, n0 = blockIdx.x * 16, rbase = blockIdx.z * kSmallMChunkRows;
   const uint32_t K = p.k, KB = K / 128;
   const uint32_t s0 = wave * KB / WAVES, s1 = (wave + 1) * KB / WAVES;  // runs differ by at most one step
   const uint32_t cnt = s1 - s0;
@@ -71,7 +79,7 @@ __global__ __launch_bounds__(WAVES * 64) void small_m_gemm_kernel(SmallParams p)
 #pragma unroll
   for (int c = 0; c < MT; ++c) {
     // rows past m read row m - 1: their sums are never stored
-    const uint32_t i = min(16u * c + lr, p.m - 1);
+    const uint32_t i = min(rbase + 16u * c + lr, p.m - 1);
     uint64_t r = (uint64_t)i * p.a_row_stride + (uint64_t)prob * p.a_prob_row;
     if (r >= p.a_rows_total) {
       bad |= kErrCode;
@@ -80,106 +88,111 @@ __global__ __launch_bounds__(WAVES * 64) void small_m_gemm_kernel(SmallParams p)
     arow[c] = r;
   }
 
-  // ---- every load of the wave's run, before any wait (steps past the run
-  // repeat its last step and are not computed)
-  v4i wl[SPW][2];
-  v4i al[SPW][MT][2];
-  uint32_t sw[SPW], sa[SPW][MT];
   const uint8_t* wsb = static_cast<const uint8_t*>(p.w_scale);
   const uint8_t* asb = static_cast<const uint8_t*>(p.a_scale);
-#pragma unroll
-  for (int j = 0; j < SPW; ++j) {
-    const uint32_t st = s0 + min((uint32_t)j, cnt - 1);
-    if constexpr (WF == kSmallFp8) {
-      wl[j][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + (uint64_t)st * 128));
-      wl[j][1] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + (uint64_t)st * 128 + 64));
-    } else {
-      wl[j][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + (uint64_t)st * 64));
-    }
-#pragma unroll
-    for (int c = 0; c < MT; ++c) {
-      const uint8_t* ap = p.a + arow[c] * K + (uint64_t)st * 128 + lg * 16;
-      al[j][c][0] = *reinterpret_cast<const v4i*>(ap);
-      al[j][c][1] = *reinterpret_cast<const v4i*>(ap + 64);
-    }
-    if constexpr (WF == kSmallFp8) {
-      // one scale per (128 W rows, 128 k): the same for the block's 16 rows
-      const uint64_t si = ((uint64_t)prob * (p.n / 128) + n0 / 128) * KB + st;
-      sw[j] = SCALE == kScaleF32 ? reinterpret_cast<const uint32_t*>(wsb)[si] : wsb[si];
-    } else {
-      // one scale per (W row, 32 k): the block the lane's 32 values are in
-      sw[j] = wsb[wrow_g * (K / 32) + st * 4 + lg];
-    }
-#pragma unroll
-    for (int c = 0; c < MT; ++c) {
-      const uint64_t si = arow[c] * KB + st;
-      sa[j][c] = SCALE == kScaleF32 ? reinterpret_cast<const uint32_t*>(asb)[si] : asb[si];
-    }
-  }
-
   v4f acc[MT];
 #pragma unroll
   for (int c = 0; c < MT; ++c) acc[c] = v4f{0.f, 0.f, 0.f, 0.f};
+  // the run in batches of SPW steps
+  const uint32_t nb = BATCHED ? cnt : min(cnt, (uint32_t)SPW);
+  for (uint32_t b0 = 0; b0 < nb; b0 += SPW) {
+    const uint32_t bn = min((uint32_t)SPW, cnt - b0);
+    // ---- every load of the batch, before any wait (steps past the run
+    // repeat its last step and are not computed)
+    v4i wl[SPW][2];
+    v4i al[SPW][MT][2];
+    uint32_t sw[SPW], sa[SPW][MT];
 #pragma unroll
-  for (int j = 0; j < SPW; ++j) {
-    if ((uint32_t)j >= cnt) break;  // wave-uniform
-    if (p.check_codes) {
-      // NaN codes count as 0 (and raise the code bit), as the reference
-      // decodes them
-      uint32_t nan = 0;
-      auto clean = [&nan](v4i& v) __attribute__((always_inline)) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t nq = e4m3_nan_bytes((uint32_t)v[q]);
-          v[q] = (int)e4m3_nan_to_zero((uint32_t)v[q], nq);
-          nan |= nq;
-        }
-      };
+    for (int j = 0; j < SPW; ++j) {
+      const uint32_t st = s0 + b0 + min((uint32_t)j, bn - 1);
       if constexpr (WF == kSmallFp8) {
-        clean(wl[j][0]);
-        clean(wl[j][1]);
+        wl[j][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + (uint64_t)st * 128));
+        wl[j][1] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + (uint64_t)st * 128 + 64));
+      } else {
+        wl[j][0] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wp + (uint64_t)st * 64));
       }
 #pragma unroll
       for (int c = 0; c < MT; ++c) {
-        clean(al[j][c][0]);
-        clean(al[j][c][1]);
+        const uint8_t* ap = p.a + arow[c] * K + (uint64_t)st * 128 + lg * 16;
+        al[j][c][0] = *reinterpret_cast<const v4i*>(ap);
+        al[j][c][1] = *reinterpret_cast<const v4i*>(ap + 64);
       }
-      if (nan) bad |= kErrCode;
-    }
-    if constexpr (SCALE == kScaleUe8m0) {
-      // a 0xFF scale raises the scale bit and its block adds nothing (the
-      // reference skips the block): the operand bytes it scales become 0
-      uint32_t ff = 0;
-      if (sw[j] == 0xffu) {
-        ff = 1;
-        sw[j] = 127;
-        wl[j][0] = v4i{0, 0, 0, 0};
-        wl[j][1] = v4i{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int c = 0; c < MT; ++c)
-        if (sa[j][c] == 0xffu) {
-          ff = 1;
-          sa[j][c] = 127;
-          al[j][c][0] = v4i{0, 0, 0, 0};
-          al[j][c][1] = v4i{0, 0, 0, 0};
-        }
-      if (ff) bad |= kErrScale;
-    }
-    const v8i wop = WF == kSmallFp8 ? cat8(wl[j][0], wl[j][1]) : cat8(wl[j][0], v4i{0, 0, 0, 0});
-    constexpr int kFmtW = WF == kSmallFp8 ? 0 : 4;
-#pragma unroll
-    for (int c = 0; c < MT; ++c) {
-      const v8i aop = cat8(al[j][c][0], al[j][c][1]);
-      if constexpr (SCALE == kScaleUe8m0) {
-        acc[c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wop, aop, acc[c], kFmtW, 0, 0, (int)sw[j], 0,
-                                                                  (int)sa[j][c]);
+      if constexpr (WF == kSmallFp8) {
+        // one scale per (128 W rows, 128 k): the same for the block's 16 rows
+        const uint64_t si = ((uint64_t)prob * (p.n / 128) + n0 / 128) * KB + st;
+        sw[j] = SCALE == kScaleF32 ? reinterpret_cast<const uint32_t*>(wsb)[si] : wsb[si];
       } else {
-        const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wop, aop, v4f{0.f, 0.f, 0.f, 0.f}, kFmtW, 0,
-                                                                       0, 127, 0, 127);
-        const float cf = __uint_as_float(sa[j][c]) * __uint_as_float(sw[j]);
+        // one scale per (W row, 32 k): the block the lane's 32 values are in
+        sw[j] = wsb[wrow_g * (K / 32) + st * 4 + lg];
+      }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[c][i] = __builtin_fmaf(t[i], cf, acc[c][i]);
+      for (int c = 0; c < MT; ++c) {
+        const uint64_t si = arow[c] * KB + st;
+        sa[j][c] = SCALE == kScaleF32 ? reinterpret_cast<const uint32_t*>(asb)[si] : asb[si];
+      }
+    }
+
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      if ((uint32_t)j >= bn) break;  // wave-uniform
+      if (p.check_codes) {
+        // NaN codes count as 0 (and raise the code bit), as the reference
+        // decodes them
+        uint32_t nan = 0;
+        auto clean = [&nan](v4i& v) __attribute__((always_inline)) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t nq = e4m3_nan_bytes((uint32_t)v[q]);
+            v[q] = (int)e4m3_nan_to_zero((uint32_t)v[q], nq);
+            nan |= nq;
+          }
+        };
+        if constexpr (WF == kSmallFp8) {
+          clean(wl[j][0]);
+          clean(wl[j][1]);
+        }
+#pragma unroll
+        for (int c = 0; c < MT; ++c) {
+          clean(al[j][c][0]);
+          clean(al[j][c][1]);
+        }
+        if (nan) bad |= kErrCode;
+      }
+      if constexpr (SCALE == kScaleUe8m0) {
+        // a 0xFF scale raises the scale bit and its block adds nothing (the
+        // reference skips the block): the operand bytes it scales become 0
+        uint32_t ff = 0;
+        if (sw[j] == 0xffu) {
+          ff = 1;
+          sw[j] = 127;
+          wl[j][0] = v4i{0, 0, 0, 0};
+          wl[j][1] = v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int c = 0; c < MT; ++c)
+          if (sa[j][c] == 0xffu) {
+            ff = 1;
+            sa[j][c] = 127;
+            al[j][c][0] = v4i{0, 0, 0, 0};
+            al[j][c][1] = v4i{0, 0, 0, 0};
+          }
+        if (ff) bad |= kErrScale;
+      }
+      const v8i wop = WF == kSmallFp8 ? cat8(wl[j][0], wl[j][1]) : cat8(wl[j][0], v4i{0, 0, 0, 0});
+      constexpr int kFmtW = WF == kSmallFp8 ? 0 : 4;
+#pragma unroll
+      for (int c = 0; c < MT; ++c) {
+        const v8i aop = cat8(al[j][c][0], al[j][c][1]);
+        if constexpr (SCALE == kScaleUe8m0) {
+          acc[c] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wop, aop, acc[c], kFmtW, 0, 0, (int)sw[j], 0,
+                                                                    (int)sa[j][c]);
+        } else {
+          const v4f t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wop, aop, v4f{0.f, 0.f, 0.f, 0.f}, kFmtW, 0,
+                                                                         0, 127, 0, 127);
+          const float cf = __uint_as_float(sa[j][c]) * __uint_as_float(sw[j]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[c][i] = __builtin_fmaf(t[i], cf, acc[c][i]);
+        }
       }
     }
   }
@@ -193,7 +206,7 @@ __global__ __launch_bounds__(WAVES * 64) void small_m_gemm_kernel(SmallParams p)
   __syncthreads();
   if (tid < 64u * MT) {
     const uint32_t c = tid / 64, l = tid % 64;
-    const uint32_t row = 16 * c + (l & 15), col = n0 + 4 * (l >> 4);
+    const uint32_t row = rbase + 16 * c + (l & 15), col = n0 + 4 * (l >> 4);
     if (row < p.m) {
       float v[4];
 #pragma unroll
@@ -231,32 +244,34 @@ __global__ __launch_bounds__(WAVES * 64) void small_m_gemm_kernel(SmallParams p)
   }
 }
 
-template <int WF, int SCALE, int WAVES, int MT, int SPW>
+template <int WF, int SCALE, int WAVES, int MT, int SPW, bool B>
 void launch_cfg(const SmallParams& sp, uint32_t problems, hipStream_t s) {
   const size_t lds = (size_t)WAVES * MT * 4 * 64 * sizeof(float);
-  hipLaunchKernelGGL((small_m_gemm_kernel<WF, SCALE, WAVES, MT, SPW>), dim3(sp.n / 16, problems), dim3(WAVES * 64),
-                     lds, s, sp);
+  const uint32_t chunks = (sp.m + kSmallMChunkRows - 1) / kSmallMChunkRows;
+  hipLaunchKernelGGL((small_m_gemm_kernel<WF, SCALE, WAVES, MT, SPW, B>), dim3(sp.n / 16, problems, chunks),
+                     dim3(WAVES * 64), lds, s, sp);
 }
 
-// MT 16-row activation blocks (m 33..48 runs as 4); SPW the longest run:
-// 2 or 4 steps with one activation block, 2 with more
-template <int WF, int SCALE, int WAVES>
+// MT 16-row activation blocks per chunk (m 33..48 runs as 4); SPW the
+// batch: 2 or 4 steps with one activation block, 2 with more
+template <int WF, int SCALE, int WAVES, bool B>
 void launch_mt(const SmallParams& sp, uint32_t problems, uint32_t run, hipStream_t s) {
-  const uint32_t mt = (sp.m + 15) / 16;
+  const uint32_t mt = (std::min(sp.m, kSmallMChunkRows) + 15) / 16;
   if (mt == 1) {
-    if (run <= 2) launch_cfg<WF, SCALE, WAVES, 1, 2>(sp, problems, s);
-    else launch_cfg<WF, SCALE, WAVES, 1, 4>(sp, problems, s);
+    if (run <= 2) launch_cfg<WF, SCALE, WAVES, 1, 2, B>(sp, problems, s);
+    else launch_cfg<WF, SCALE, WAVES, 1, 4, B>(sp, problems, s);
   } else if (mt == 2) {
-    launch_cfg<WF, SCALE, WAVES, 2, 2>(sp, problems, s);
+    launch_cfg<WF, SCALE, WAVES, 2, 2, B>(sp, problems, s);
   } else {
-    launch_cfg<WF, SCALE, WAVES, 4, 2>(sp, problems, s);
+    launch_cfg<WF, SCALE, WAVES, 4, 2, B>(sp, problems, s);
   }
 }
 
 // Waves per block: the fewest of 4, 8, 16 whose runs are at most 4 (one
-// activation block) or 2 steps, doubled while the grid has fewer than 2048
-// waves and every run keeps at least two steps; 0 when no split fits (the
-// caller uses the tiled kernel).
+// activation block) or 2 steps (one batch), doubled while the grid has
+// fewer than 2048 waves and every run keeps at least two steps; 0 when no
+// single-batch split fits (the caller then runs 8 waves in batches: the
+// batch loop's registers do not fit 16 waves per block).
 int pick_waves(uint32_t blocks, uint32_t kb, uint32_t m) {
   const uint32_t spw = m <= 16 ? 4 : 2;
   int waves = 0;
@@ -272,17 +287,22 @@ int pick_waves(uint32_t blocks, uint32_t kb, uint32_t m) {
 
 template <int WF, int SCALE>
 void launch_waves(const SmallParams& sp, uint32_t problems, int waves, hipStream_t s) {
-  const uint32_t kb = sp.k / 128, run = (kb + waves - 1) / waves;
-  if (waves == 4) launch_mt<WF, SCALE, 4>(sp, problems, run, s);
-  else if (waves == 8) launch_mt<WF, SCALE, 8>(sp, problems, run, s);
-  else launch_mt<WF, SCALE, 16>(sp, problems, run, s);
+  const uint32_t kb = sp.k / 128;
+  if (!waves) {
+    launch_mt<WF, SCALE, 8, true>(sp, problems, (kb + 7) / 8, s);
+    return;
+  }
+  const uint32_t run = (kb + waves - 1) / waves;
+  if (waves == 4) launch_mt<WF, SCALE, 4, false>(sp, problems, run, s);
+  else if (waves == 8) launch_mt<WF, SCALE, 8, false>(sp, problems, run, s);
+  else launch_mt<WF, SCALE, 16, false>(sp, problems, run, s);
 }
 
 St launch_small(SmallParams sp, int wf, ScaleFmt fmt, uint32_t problems, hipStream_t s, bool& taken) {
   taken = false;
-  if (sp.m == 0 || sp.m > kSmallMRows || sp.n % 16 || sp.k % 128) return Ok();
-  const int waves = pick_waves(sp.n / 16 * problems, sp.k / 128, sp.m);
-  if (!waves) return Ok();
+  if (sp.m == 0 || sp.n % 16 || sp.k % 128 || !SmallMTakes(sp.m, sp.n, problems)) return Ok();
+  const uint32_t chunks = (sp.m + kSmallMChunkRows - 1) / kSmallMChunkRows;
+  const int waves = pick_waves(sp.n / 16 * problems * chunks, sp.k / 128, std::min(sp.m, kSmallMChunkRows));
   taken = true;
   St clean = RequireCleanLastError();
   if (!clean.ok()) return clean;

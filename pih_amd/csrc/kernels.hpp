@@ -103,11 +103,18 @@ struct Fp4GemmArgs {
 };
 St LaunchFp4Gemm(const Fp4GemmArgs& a);
 
-// Small-M (m <= kSmallMRows) dense GEMM with FP8 or MXFP4 weights and e4m3
-// activations (gemm_small_m.hip): 16 weight rows per block, the block's
-// waves splitting K.  `taken` is false when the shape has no fitting split
-// (the caller then uses the tiled kernel); the callers' checks come first.
-constexpr uint32_t kSmallMRows = 64;
+// Small-M dense GEMM with FP8 or MXFP4 weights and e4m3 activations
+// (gemm_small_m.hip): 16 weight rows and up to 64 activation rows per
+// block, the block's waves splitting K.  It takes m <= 64, and m up to
+// kSmallMRows while the 128 x 128 tiled kernel would have fewer than 128
+// tiles (too few blocks to stream the weights).  `taken` is false when it
+// does not take the shape (the caller then uses the tiled kernel); the
+// callers' checks come first.
+constexpr uint32_t kSmallMChunkRows = 64, kSmallMRows = 256;
+inline bool SmallMTakes(uint32_t m, uint32_t n, uint32_t problems) {
+  if (m <= kSmallMChunkRows) return m > 0;
+  return m <= kSmallMRows && (uint64_t)((m + 127) / 128) * ((n + 127) / 128) * problems < 128;
+}
 St LaunchFp8SmallM(const BlockGemmArgs& a, bool& taken);
 St LaunchFp4SmallM(const Fp4GemmArgs& a, bool& taken);
 // MoE problems: experts with at most Fp4MoeLightRows(a) rows (64; 0 when

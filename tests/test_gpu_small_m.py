@@ -1,13 +1,17 @@
 """GPU parity of the small-M GEMM path (gemm_small_m.hip): the dense FP8
 GEMM (UE8M0 through the DeepSeek table, fp32 scales through the linear
 pack), the FP4 x FP8 GEMM and the grouped FP8 GEMM with at most 64
-activation rows, which stream their weights over 16-row blocks instead of
-the 128 x 128 tiles.  Every output is checked against the CPU oracle
-(max_rel <= 1e-2 normwise, cosine >= 0.9999), across the activation-block
-counts (1, 2 and 4 blocks of 16 rows), K splits with equal and unequal runs
-per wave, a K with no fitting split (the tiled fallback), and the error bits
-of the reference kernels (NaN code 1, scale 0xFF 2, non-finite result 4: the
-element is skipped, as deepseek_fp8_gemm.cu:67-70 skips it)."""
+activation rows, and with up to 256 rows in 64-row chunks where the
+128 x 128 tiles would be fewer than 128 (M = 65..256 at N <= 4096), which
+stream their weights over 16-row blocks instead of the tiles.  Every output
+is checked against the CPU oracle (max_rel <= 1e-2 normwise, cosine >=
+0.9999), across the activation-block counts (1, 2 and 4 blocks of 16 rows),
+chunk counts 2-4 with a short last chunk, K splits with equal and unequal
+runs per wave, runs of several batches (K = 12288 past 16 rows), the tiled
+fallback (M = 65..256 at N = 128, K = 12288: one tile), and the error bits
+of the reference kernels (NaN code 1, scale 0xFF 2, non-finite
+result 4: the element is skipped, as deepseek_fp8_gemm.cu:67-70 skips
+it)."""
 import numpy as np
 import pytest
 
@@ -26,6 +30,7 @@ def eng():
 
     from pih_amd.device import engine_stream
 
+    oracle.set_threads(min(16, __import__("os").cpu_count() or 1))
     with engine_stream() as s:
         yield s
         torch.cuda.synchronize()
@@ -72,7 +77,7 @@ def _fp8_inputs(seed, m, n, k):
     return a, sa, w, sw.reshape(n // 128, k // 128)
 
 
-@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64])
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 65, 128, 200])
 @pytest.mark.parametrize("n,k", [(1024, 4096), (384, 7168), (256, 1024), (128, 12288)])
 def test_fp8_ue8m0_small_m(eng, m, n, k):
     a, sa, w, sw = _fp8_inputs(synth.config_seed(4, 15000 + m + n), m, n, k)
@@ -81,7 +86,8 @@ def test_fp8_ue8m0_small_m(eng, m, n, k):
     assert_close(oracle.bf16_bits_to_f32(got), oracle.fp8_gemm_ue8m0(a, sa, w, sw), f"fp8 small m {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 512, 2048), (16, 256, 7168), (40, 512, 4096), (64, 128, 1024)])
+@pytest.mark.parametrize("m,n,k", [(1, 512, 2048), (16, 256, 7168), (40, 512, 4096), (64, 128, 1024),
+                                   (128, 512, 4096), (256, 1024, 2048)])
 @pytest.mark.parametrize("out_type", [abi.OUTPUT_BF16, abi.OUTPUT_F32])
 def test_fp8_f32_scales_small_m(eng, m, n, k, out_type):
     from pih_amd import linear
@@ -97,7 +103,7 @@ def test_fp8_f32_scales_small_m(eng, m, n, k, out_type):
     assert_close(got, oracle.fp8_gemm_f32(xq, xs, w, ws), f"fp8 f32 small m {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m", [1, 8, 16, 17, 64])
+@pytest.mark.parametrize("m", [1, 8, 16, 17, 64, 128, 256])
 @pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 2048), (256, 7168)])
 def test_fp4_small_m(eng, m, n, k):
     import torch
@@ -147,10 +153,11 @@ def test_small_m_error_bits(eng):
                                                                                 np.float32)))
 
 
-@pytest.mark.parametrize("t", [1, 3, 16])
+@pytest.mark.parametrize("t", [1, 3, 16, 100])
 def test_grouped_fp8_small_t(eng, t):
     """The attention wo_a geometry (G = 8, 1024, 4096) at decode token
-    counts: A row t * 8 + g of the quantised input feeds group g."""
+    counts (and at 100, two row chunks): A row t * 8 + g of the quantised
+    input feeds group g."""
     import torch
 
     from pih_amd.device import ptr, stream_handle
