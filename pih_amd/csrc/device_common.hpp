@@ -33,15 +33,36 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) {
-  const uint32_t raw = __float_as_uint(v);
-  if ((raw & 0x7fffffffu) > 0x7f800000u) return (raw >> 16) | 0x0040u;
-  return (raw + 0x7fffu + ((raw >> 16) & 1u)) >> 16;
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 bits by v_cvt_pk_bf16_f32: round to nearest even, a NaN
+// keeps its sign and upper payload with the quiet bit set, i.e.
+// (raw + 0x7fff + ((raw >> 16) & 1)) >> 16 and (raw >> 16) | 0x40 for a
+// NaN (the same bits for all 2^32 inputs, checked on gfx950 with IEEE fp32
+// denormals, the kernels' mode).
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
 }
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float v) { return f32x2_to_bf16x2(v, 0.0f) & 0xffffu; }
 
 __device__ __forceinline__ float bf16_round(float v) {
   return bf16_bits_to_f32(f32_to_bf16_bits(v));
 }
+
+// SiLU x / (1 + e^-x) with the quotient as v_rcp_f32, a product and one FMA
+// correction, sign restored: bit-equal to the IEEE quotient for every
+// finite x whose denominator stays below 2^126 (all 2^32 inputs checked on
+// gfx950).  `big` is set for the others (x < -87.3: the reciprocal
+// underflows); there the caller uses silu_ieee.
+__device__ __forceinline__ float silu_rcp(float x, bool& big) {
+  const float d = 1.0f + expf(-x);
+  big |= !(d < 0x1p126f);
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float q = x * r;
+  return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q, d, x), r, q), x);
+}
+__device__ __forceinline__ float silu_ieee(float x) { return x / (1.0f + expf(-x)); }
 
 // Nearest finite e4m3fn code with ties to the even code; |v| <= 448 and
 // finite is the caller's contract (every quantizer clamps first).

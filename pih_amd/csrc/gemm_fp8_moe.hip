@@ -57,6 +57,7 @@ constexpr int kWaitVm6 = 0x0F76;     // vmcnt(6)
 // operand kinds: e4m3 with block scales, or bf16 (no scales)
 enum : int { kOpFp8 = 0, kOpBf16 = 1 };
 constexpr int kWaitVm0 = 0x0F70;     // vmcnt(0)
+constexpr uint32_t kCodePitch = 144;  // staged e4m3 code rows (128 bytes + 16)
 
 // LDS byte address of a __shared__ object
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -114,6 +115,7 @@ struct MoeParams {
   uint32_t a_row_stride, a_prob_row;
   uint64_t out_prob_col;
   uint32_t write_nonfinite;  // store a non-finite result (and flag it)
+  uint32_t stage_out;        // output rows 16-byte aligned: stores staged in LDS
   const uint32_t* skip_if;   // every block exits at once if (*skip_if & skip_bit)
   uint32_t skip_bit;
   uint64_t out_row_stride;
@@ -601,6 +603,40 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   __builtin_amdgcn_s_waitcnt(kWaitVm0);
 
   // ---- epilogue: lane holds out[row wm*64 + r*16 + lr][4*lg + i] of block nb
+  // SwiGLU tiles: bf16(SiLU(g) x u x w) of a gate value g = bf16(ga) clamped
+  // to the limit and an up value u = bf16(ua) clamped to +-limit; NaN where
+  // g or u is not finite
+  auto swiglu_one = [&](float ga, float ua, float w, auto IEEE, bool& big) __attribute__((always_inline)) -> float {
+    float gt = bf16_round(ga), up = bf16_round(ua);
+    if (!(__builtin_isfinite(gt) && __builtin_isfinite(up))) return __builtin_nanf("");
+    if (p.limit > 0.0f) {
+      gt = fminf(gt, p.limit);
+      up = fminf(fmaxf(up, -p.limit), p.limit);
+    }
+    const float sl = decltype(IEEE)::value ? silu_ieee(gt) : silu_rcp(gt, big);
+    return bf16_round(sl * up * w);
+  };
+  // the tile's SwiGLU values v[r][h][i] of gate acc[h][r][i] and up
+  // acc[h + 2][r][i] with route weight w[r]: SiLU's quotient by reciprocal
+  // (silu_rcp), redone with the IEEE division when a lane of the wave needs
+  // it (the same bits either way)
+  auto swiglu_values = [&](float (&v)[4][2][4], const float (&w)[4]) __attribute__((always_inline)) {
+    bool big = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[r][h][i] = swiglu_one(acc[h][r][i], acc[h + 2][r][i], w[r], std::false_type{}, big);
+    if (__builtin_amdgcn_ballot_w64(big)) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[r][h][i] = swiglu_one(acc[h][r][i], acc[h + 2][r][i], w[r], std::true_type{}, big);
+    }
+  };
   if constexpr (OUT == kOutSwiGluFp8) {
     // SwiGLU x route weight rounded to bf16 (the values the bf16 output
     // holds), then quantised to e4m3 exactly as fp8_quant_kernel would: the
@@ -608,28 +644,23 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     // its absolute maximum meets across the 4 waves of a row half in LDS
     __shared__ float s_amax[BM][4];
     float vq[4][2][4];
+    float rwt[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t rr = wm * 64 + r * 16 + lr;
+      rwt[r] = rr < rows && p.row_weight ? p.row_weight[row0 + rr] : 1.0f;
+    }
+    swiglu_values(vq, rwt);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t rr = wm * 64 + r * 16 + lr;
       const bool live = rr < rows;
-      const float rwt = live && p.row_weight ? p.row_weight[row0 + rr] : 1.0f;
       float am = 0.0f;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float gt = bf16_round(acc[h][r][i]);
-          float up = bf16_round(acc[h + 2][r][i]);
-          float v = 0.0f;
-          if (__builtin_isfinite(gt) && __builtin_isfinite(up)) {
-            if (p.limit > 0.0f) {
-              gt = fminf(gt, p.limit);
-              up = fminf(fmaxf(up, -p.limit), p.limit);
-            }
-            v = bf16_round((gt / (1.0f + expf(-gt))) * up * rwt);
-          } else {
-            v = __builtin_nanf("");
-          }
+          float v = vq[r][h][i];
           if (!__builtin_isfinite(v)) {
             if (live) bad |= kErrNonFinite;
             v = 0.0f;
@@ -665,16 +696,103 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
         inv = 1.0f / scale;
         if (wn == 0 && lg == 0) static_cast<float*>(p.out_scale)[g] = scale;
       }
-      uint8_t* dst = static_cast<uint8_t*>(p.out) + (uint64_t)(row0 + rr) * p.out_row_stride + nt * 128 + wn * 32 +
-                     4 * lg;
+      // codes of row rr, bytes wn*32 + h*16 + 4lg: into the staged tile
+      // (rows 144 bytes apart: a store's 16 rows x 4 lanes hit 64 banks) or
+      // straight to memory
+      uint8_t* dst = p.stage_out ? smem + rr * kCodePitch + wn * 32 + 4 * lg
+                                 : static_cast<uint8_t*>(p.out) + (uint64_t)(row0 + rr) * p.out_row_stride + nt * 128 +
+                                       wn * 32 + 4 * lg;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
         *reinterpret_cast<uint32_t*>(dst + h * 16) =
             SCALE == kScaleUe8m0 ? e4m3_quant4_mul(vq[r][h], inv) : e4m3_quant4_recip(vq[r][h], scale, inv);
     }
+    if (p.stage_out) {
+      // whole 128-byte code rows, 16 bytes per lane
+      __syncthreads();
+#pragma unroll
+      for (uint32_t c = tid; c < BM * 8; c += NTH) {
+        const uint32_t R = c / 8, ch = c % 8;
+        if (R < rows)
+          *reinterpret_cast<v4i*>(static_cast<uint8_t*>(p.out) + (uint64_t)(row0 + R) * p.out_row_stride + nt * 128 +
+                                  ch * 16) = *reinterpret_cast<const v4i*>(smem + R * kCodePitch + ch * 16);
+      }
+    }
+  }
+  // Plain outputs: when no live block of the wave holds a non-finite value
+  // that must be skipped (the common case), every live block is stored
+  // whole, with no per-row or per-column test at all on a full tile;
+  // otherwise the per-element path below.
+  bool stored = false;
+  if constexpr (OUT == kOutBf16 || OUT == kOutF32) {
+    bool nonfin = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const v4f v = acc[nb][r];
+        const bool live = wm * 64 + r * 16 + lr < rows && nt * BN + wn * 64 + nb * 16 + 4 * lg < p.n;
+        if (live && !(__builtin_isfinite(v[0]) && __builtin_isfinite(v[1]) && __builtin_isfinite(v[2]) &&
+                      __builtin_isfinite(v[3])))
+          nonfin = true;
+      }
+    if (nonfin) bad |= kErrNonFinite;
+    const bool keep_finite = nonfin && p.err_nonfinite && !p.write_nonfinite;
+    // one decision for the block: every wave is past its main loop and its
+    // DMAs (vmcnt(0) above), so the stages are free for the staged tile
+    if (p.stage_out && !__syncthreads_or(keep_finite)) {
+      stored = true;
+      // the tile staged in LDS (rows padded by 32 bytes: the 16 rows of a
+      // fragment start 8 banks apart), then whole rows stored with 16 bytes
+      // per lane: 128-byte lines instead of 16 rows x 32 bytes per store
+      constexpr uint32_t OSZ = OUT == kOutF32 ? 4 : 2, PITCH = BN * OSZ + 32, CPR = BN * OSZ / 16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          uint8_t* d = smem + (wm * 64 + r * 16 + lr) * PITCH + (wn * 64 + nb * 16 + 4 * lg) * OSZ;
+          const v4f v = acc[nb][r];
+          if constexpr (OUT == kOutF32) *reinterpret_cast<v4f*>(d) = v;
+          else *reinterpret_cast<uint2*>(d) = uint2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
+        }
+      __syncthreads();
+#pragma unroll
+      for (uint32_t c = tid; c < BM * CPR; c += NTH) {
+        const uint32_t R = c / CPR, ch = c % CPR, col = nt * BN + ch * (16 / OSZ);
+        if (R < rows && col < p.n)
+          *reinterpret_cast<v4i*>(static_cast<uint8_t*>(p.out) +
+                                  ((uint64_t)(row0 + R) * p.out_row_stride + (uint64_t)expert * p.out_prob_col + col) *
+                                      OSZ) = *reinterpret_cast<const v4i*>(smem + R * PITCH + ch * 16);
+      }
+    } else if (!__builtin_amdgcn_ballot_w64(keep_finite)) {
+      stored = true;
+      auto store = [&](int r, int nb) __attribute__((always_inline)) {
+        const uint64_t o = (uint64_t)(row0 + wm * 64 + r * 16 + lr) * p.out_row_stride +
+                           (uint64_t)expert * p.out_prob_col + nt * BN + wn * 64 + nb * 16 + 4 * lg;
+        const v4f v = acc[nb][r];
+        if constexpr (OUT == kOutF32) *reinterpret_cast<v4f*>(static_cast<float*>(p.out) + o) = v;
+        else
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + o) =
+              uint2{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
+      };
+      if (rows == BM && nt * BN + BN <= p.n) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) store(r, nb);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (wm * 64 + r * 16 + lr >= rows) continue;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb)
+            if (nt * BN + wn * 64 + nb * 16 + 4 * lg < p.n) store(r, nb);
+        }
+      }
+    }
   }
 #pragma unroll
-  for (int r = 0; r < 4 && OUT != kOutSwiGluFp8; ++r) {
+  for (int r = 0; r < 4 && OUT != kOutSwiGluFp8 && !stored; ++r) {
     const uint32_t rr = wm * 64 + r * 16 + lr;
     if (rr >= rows) continue;
     const uint64_t orow = (uint64_t)(row0 + rr) * p.out_row_stride + (uint64_t)expert * p.out_prob_col;
@@ -768,6 +886,13 @@ void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out) 
   else hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutBf16>), dim3(grid), dim3(NTH), 0, s, mp);
 }
 
+// Output rows and problem column offsets on 16-byte boundaries: the kernel
+// may stage its tile in LDS and store whole rows.
+uint32_t StageOut(const void* out, uint64_t row_stride, uint64_t prob_col, OutKind kind) {
+  const uint64_t osz = kind == kOutF32 ? 4 : kind == kOutSwiGluFp8 ? 1 : 2;
+  return reinterpret_cast<uintptr_t>(out) % 16 == 0 && row_stride * osz % 16 == 0 && prob_col * osz % 16 == 0;
+}
+
 }  // namespace
 
 // Called by LaunchFp8BlockGemm for MoE problems without the code scan; the
@@ -792,6 +917,7 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
   mp.out_scale = a.out_scale;
   mp.out_row_stride = a.out_row_stride ? a.out_row_stride : (swiglu ? a.n / 2 : a.n);
   mp.n_tiles = swiglu ? a.n / 256 : (a.n + BN - 1) / BN;
+  mp.stage_out = StageOut(a.out, mp.out_row_stride, 0, a.out_kind);
   mp.limit = a.swiglu_limit;
   mp.err_code = a.err_code_bit;
   mp.err_scale = a.err_scale_bit;
@@ -842,6 +968,7 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.out_row_stride = a.out_row_stride ? a.out_row_stride : a.n;
   mp.out_prob_col = a.out_prob_col;
   mp.n_tiles = (a.n + BN - 1) / BN;
+  mp.stage_out = StageOut(a.out, mp.out_row_stride, mp.out_prob_col, a.out_kind);
   mp.err_code = a.error_flag ? a.err_code_bit : 0u;
   mp.err_scale = a.error_flag ? a.err_scale_bit : 0u;
   mp.err_nonfinite = a.error_flag ? a.err_nonfinite_bit : 0u;
