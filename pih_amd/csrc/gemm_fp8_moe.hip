@@ -37,6 +37,7 @@
 // Tile order: see moe_tile (streaming and multi-tile experts interleaved;
 // an 8 M x 4 N grouping of the multi-tile ones cut the L2-miss bytes by
 // 9 % but ran 3 % slower than M-fastest groups of 32).
+#include <algorithm>
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -58,6 +59,11 @@ constexpr int kWaitVm6 = 0x0F76;     // vmcnt(6)
 enum : int { kOpFp8 = 0, kOpBf16 = 1 };
 constexpr int kWaitVm0 = 0x0F70;     // vmcnt(0)
 constexpr uint32_t kCodePitch = 144;  // staged e4m3 code rows (128 bytes + 16)
+// s_waitcnt immediate waiting for vmcnt <= n (n < 64; bits [3:0] and [15:14])
+constexpr int vmcnt_enc(int n) { return ((n >> 4) << 14) | 0x0F70 | (n & 15); }
+static_assert(vmcnt_enc(7) == kWaitVm7 && vmcnt_enc(0) == kWaitVm0, "vmcnt encoding");
+// stores one lane of a persistent block issues per tile of plain output
+constexpr uint32_t kStoreOps = 16;
 
 // LDS byte address of a __shared__ object
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -124,6 +130,9 @@ struct MoeParams {
   uint32_t err_code, err_scale, err_nonfinite;
 };
 
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ v8i cat8(v4i x, v4i y) {
   return v8i{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
 }
@@ -144,7 +153,8 @@ __device__ __forceinline__ v8i cat8(v4i x, v4i y) {
 // walked M-fastest, so concurrently running tiles share W in L2.
 // The per-expert tile counts are scanned by the whole block (wave-level
 // shuffle scans plus the eight wave totals).
-__device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, uint32_t& rows, uint32_t& nt) {
+__device__ bool moe_tile(const MoeParams& p, uint32_t vb, uint32_t& expert, uint32_t& row0, uint32_t& rows,
+                         uint32_t& nt) {
   __shared__ uint32_t s_wave[2][NTH / 64];
   __shared__ uint32_t s_res[3];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -183,7 +193,7 @@ __device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, u
   const uint32_t exc_h = inc_h - cnt_h, exc_s = inc_s - cnt_s;
   const uint64_t Ls = (uint64_t)tot_s * NTL, T = ((uint64_t)tot_h + tot_s) * NTL;
   const uint32_t per = (uint32_t)((T + 7) / 8);
-  const uint32_t xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const uint32_t xcd = vb & 7, jj = vb >> 3;
   const uint64_t t = (uint64_t)xcd * per + jj;
   if (jj >= per || t >= T) return false;  // same for every thread
   const uint32_t s_lo = (uint32_t)(t * Ls / T), s_hi = (uint32_t)((t + 1) * Ls / T);
@@ -255,11 +265,12 @@ __device__ bool moe_tile(const MoeParams& p, uint32_t& expert, uint32_t& row0, u
 // Dense form: tile t of the problems x M x N tile grid (problem-major),
 // each XCD (blocks b % 8) walking one contiguous range, M-fastest in groups
 // of GROUP_M so that concurrent tiles share their W tile in L2.
-__device__ bool dense_tile(const MoeParams& p, uint32_t& prob, uint32_t& row0, uint32_t& rows, uint32_t& nt) {
+__device__ bool dense_tile(const MoeParams& p, uint32_t vb, uint32_t& prob, uint32_t& row0, uint32_t& rows,
+                           uint32_t& nt) {
   const uint32_t MT = p.dense_m_tiles, NTL = p.n_tiles;
   const uint64_t per_prob = (uint64_t)MT * NTL, T = per_prob * p.experts;
   const uint32_t per = (uint32_t)((T + 7) / 8);
-  const uint32_t xcd = blockIdx.x & 7, jj = blockIdx.x >> 3;
+  const uint32_t xcd = vb & 7, jj = vb >> 3;
   const uint64_t tt = (uint64_t)xcd * per + jj;
   if (jj >= per || tt >= T) return false;
   prob = (uint32_t)(tt / per_prob);
@@ -273,7 +284,114 @@ __device__ bool dense_tile(const MoeParams& p, uint32_t& prob, uint32_t& row0, u
   return true;
 }
 
-template <int OP, int SCALE, int OUT>
+// Persistent blocks (one per CU, each walking the tiles vb = blockIdx.x,
+// blockIdx.x + gridDim.x, ... of the sequence moe_tile defines) find their
+// tiles in a per-block LDS table instead: the experts' row offsets and the
+// inclusive counts of multi-tile M tiles and of one-tile experts, built
+// once, so a lookup is a binary search in LDS (no global read, no barrier).
+constexpr uint32_t kTableExperts = 1024;
+struct MoeTable {
+  uint32_t* off;    // [E + 1] row offsets
+  uint32_t* inc_h;  // [E] M tiles of the multi-tile experts 0..e
+  uint32_t* inc_s;  // [E] one-tile experts among 0..e
+};
+
+__device__ void moe_table_build(const MoeParams& p, const MoeTable& t) {
+  __shared__ uint32_t s_wave[2][NTH / 64];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = p.experts;
+  for (uint32_t e = tid; e <= E; e += NTH) t.off[e] = p.offsets[e];
+  __syncthreads();
+  const uint32_t per_t = (E + NTH - 1) / NTH;
+  auto m_tiles = [&](uint32_t e) -> uint32_t {
+    const uint32_t lo = t.off[e], hi = t.off[e + 1];
+    return hi > lo ? (hi - lo + BM - 1) / BM : 0u;
+  };
+  uint32_t cnt_h = 0, cnt_s = 0;
+  for (uint32_t j = 0; j < per_t; ++j) {
+    const uint32_t e = tid * per_t + j;
+    if (e < E) {
+      const uint32_t c = m_tiles(e);
+      cnt_h += c > 1 ? c : 0u;
+      cnt_s += c == 1 ? 1u : 0u;
+    }
+  }
+  uint32_t inc_h = cnt_h, inc_s = cnt_s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t vh = __shfl_up(inc_h, o, 64), vs = __shfl_up(inc_s, o, 64);
+    if ((int)lane >= o) inc_h += vh, inc_s += vs;
+  }
+  if (lane == 63) s_wave[0][wave] = inc_h, s_wave[1][wave] = inc_s;
+  __syncthreads();
+  uint32_t acc_h = inc_h - cnt_h, acc_s = inc_s - cnt_s;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w)
+    if (w < (int)wave) acc_h += s_wave[0][w], acc_s += s_wave[1][w];
+  for (uint32_t j = 0; j < per_t; ++j) {
+    const uint32_t e = tid * per_t + j;
+    if (e < E) {
+      const uint32_t c = m_tiles(e);
+      acc_h += c > 1 ? c : 0u;
+      acc_s += c == 1 ? 1u : 0u;
+      t.inc_h[e] = acc_h;
+      t.inc_s[e] = acc_s;
+    }
+  }
+  __syncthreads();
+}
+
+// first e < E with inc[e] > k (inc non-decreasing)
+__device__ __forceinline__ uint32_t first_above(const uint32_t* inc, uint32_t E, uint32_t k) {
+  uint32_t lo = 0, hi = E;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (inc[mid] > k) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
+}
+
+// moe_tile's mapping, read from the table; a tile of an invalid segment
+// raises the code bit and has no rows
+__device__ bool moe_table_tile(const MoeParams& p, const MoeTable& t, uint32_t vb, uint32_t& expert, uint32_t& row0,
+                               uint32_t& rows, uint32_t& nt, uint32_t& bad) {
+  const uint32_t E = p.experts, NTL = p.n_tiles;
+  const uint32_t tot_h = t.inc_h[E - 1], tot_s = t.inc_s[E - 1];
+  const uint64_t Ls = (uint64_t)tot_s * NTL, T = ((uint64_t)tot_h + tot_s) * NTL;
+  const uint32_t per = (uint32_t)((T + 7) / 8);
+  const uint32_t xcd = vb & 7, jj = vb >> 3;
+  const uint64_t tt = (uint64_t)xcd * per + jj;
+  if (jj >= per || tt >= T) return false;
+  const uint32_t s_lo = (uint32_t)(tt * Ls / T), s_hi = (uint32_t)((tt + 1) * Ls / T);
+  uint32_t e, mtile = 0;
+  if (s_hi > s_lo) {
+    e = first_above(t.inc_s, E, s_lo / NTL);
+    nt = s_lo % NTL;
+  } else {
+    const uint32_t h = (uint32_t)(tt - s_hi), slot = h / NTL;
+    e = first_above(t.inc_h, E, slot);
+    const uint32_t c = t.inc_h[e] - (e ? t.inc_h[e - 1] : 0u), mbase = t.inc_h[e] - c;
+    const uint32_t local = h - mbase * NTL;
+    const uint32_t mg = local / (GROUP_M * NTL);
+    const uint32_t gsize = min((uint32_t)GROUP_M, c - mg * GROUP_M);
+    const uint32_t r = local - mg * GROUP_M * NTL;
+    mtile = mg * GROUP_M + r % gsize;
+    nt = r / gsize;
+  }
+  const uint32_t lo = t.off[e], hi = t.off[e + 1];
+  expert = e;
+  if (hi > p.m || lo > hi) {
+    bad |= kErrCode;
+    row0 = 0;
+    rows = 0;
+    return true;
+  }
+  row0 = lo + mtile * BM;
+  rows = min((uint32_t)BM, hi - row0);
+  return true;
+}
+
+template <int OP, int SCALE, int OUT, bool PERSIST>
 __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // Stage s at smem + s * STAGE: A tile, W tile, A-row scales, W scales.
   __shared__ __align__(16) uint8_t smem[STAGES * STAGE + DUMMY_BYTES];
@@ -287,31 +405,45 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 
   // the masked bit is not changed while this kernel runs: one value for every thread
   if (p.skip_if && (__hip_atomic_load(p.skip_if, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & p.skip_bit)) return;
-  uint32_t expert = 0, row0, rows, nt;
-  if (p.dense_m_tiles) {
-    if (!dense_tile(p, expert, row0, rows, nt)) return;
-  } else if (!moe_tile(p, expert, row0, rows, nt)) {
-    return;
-  }
-  expert = __builtin_amdgcn_readfirstlane(expert);
-  row0 = __builtin_amdgcn_readfirstlane(row0);
-  rows = __builtin_amdgcn_readfirstlane(rows);
-  nt = __builtin_amdgcn_readfirstlane(nt);
 
   // a K step is 128 bytes of a row: 128 e4m3 or 64 bf16 values
   constexpr bool kBf = OP == kOpBf16;
   const uint32_t K = p.k, RB = kBf ? 2 * K : K, KB = RB / 128;
   uint32_t bad = 0;
 
+  [[maybe_unused]] MoeTable tab{};
+  if constexpr (PERSIST) {
+    __shared__ uint32_t s_off[kTableExperts + 1], s_inc_h[kTableExperts], s_inc_s[kTableExperts];
+    tab = MoeTable{s_off, s_inc_h, s_inc_s};
+    if (!p.dense_m_tiles) moe_table_build(p, tab);
+  }
+  // tile vb of the block sequence: expert (problem), first row, rows, N tile
+  auto find_tile = [&](uint32_t vb, uint32_t& e, uint32_t& r0, uint32_t& rs, uint32_t& t) -> bool {
+    bool ok;
+    if (p.dense_m_tiles) ok = dense_tile(p, vb, e, r0, rs, t);
+    else if constexpr (PERSIST) ok = moe_table_tile(p, tab, vb, e, r0, rs, t, bad);
+    else ok = moe_tile(p, vb, e, r0, rs, t);
+    e = __builtin_amdgcn_readfirstlane(e);
+    r0 = __builtin_amdgcn_readfirstlane(r0);
+    rs = __builtin_amdgcn_readfirstlane(rs);
+    t = __builtin_amdgcn_readfirstlane(t);
+    return ok;
+  };
+  uint32_t vb = blockIdx.x, expert = 0, row0 = 0, rows = 0, nt = 0;
+  if (!find_tile(vb, expert, row0, rows, nt)) return;
+
   // Rows past the tile's end (and rejected gather indices) read A row 0:
   // loads stay unconditional and in bounds, and the output rows they feed
   // are never stored (an output row depends on its own A row only).
-  auto a_source = [&](uint32_t r) -> uint64_t {
-    if (r >= rows) return 0;
-    const uint32_t logical = row0 + r;
-    const uint64_t src = p.dense_m_tiles ? (uint64_t)logical * p.a_row_stride + (uint64_t)expert * p.a_prob_row
-                         : p.a_gather     ? p.a_gather[logical]
-                                          : logical;
+  // (Persistent launches have no gather: the next tile's rows are known
+  // without a global read.)
+  auto a_source = [&](uint32_t r, uint32_t e, uint32_t r0, uint32_t rs) -> uint64_t {
+    if (r >= rs) return 0;
+    const uint32_t logical = r0 + r;
+    uint64_t src;
+    if (p.dense_m_tiles) src = (uint64_t)logical * p.a_row_stride + (uint64_t)e * p.a_prob_row;
+    else if constexpr (PERSIST) src = logical;
+    else src = p.a_gather ? p.a_gather[logical] : logical;
     if (src >= p.a_rows_total) {
       bad |= kErrCode;
       return 0;
@@ -320,29 +452,17 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   };
   // W tile row R: for SwiGLU, wave block R >> 6 holds 32 gate rows (R & 63
   // below 32) and the 32 matching up rows, so each wave owns gate/up pairs
-  auto w_row = [&](uint32_t R) -> uint32_t {
+  auto w_row = [&](uint32_t R, uint32_t t) -> uint32_t {
     if constexpr (kSwi) {
       const uint32_t wb = R >> 6, j = (R & 63) >> 4, rr = R & 15;
-      const uint32_t base = nt * 128 + wb * 32 + (j & 1) * 16 + rr;
+      const uint32_t base = t * 128 + wb * 32 + (j & 1) * 16 + rr;
       return j >= 2 ? p.n / 2 + base : base;
     } else {
-      const uint32_t row = nt * BN + R;
+      const uint32_t row = t * BN + R;
       return row < p.n ? row : p.n - 1;
     }
   };
-  const uint8_t* w_base = p.w + (uint64_t)expert * p.n * RB;
-  // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
-  uint32_t wblk0, wblk1;
-  if constexpr (kSwi) {
-    wblk0 = nt;
-    wblk1 = (p.n / 2 + nt * 128) / 128;
-  } else {
-    wblk0 = min(2 * nt, p.n / 128 - 1);
-    wblk1 = min(2 * nt + 1, p.n / 128 - 1);
-  }
   constexpr uint32_t ESZ = SCALE == kScaleUe8m0 ? 1 : 4;
-  const uint64_t ws_off[2] = {((uint64_t)expert * (p.n / 128) + wblk0) * KB,
-                              ((uint64_t)expert * (p.n / 128) + wblk1) * KB};
 
   // Operand tiles move global -> LDS by DMA
   // (global_load_lds_dwordx4): an instruction lands lane l's 16 bytes at
@@ -351,19 +471,6 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // of that row (full 128-byte lines per 8 lanes).  Wave w fills A rows
   // [16w, 16w + 16) and W rows [32w, 32w + 32) of a stage.
   const uint32_t lrow = lane >> 3, lslot = lane & 7;
-  // byte offsets from the operand bases (A: a_rows_total rows and W: n rows
-  // per expert stay below 2^32 bytes, which the launcher checks)
-  uint32_t a_off[2], w_off[4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t R = 16 * wv + 8 * i + lrow;
-    a_off[i] = (uint32_t)(a_source(R) * RB) + ((lslot ^ ((R >> 1) & 7u)) << 4);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t R = 32 * wv + 8 * i + lrow;
-    w_off[i] = w_row(R) * RB + ((lslot ^ ((R >> 1) & 7u)) << 4);
-  }
   // Scales (one dword DMA per wave and step, so every compute wave issues
   // seven loads per step): waves 0 and 1 fetch the A-row scales of rows
   // 64w + (l & 3) * 16 + (l >> 2) into word 64w + l of the stage's scale
@@ -372,46 +479,104 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // 2's load into the scratch word.  UE8M0 bytes come in their aligned
   // dword and are picked out by byte offset.  bf16 operands have no scales
   // (six loads per step).
-  const uint8_t* s_src = nullptr;
-  uint32_t s_lds = 0;
-  if constexpr (!kBf) {
-    if (wv < 2) {
-      const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2));
-      s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB * ESZ;
-      s_lds = A_BYTES + W_BYTES + 256 * wv;
+  struct Ops {
+    uint32_t a_off[2], w_off[4];  // byte offsets from the operand bases
+    const uint8_t* w_base;        // the expert's (problem's) W
+    const uint8_t* s_src;         // this lane's scale source at k step 0
+    uint64_t ws_off[2];           // the tile's two W scale blocks (entries)
+  };
+  // A: a_rows_total rows and W: n rows per expert stay below 2^32 bytes,
+  // which the launcher checks
+  auto make_ops = [&](uint32_t e, uint32_t r0, uint32_t rs, uint32_t t, Ops& o) __attribute__((always_inline)) {
+    o.w_base = p.w + (uint64_t)e * p.n * RB;
+    // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
+    uint32_t wblk0, wblk1;
+    if constexpr (kSwi) {
+      wblk0 = t;
+      wblk1 = (p.n / 2 + t * 128) / 128;
     } else {
-      s_src = static_cast<const uint8_t*>(p.w_scale) + ws_off[lane & 1] * ESZ;
-      s_lds = A_BYTES + W_BYTES + SA_BYTES;
+      wblk0 = min(2 * t, p.n / 128 - 1);
+      wblk1 = min(2 * t + 1, p.n / 128 - 1);
     }
-  }
+    o.ws_off[0] = ((uint64_t)e * (p.n / 128) + wblk0) * KB;
+    o.ws_off[1] = ((uint64_t)e * (p.n / 128) + wblk1) * KB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t R = 16 * wv + 8 * i + lrow;
+      o.a_off[i] = (uint32_t)(a_source(R, e, r0, rs) * RB) + ((lslot ^ ((R >> 1) & 7u)) << 4);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t R = 32 * wv + 8 * i + lrow;
+      o.w_off[i] = w_row(R, t) * RB + ((lslot ^ ((R >> 1) & 7u)) << 4);
+    }
+    o.s_src = nullptr;
+    if constexpr (!kBf) {
+      if (wv < 2) {
+        const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2), e, r0, rs);
+        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB * ESZ;
+      } else {
+        o.s_src = static_cast<const uint8_t*>(p.w_scale) + ((lane & 1) ? o.ws_off[1] : o.ws_off[0]) * ESZ;
+      }
+    }
+  };
+  uint32_t s_lds = 0;
+  if constexpr (!kBf) s_lds = wv < 2 ? A_BYTES + W_BYTES + 256 * wv : A_BYTES + W_BYTES + SA_BYTES;
   s_lds = __builtin_amdgcn_readfirstlane(s_lds);
   const bool s_scratch = wv > 2;
   const uint32_t a_lds = __builtin_amdgcn_readfirstlane(wv * 2048), w_lds = __builtin_amdgcn_readfirstlane(A_BYTES + wv * 4096);
-  auto issue = [&](uint32_t stage, uint32_t kb) __attribute__((always_inline)) {
+  auto issue = [&](uint32_t stage, uint32_t kb, const Ops& o) __attribute__((always_inline)) {
     const uint32_t base = lds0 + stage * STAGE;
     const uint8_t* ab = uniform_ptr(p.a + (uint64_t)kb * 128);
-    const uint8_t* wb = uniform_ptr(w_base + (uint64_t)kb * 128);
+    const uint8_t* wb = uniform_ptr(o.w_base + (uint64_t)kb * 128);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(ab, a_off[i], base + a_lds + i * 1024);
+    for (int i = 0; i < 2; ++i) dma16(ab, o.a_off[i], base + a_lds + i * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(wb, w_off[i], base + w_lds + i * 1024);
+    for (int i = 0; i < 4; ++i) dma16(wb, o.w_off[i], base + w_lds + i * 1024);
     // scales: a per-lane pointer (UE8M0 bytes come in their aligned dword)
     if constexpr (!kBf) {
-      uintptr_t sp = reinterpret_cast<uintptr_t>(s_src) + (uint64_t)kb * ESZ;
+      uintptr_t sp = reinterpret_cast<uintptr_t>(o.s_src) + (uint64_t)kb * ESZ;
       if constexpr (ESZ == 1) sp &= ~uintptr_t(3);
       dma4v(reinterpret_cast<const void*>(sp), s_scratch ? lds0 + STAGES * STAGE : base + s_lds);
     }
   };
 
+  Ops cur;
+  make_ops(expert, row0, rows, nt, cur);
+  const uint32_t last = KB - 1;
+  issue(0, 0, cur);
+  issue(1, min(1u, last), cur);
+  // Persistent blocks: the epilogue's kStoreOps stores of one tile follow
+  // the next tile's first two steps' loads, so those two steps wait with
+  // vmcnt(loads per step + kStoreOps); the first tile gets as many loads
+  // (into the scratch bytes) in place of stores.
+  if constexpr (PERSIST) {
+#pragma unroll
+    for (uint32_t i = 0; i < kStoreOps; ++i) dma4(p.w, lane * 4u, lds0 + STAGES * STAGE);
+  }
+  uint32_t rot = 0;  // stage of the tile's step 0 (persistent blocks)
+
+  for (;;) {
+  // ---- one tile: the next one's operands (persistent blocks) are read
+  // in this tile's last two steps
+  uint32_t e2 = expert, r2 = row0, rs2 = rows, t2 = nt;
+  bool has_next = false;
+  if constexpr (PERSIST) {
+    has_next = __builtin_amdgcn_readfirstlane(find_tile(vb + gridDim.x, e2, r2, rs2, t2) ? 1u : 0u) != 0;
+    if (!has_next) e2 = expert, r2 = row0, rs2 = rows, t2 = nt;
+  }
+  Ops nxt;
   // byte offsets of this lane's UE8M0 A scales (rows wm*64 + r*16 + lr) and
   // of the W block scales within their aligned dwords, at k step 0
   uint32_t a_byte0[4] = {0, 0, 0, 0}, w_byte0[2] = {0, 0};
   if constexpr (ESZ == 1) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      a_byte0[r] = (uint32_t)((reinterpret_cast<uintptr_t>(p.a_scale) + a_source(wm * 64 + r * 16 + lr) * KB) & 3u);
-    w_byte0[0] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + ws_off[0]) & 3u);
-    w_byte0[1] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + ws_off[1]) & 3u);
+      a_byte0[r] = (uint32_t)((reinterpret_cast<uintptr_t>(p.a_scale) +
+                               a_source(wm * 64 + r * 16 + lr, expert, row0, rows) * KB) &
+                              3u);
+    w_byte0[0] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + cur.ws_off[0]) & 3u);
+    w_byte0[1] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + cur.ws_off[1]) & 3u);
   }
   // live 16-row blocks of this wave's 64-row half
   const uint32_t rb_live =
@@ -423,8 +588,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](auto STG, uint32_t kb, auto FULL) __attribute__((always_inline)) {
-    constexpr uint32_t stage = decltype(STG)::value;
+  auto compute = [&](uint32_t stage, uint32_t kb, auto FULL) __attribute__((always_inline)) {
     constexpr bool kFull = decltype(FULL)::value;
     if (!kFull && rb_live == 0) return;
     const uint8_t* sA = smem + stage * STAGE;
@@ -559,48 +723,85 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // are in flight (step j + 1's: step j's tiles and scales have landed),
   // barrier (every wave's DMA for step j is visible and step j - 1's compute
   // is done, so its stage may be refilled), issue, compute step j.  Loads
-  // past the last step re-read it (into a stage that is never used).  The
-  // loads are issued by inline asm, so the compiler adds no waits of its
-  // own.  (A per-step L2 prefetch of a later step, one 4-byte load per lane
-  // and line, measured slower: the tiles already hit L2 about nine times in
-  // ten, and the extra load lengthens every wait.)
-  const uint32_t last = KB - 1;
-  issue(0, 0);
-  issue(1, min(1u, last));
-  // Six steps per trip (stages fixed at compile time, so every LDS address
-  // is a per-lane base plus an immediate); whole tiles (all 128 A rows) run
-  // a compute without per-block guards.
+  // past the last step re-read it (into a stage that is never used), or, in
+  // a persistent block with a next tile, fetch that tile's first two steps.
+  // The loads are issued by inline asm, so the compiler adds no waits of its
+  // own; which tile a load reads is selected, not branched on, so that the
+  // step stays one straight line.  (A per-step L2 prefetch of a later step,
+  // one 4-byte load per lane and line, measured slower: the tiles already
+  // hit L2 about nine times in ten, and the extra load lengthens every wait.)
+  constexpr int kWaitStep = kBf ? kWaitVm6 : kWaitVm7;
+  constexpr int kWaitFirstEnc = vmcnt_enc((kBf ? 6 : 7) + (int)kStoreOps);
+  // stages of steps kb + 0, 1, 2 (kb a multiple of 3)
+  const uint32_t st0 = rot, st1 = rot == 2 ? 0u : rot + 1, st2 = rot == 0 ? 2u : rot - 1;
+  // persistent blocks run steps 0 .. KB - 3 in the unrolled loop and the
+  // last two, which load the next tile's first two, after it (KB >= 4)
+  const uint32_t KBm = PERSIST ? KB - 2 : KB;
   auto run = [&](auto FULL) __attribute__((always_inline)) {
-#define PIH_MOE_STEP(J, TAIL)                                                                        \
+    auto steps = [&]() __attribute__((always_inline)) {
+#define PIH_MOE_STEP(J, TAIL, WAIT)                                                                  \
   {                                                                                                  \
     const uint32_t j = kb + (J);                                                                     \
-    if ((TAIL) && j >= KB) return;                                                                   \
-    __builtin_amdgcn_s_waitcnt(kBf ? kWaitVm6 : kWaitVm7);                                           \
+    if ((TAIL) && j >= KBm) return;                                                                  \
+    __builtin_amdgcn_s_waitcnt(WAIT);                                                                \
     __builtin_amdgcn_s_barrier();                                                                    \
-    issue(((J) + 2) % 3, min(j + 2, last));                                                          \
-    compute(std::integral_constant<uint32_t, (J) % 3>{}, j, FULL);                                   \
+    if constexpr (PERSIST) {                                                                         \
+      issue((J) % 3 == 0 ? st2 : (J) % 3 == 1 ? st0 : st1, j + 2, cur);                              \
+      compute((J) % 3 == 0 ? st0 : (J) % 3 == 1 ? st1 : st2, j, FULL);                               \
+    } else {                                                                                         \
+      issue(((J) + 2) % 3, min(j + 2, last), cur);                                                   \
+      compute((J) % 3, j, FULL);                                                                     \
+    }                                                                                                \
   }
-    uint32_t kb = 0;
-    for (; kb + 6 < KB; kb += 6) {
-      PIH_MOE_STEP(0, false)
-      PIH_MOE_STEP(1, false)
-      PIH_MOE_STEP(2, false)
-      PIH_MOE_STEP(3, false)
-      PIH_MOE_STEP(4, false)
-      PIH_MOE_STEP(5, false)
-    }
-    PIH_MOE_STEP(0, true)
-    PIH_MOE_STEP(1, true)
-    PIH_MOE_STEP(2, true)
-    PIH_MOE_STEP(3, true)
-    PIH_MOE_STEP(4, true)
-    PIH_MOE_STEP(5, true)
+      uint32_t kb = 0;
+      if constexpr (PERSIST) {
+        // the tile's first two steps wait past the previous tile's stores
+        PIH_MOE_STEP(0, true, kWaitFirstEnc)
+        PIH_MOE_STEP(1, true, kWaitFirstEnc)
+        PIH_MOE_STEP(2, true, kWaitStep)
+        PIH_MOE_STEP(3, true, kWaitStep)
+        PIH_MOE_STEP(4, true, kWaitStep)
+        PIH_MOE_STEP(5, true, kWaitStep)
+        kb = 6;
+      }
+      for (; kb + 6 < KBm; kb += 6) {
+        PIH_MOE_STEP(0, false, kWaitStep)
+        PIH_MOE_STEP(1, false, kWaitStep)
+        PIH_MOE_STEP(2, false, kWaitStep)
+        PIH_MOE_STEP(3, false, kWaitStep)
+        PIH_MOE_STEP(4, false, kWaitStep)
+        PIH_MOE_STEP(5, false, kWaitStep)
+      }
+      PIH_MOE_STEP(0, true, kWaitStep)
+      PIH_MOE_STEP(1, true, kWaitStep)
+      PIH_MOE_STEP(2, true, kWaitStep)
+      PIH_MOE_STEP(3, true, kWaitStep)
+      PIH_MOE_STEP(4, true, kWaitStep)
+      PIH_MOE_STEP(5, true, kWaitStep)
 #undef PIH_MOE_STEP
+    };
+    steps();
+    if constexpr (PERSIST) {
+      // the last two steps load the next tile's steps 0 and 1 (or re-read
+      // this tile's last step when there is none)
+      make_ops(e2, r2, rs2, t2, nxt);
+#pragma unroll
+      for (uint32_t f = 0; f < 2; ++f) {
+        const uint32_t j = KB - 2 + f;
+        const uint32_t sj = (rot + j) % 3;
+        __builtin_amdgcn_s_waitcnt(kWaitStep);
+        __builtin_amdgcn_s_barrier();
+        issue(sj == 0 ? 2u : sj - 1, has_next ? f : last, nxt);
+        compute(sj, j, FULL);
+      }
+    }
   };
   if (rb_live == 4) run(std::true_type{});
   else run(std::false_type{});
-  // no DMA may still target this block's LDS when its waves end
-  __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  // no DMA may still target this block's LDS when its waves end (a
+  // persistent block's loads of its next tile stay in flight)
+  if (!PERSIST || !has_next) __builtin_amdgcn_s_waitcnt(kWaitVm0);
+
 
   // ---- epilogue: lane holds out[row wm*64 + r*16 + lr][4*lg + i] of block nb
   // SwiGLU tiles: bf16(SiLU(g) x u x w) of a gate value g = bf16(ga) clamped
@@ -724,6 +925,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // whole, with no per-row or per-column test at all on a full tile;
   // otherwise the per-element path below.
   bool stored = false;
+  [[maybe_unused]] bool slow = false;  // wave-uniform
   if constexpr (OUT == kOutBf16 || OUT == kOutF32) {
     bool nonfin = false;
 #pragma unroll
@@ -738,9 +940,37 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       }
     if (nonfin) bad |= kErrNonFinite;
     const bool keep_finite = nonfin && p.err_nonfinite && !p.write_nonfinite;
-    // one decision for the block: every wave is past its main loop and its
-    // DMAs (vmcnt(0) above), so the stages are free for the staged tile
-    if (p.stage_out && !__syncthreads_or(keep_finite)) {
+    if constexpr (PERSIST) {
+      // Persistent blocks: exactly kStoreOps buffer stores per lane (rows
+      // past the tile's end fall outside the buffer's range and columns past
+      // n get an offset outside it; the hardware drops both), so the next
+      // tile's first waits count them; a wave that must skip non-finite
+      // elements stores per element below and then drains its stores.
+      slow = __builtin_amdgcn_ballot_w64(keep_finite) != 0;
+      if (!slow) {
+        stored = true;
+        constexpr uint32_t OSZ = OUT == kOutF32 ? 4 : 2;
+        const uint32_t stride_b = p.out_row_stride * OSZ;
+        uint8_t* tile_out = static_cast<uint8_t*>(p.out) +
+                            ((uint64_t)row0 * p.out_row_stride + (uint64_t)expert * p.out_prob_col + nt * BN) * OSZ;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(tile_out, 0, rows * stride_b, 0x00020000);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) {
+            const uint32_t R = wm * 64 + r * 16 + lr, C = wn * 64 + nb * 16 + 4 * lg;
+            const uint32_t off = nt * BN + C < p.n ? R * stride_b + C * OSZ : 0x80000000u;
+            const v4f v = acc[nb][r];
+            if constexpr (OUT == kOutF32)
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u, v), rsrc, off, 0, 0);
+            else
+              __builtin_amdgcn_raw_buffer_store_b64(v2u{f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])}, rsrc,
+                                                    off, 0, 0);
+          }
+      }
+    } else if (p.stage_out && !__syncthreads_or(keep_finite)) {
+      // one decision for the block: every wave is past its main loop and its
+      // DMAs (vmcnt(0) above), so the stages are free for the staged tile
       stored = true;
       // the tile staged in LDS (rows padded by 32 bytes: the 16 rows of a
       // fragment start 8 banks apart), then whole rows stored with 16 bytes
@@ -863,6 +1093,20 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       }
     }
   }
+  if constexpr (!PERSIST) {
+    break;
+  } else {
+    if (slow) __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    if (!has_next) break;
+    vb += gridDim.x;
+    expert = e2;
+    row0 = r2;
+    rows = rs2;
+    nt = t2;
+    cur = nxt;
+    rot = (rot + KB) % 3;
+  }
+  }  // tiles
   if (bad) {
     const uint32_t bits = ((bad & kErrCode) ? p.err_code : 0u) | ((bad & kErrScale) ? p.err_scale : 0u) |
                           ((bad & kErrNonFinite) ? p.err_nonfinite : 0u);
@@ -871,19 +1115,52 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 }
 
 template <int OP, int SCALE>
-void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out) {
+void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out, bool persist) {
   if constexpr (OP == kOpFp8) {
     if (out == kOutSwiGlu) {
-      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGlu>), dim3(grid), dim3(NTH), 0, s, mp);
+      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGlu, false>), dim3(grid), dim3(NTH), 0, s, mp);
       return;
     }
     if (out == kOutSwiGluFp8) {
-      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGluFp8>), dim3(grid), dim3(NTH), 0, s, mp);
+      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGluFp8, false>), dim3(grid), dim3(NTH), 0, s, mp);
       return;
     }
   }
-  if (out == kOutF32) hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutF32>), dim3(grid), dim3(NTH), 0, s, mp);
-  else hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutBf16>), dim3(grid), dim3(NTH), 0, s, mp);
+  if (persist) {
+    if (out == kOutF32)
+      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutF32, true>), dim3(grid), dim3(NTH), 0, s, mp);
+    else hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutBf16, true>), dim3(grid), dim3(NTH), 0, s, mp);
+    return;
+  }
+  if (out == kOutF32)
+    hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutF32, false>), dim3(grid), dim3(NTH), 0, s, mp);
+  else hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutBf16, false>), dim3(grid), dim3(NTH), 0, s, mp);
+}
+
+// Blocks of a persistent launch: one per CU, a multiple of 8 (the tile
+// sequence is split into 8 XCD ranges by blockIdx % 8); 0 if unknown.
+uint32_t PersistentBlocks() {
+  static uint32_t cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) return 0;
+    cached[dev] = (uint32_t)cus / 8 * 8;
+  }
+  return cached[dev];
+}
+
+// Plain (bf16 / fp32) outputs without an A gather run persistent: a block
+// walks its XCD's tiles, the next tile's first loads overlap this tile's
+// epilogue and its stores drain under the next tile's first steps.  The
+// buffer stores need the tile's output bytes below 2^31; MoE segments need
+// the LDS table (at most kTableExperts experts); the last two K steps of a
+// tile load the next tile's first two, so a tile has at least four.
+bool Persistent(OutKind out, bool gather, bool dense, uint32_t problems, uint64_t row_stride, uint32_t k_steps) {
+  const uint64_t osz = out == kOutF32 ? 4 : 2;
+  return (out == kOutBf16 || out == kOutF32) && !gather && (dense || problems <= kTableExperts) && k_steps >= 4 &&
+         (uint64_t)BM * row_stride * osz < 0x80000000ull && PersistentBlocks() > 0;
 }
 
 // Output rows and problem column offsets on 16-byte boundaries: the kernel
@@ -929,11 +1206,13 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
   // the tile loads address A and one expert's W by 32-bit byte offsets
   if ((uint64_t)a.a_rows_total * a.k > 0xffffffffull || (uint64_t)a.n * a.k > 0xffffffffull)
     return Invalid("fp8_moe_gemm_operand_too_large");
-  const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  const bool persist = Persistent(a.out_kind, a.a_gather != nullptr, false, a.problems, mp.out_row_stride, a.k / 128);
+  uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  if (persist) grid = std::min(grid, PersistentBlocks());
   St s = RequireCleanLastError();
   if (!s.ok()) return s;
-  if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind);
-  else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind);
+  if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind, persist);
+  else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
   return AfterLaunch("fp8_moe_gemm_launch_failed");
 }
 
@@ -977,12 +1256,14 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.skip_bit = a.skip_bit;
   const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles * a.problems;
   if (total > 0x7fffffffull - 8) return Invalid("big_tile_gemm_grid_too_large");
-  const uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  const bool persist = Persistent(a.out_kind, false, true, a.problems, mp.out_row_stride, (uint32_t)(rb / 128));
+  uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  if (persist) grid = std::min(grid, PersistentBlocks());
   St s = RequireCleanLastError();
   if (!s.ok()) return s;
-  if (bf) launch_out<kOpBf16, kScaleF32>(mp, grid, a.stream, a.out_kind);
-  else if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind);
-  else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind);
+  if (bf) launch_out<kOpBf16, kScaleF32>(mp, grid, a.stream, a.out_kind, persist);
+  else if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind, persist);
+  else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
   return AfterLaunch("big_tile_gemm_launch_failed");
 }
 

@@ -160,3 +160,38 @@ def test_bf16_gemm_big_tile(eng, m, n, k, out_type):
     rows = np.unique(np.linspace(0, m - 1, 24).astype(np.int64))
     ref = oracle.bf16_gemm(np.ascontiguousarray(x[rows]), w)
     assert_close(got[rows], ref, f"big-tile bf16 {m}x{n}x{k}")
+
+
+def test_big_tile_nonfinite_results_skipped(eng):
+    """Sums that overflow (UE8M0 weight scale 2^127 on one 128-row block)
+    raise bit 4 and leave their elements unwritten, as the reference's
+    fp8_gemm_kernel skips them (deepseek_fp8_gemm.cu:67-70); the other
+    columns hold the oracle's values.  M = 2048 runs the persistent big-tile
+    kernel, whose waves with such an element store per element."""
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    m, n, k = 2048, 4096, 1024
+    a = np.zeros((m, k), np.uint8)
+    a[:, :128] = 0x7E  # 448
+    w = np.zeros((n, k), np.uint8)
+    w[:, :128] = 0x7E
+    sa = np.full((m, k // 128), 127, np.uint8)
+    sw = np.full((n // 128, k // 128), 127, np.uint8)
+    sw[3, 0] = 254  # W rows 384..511: 448 * 448 * 128 * 2^127 overflows
+    sentinel = 0x7FC1
+    out = torch.full((m, n), sentinel, dtype=torch.int16, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ad, sad, wd, swd = to_dev(a), to_dev(sa), to_dev(w), to_dev(sw)
+    r = abi.request(abi.DS["fp8_gemm"], activation_e4m3=ptr(ad), activation_scale_bits=ptr(sad),
+                    weight_e4m3=ptr(wd), weight_scale_bits=ptr(swd), output=ptr(out), error_flag=ptr(flag),
+                    stream=stream_handle(), m=m, n=n, k=k, output_type=1)
+    st = abi.deepseek_pack().call("launch_fp8_gemm", r)
+    assert st.code == abi.OK, st
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 4
+    got = to_host(out).view(np.uint16)
+    assert np.all(got[:, 384:512] == sentinel)
+    want = oracle.f32_to_bf16_bits(np.float32(448.0 * 448 * 128))
+    assert np.all(got[:, :384] == want) and np.all(got[:, 512:] == want)
