@@ -798,7 +798,7 @@ def main() -> int:
         "mfma_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
         "layer_hbm_gbs": round(bytes_layer / (ms * 1e-3) / 1e9, 1),
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
-        "roofline": {"kernel": "fp8_moe_gemm_kernel<1, 4> (MoE gate/up, SwiGLU + e4m3 requant epilogue)",
+        "roofline": {"kernel": "fp8_moe_gemm_kernel<0, 1, 4, false> (MoE gate/up, SwiGLU + e4m3 requant epilogue)",
                      "bound": "hbm",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
