@@ -126,6 +126,7 @@ struct MoeParams {
   uint32_t skip_bit;
   uint64_t out_row_stride;
   uint32_t n_tiles;
+  uint32_t vb_end;  // blocks of the one-block-per-tile grid; persistent blocks walk no further
   float limit;
   uint32_t err_code, err_scale, err_nonfinite;
 };
@@ -361,7 +362,7 @@ __device__ bool moe_table_tile(const MoeParams& p, const MoeTable& t, uint32_t v
   const uint32_t per = (uint32_t)((T + 7) / 8);
   const uint32_t xcd = vb & 7, jj = vb >> 3;
   const uint64_t tt = (uint64_t)xcd * per + jj;
-  if (jj >= per || tt >= T) return false;
+  if (jj >= per || tt >= T || vb >= p.vb_end) return false;
   const uint32_t s_lo = (uint32_t)(tt * Ls / T), s_hi = (uint32_t)((tt + 1) * Ls / T);
   uint32_t e, mtile = 0;
   if (s_hi > s_lo) {
@@ -370,23 +371,31 @@ __device__ bool moe_table_tile(const MoeParams& p, const MoeTable& t, uint32_t v
   } else {
     const uint32_t h = (uint32_t)(tt - s_hi), slot = h / NTL;
     e = first_above(t.inc_h, E, slot);
-    const uint32_t c = t.inc_h[e] - (e ? t.inc_h[e - 1] : 0u), mbase = t.inc_h[e] - c;
-    const uint32_t local = h - mbase * NTL;
-    const uint32_t mg = local / (GROUP_M * NTL);
-    const uint32_t gsize = min((uint32_t)GROUP_M, c - mg * GROUP_M);
-    const uint32_t r = local - mg * GROUP_M * NTL;
-    mtile = mg * GROUP_M + r % gsize;
-    nt = r / gsize;
+    if (e < E) {
+      const uint32_t c = t.inc_h[e] - (e ? t.inc_h[e - 1] : 0u), mbase = t.inc_h[e] - c;
+      const uint32_t local = h - mbase * NTL;
+      const uint32_t mg = local / (GROUP_M * NTL);
+      const uint32_t gsize = max(1u, min((uint32_t)GROUP_M, c - mg * GROUP_M));
+      const uint32_t r = local - mg * GROUP_M * NTL;
+      mtile = mg * GROUP_M + r % gsize;
+      nt = r / gsize;
+    }
   }
-  const uint32_t lo = t.off[e], hi = t.off[e + 1];
-  expert = e;
-  if (hi > p.m || lo > hi) {
+  // Offsets that are not non-decreasing within [0, m] can make the counts
+  // wrap and the table non-monotone: a tile whose rows do not lie inside
+  // one valid segment raises the code bit, has no rows and reads expert 0.
+  const uint32_t lo = e < E ? t.off[e] : 0u, hi = e < E ? t.off[e + 1] : 0u;
+  const uint64_t r0 = lo + (uint64_t)mtile * BM;
+  if (e >= E || hi > p.m || lo > hi || r0 >= hi || nt >= NTL) {
     bad |= kErrCode;
+    expert = 0;
     row0 = 0;
     rows = 0;
+    nt = 0;
     return true;
   }
-  row0 = lo + mtile * BM;
+  expert = e;
+  row0 = (uint32_t)r0;
   rows = min((uint32_t)BM, hi - row0);
   return true;
 }
@@ -1208,6 +1217,7 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
     return Invalid("fp8_moe_gemm_operand_too_large");
   const bool persist = Persistent(a.out_kind, a.a_gather != nullptr, false, a.problems, mp.out_row_stride, a.k / 128);
   uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  mp.vb_end = grid;
   if (persist) grid = std::min(grid, PersistentBlocks());
   St s = RequireCleanLastError();
   if (!s.ok()) return s;
@@ -1258,6 +1268,7 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   if (total > 0x7fffffffull - 8) return Invalid("big_tile_gemm_grid_too_large");
   const bool persist = Persistent(a.out_kind, false, true, a.problems, mp.out_row_stride, (uint32_t)(rb / 128));
   uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  mp.vb_end = grid;
   if (persist) grid = std::min(grid, PersistentBlocks());
   St s = RequireCleanLastError();
   if (!s.ok()) return s;

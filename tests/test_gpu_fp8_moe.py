@@ -324,3 +324,66 @@ def test_moe_fp8_layer_full_shape_cold_experts(eng):
         a, sa, bw, sb = host[e]
         ref = oracle.expert_fp8(np.ascontiguousarray(x[rt_ref[b:en]]), rw_ref[b:en], hidden, inter, a, sa, bw, sb)
         assert_close(oracle.bf16_bits_to_f32(y[b:en]), oracle.bf16_bits_to_f32(ref), f"expert {e} rows")
+
+
+def test_moe_gemm_plain_output_forms_and_bad_segment(eng):
+    """The plain-output MoE GEMM without a row gather (the down projection's
+    form, one block per CU walking its XCD's tiles) and with an identity
+    gather (one block per tile) give the same bits on the same segments:
+    empty experts, a one-row expert, 8 x 16 tiles more than the GPU has CUs.
+    Sampled rows of every segment match the oracle.  Offsets whose segment
+    ends past the row capacity (its tile count runs to 2^25) raise bit 1,
+    the rows outside the valid segment stay unwritten and the walk ends at
+    the one-block-per-tile grid; a valid call afterwards gives the first
+    result again."""
+    import torch
+
+    from pih_amd import linear
+
+    experts, n, k, cap = 8, 4096, 1024, 4000
+    counts = np.array([0, 900, 1, 0, 1300, 129, 700, 960], np.int64)
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint32)
+    assert off[-1] <= cap
+    a = _codes(synth.config_seed(4, 9500), (cap, k))
+    w = _codes(synth.config_seed(4, 9501), (experts, n, k))
+    rng = np.random.default_rng(9502)
+    sa = (rng.uniform(0.5, 2.0, (cap, k // 128)) / 448).astype(np.float32)
+    sw = (rng.uniform(0.5, 2.0, (experts, n // 128, k // 128)) / 448).astype(np.float32)
+    ad, sad, wd, swd = to_dev(a), to_dev(sa), to_dev(w), to_dev(sw)
+    ident = to_dev(np.arange(cap, dtype=np.uint32))
+    sentinel = 0x7FC1
+
+    def call(offsets, gather):
+        out = torch.full((cap + 64, n), sentinel, dtype=torch.int16, device="cuda")
+        view = out[:cap].view(torch.bfloat16)
+        _, flag = linear.moe_fp8_gemm(ad, sad, ident if gather else None, wd, swd, to_dev(offsets), cap,
+                                      abi.SCALE_F32, abi.OUTPUT_BF16, out=view)
+        _sync()
+        return to_host(out).view(np.uint16), _flag(flag)
+
+    walk, f_walk = call(off, False)
+    tiled, f_tiled = call(off, True)
+    assert f_walk == 0 and f_tiled == 0
+    np.testing.assert_array_equal(walk, tiled)
+    assert np.all(walk[off[-1]:] == sentinel)
+    for e in range(experts):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi == lo:
+            continue
+        rows = np.unique(np.array([lo, lo + 1, (lo + hi) // 2, hi - 2, hi - 1]).clip(lo, hi - 1))
+        ref = oracle.fp8_gemm_f32(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows]), w[e], sw[e])
+        assert_close(oracle.bf16_bits_to_f32(walk[rows]), ref, f"expert {e} rows {lo}..{hi}")
+
+    bad = off.copy()  # expert 1 keeps rows 0..900, expert 2 runs from 900 to 0xFFFF0000
+    bad[3:] = 0xFFFF0000
+    bad[-1] = cap
+    for gather in (False, True):
+        got, flag = call(bad, gather)
+        assert flag & 1, (gather, flag)
+        assert np.all(got[int(off[2]):] == sentinel), gather
+        written = got[: int(off[2])]
+        assert np.all((written == sentinel) | (written == walk[: int(off[2])])), gather
+
+    again, f_again = call(off, False)
+    assert f_again == 0
+    np.testing.assert_array_equal(again, walk)
