@@ -53,6 +53,8 @@
 // holds 64 gate rows and the 64 matching up rows, so every lane owns a
 // gate/up pair and writes mid = bf16(silu(g') * u' * route_weight) with
 // g, u the bf16-rounded GEMM results (clamped when limit > 0).
+#include <mutex>
+
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -647,6 +649,62 @@ St prepare(GemmParams& gp, uint32_t& grid, uint32_t m, uint32_t n, uint32_t k, u
   return RequireCleanLastError();
 }
 
+// The tiled and the weight-streaming experts of one MXFP4 MoE launch are
+// independent (disjoint output rows; the error word is only OR-ed), so the
+// tiled kernel (MFMA work) runs on a per-device auxiliary stream forked from
+// the caller's and the streaming kernel (HBM work) on the caller's, joined
+// before the entry returns.  The auxiliary stream has the default priority.
+// A device's record + wait pairs are serialized, so concurrent callers cannot
+// interleave them; a capturing stream keeps both launches on itself.
+struct ForkStreams {
+  std::mutex mu;
+  hipStream_t aux = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool broken = false;
+};
+ForkStreams g_fork[64];
+
+// The current device's fork streams, locked, with the auxiliary stream
+// already waiting for the work enqueued on `s`; null (nothing locked) when
+// `s` is capturing or the streams cannot be made.
+ForkStreams* ForkBegin(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  ForkStreams& f = g_fork[dev];
+  f.mu.lock();
+  if (!f.aux && !f.broken) {
+    if (hipStreamCreateWithFlags(&f.aux, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess) {
+      f.broken = true;
+      (void)hipGetLastError();
+    }
+  }
+  if (f.broken || hipEventRecord(f.fork, s) != hipSuccess || hipStreamWaitEvent(f.aux, f.fork, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    f.mu.unlock();
+    return nullptr;
+  }
+  return &f;
+}
+
+// Makes `s` wait for the auxiliary stream's work and unlocks.
+St ForkEnd(ForkStreams* f, hipStream_t s) {
+  St r = Ok();
+  if (hipEventRecord(f->join, f->aux) != hipSuccess || hipStreamWaitEvent(s, f->join, 0) != hipSuccess)
+    r = Internal("fp4_gemm_stream_join_failed");
+  f->mu.unlock();
+  return r;
+}
+
 }  // namespace
 
 St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
@@ -794,9 +852,16 @@ St LaunchFp4Gemm(const Fp4GemmArgs& a) {
   St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, 0, a.moe ? Fp4MoeLightRows(a) : 0);
   if (!s.ok()) return s;
   if (grid) {
-    if (a.act == kActE4m3) dispatch_out<kFp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, !a.moe);
-    else dispatch_out<kBf16Fp4, kScaleUe8m0>(gp, grid, a.stream, a.out_kind, a.moe, false);
+    ForkStreams* f = gp.light_rows ? ForkBegin(a.stream) : nullptr;
+    const hipStream_t hs = f ? f->aux : a.stream;
+    if (a.act == kActE4m3) dispatch_out<kFp4, kScaleUe8m0>(gp, grid, hs, a.out_kind, a.moe, !a.moe);
+    else dispatch_out<kBf16Fp4, kScaleUe8m0>(gp, grid, hs, a.out_kind, a.moe, false);
     s = AfterLaunch("fp4_gemm_launch_failed");
+    if (f) {
+      if (s.ok()) s = LaunchFp4MoeStream(a);
+      const St joined = ForkEnd(f, a.stream);
+      return s.ok() ? joined : s;
+    }
   }
   if (!s.ok() || gp.light_rows == 0) return s;
   return LaunchFp4MoeStream(a);

@@ -404,6 +404,81 @@ def test_moe_mxfp4_gemm_down_bf16_out(eng, act):
     assert_close(oracle.bf16_bits_to_f32(to_host(out)), ref, "mxfp4 moe down")
 
 
+def test_moe_mxfp4_gemm_forked_stream_threads_and_graph(eng):
+    """The tiled experts of an MXFP4 MoE launch run on an auxiliary stream
+    forked from the caller's (the weight-streaming experts on the caller's)
+    and joined before the entry returns.  Two host threads calling at once on
+    two streams, and a captured graph (capture keeps both launches on the
+    capturing stream) replayed three times with eager work between the
+    replays, give the bits of one plain call."""
+    import threading
+
+    import torch
+
+    from pih_amd import linear
+
+    tokens, experts, topk, hidden, inter = 200, 8, 2, 512, 256
+    ids, wts = synth.zipf_router(synth.config_seed(5, 800 + tokens), tokens, experts, topk)
+    x = synth.bf16_normal(synth.config_seed(5, 801), (tokens, hidden))
+    w13, s13 = _mx_moe_weights(experts, 2 * inter, hidden, synth.config_seed(5, 900))
+    off, rt, rw, _ = oracle.route_plan(ids, wts, experts)
+    counts = np.diff(off.astype(np.int64))
+    assert (counts > 64).any() and ((counts > 0) & (counts <= 64)).any()  # both kernels run
+    xq, xs = oracle.fp8_quant_ue8m0(oracle.bf16_bits_to_f32(x))
+    rows = tokens * topk
+    dev = [to_dev(t) for t in (xq, xs, rt, w13, s13, off, rw)]
+
+    def call(out=None, flag=None):
+        return linear.moe_mxfp4_gemm(dev[0], dev[1], dev[2], dev[3], dev[4], dev[5], rows, abi.ACTIVATION_E4M3,
+                                     abi.OUTPUT_SWIGLU_BF16, row_weight=dev[6], out=out, flag=flag)
+
+    ref, flag = call()
+    _sync()
+    assert _flag(flag) == 0
+    n_rows = int(off[-1])
+    want = to_host(ref)[:n_rows]
+
+    results, errors = {}, []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                outs = [call() for _ in range(8)]
+            s.synchronize()
+            results[i] = [(to_host(o)[:n_rows], _flag(f)) for o, f in outs]
+        except Exception as e:  # reported below, on the test's thread
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        for got, f in results[i]:
+            assert f == 0
+            np.testing.assert_array_equal(got, want)
+
+    out = torch.empty_like(ref)
+    gflag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        gflag.zero_()
+        call(out=out, flag=gflag)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        out.fill_(0)
+        _ = call()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert _flag(gflag) == 0
+        np.testing.assert_array_equal(to_host(out)[:n_rows], want)
+
+
 # ---------------------------------------------------------- elementwise
 def test_mxfp4_decode_bit_exact(eng):
     import torch
