@@ -83,6 +83,10 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off), "s"(base)
                : "memory");
 }
+__device__ __forceinline__ void dma16nt(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(lds), "v"(off), "s"(base)
+               : "memory");
+}
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off), "s"(base)
                : "memory");
@@ -297,7 +301,7 @@ struct MoeTable {
   uint32_t* inc_s;  // [E] one-tile experts among 0..e
 };
 
-__device__ void moe_table_build(const MoeParams& p, const MoeTable& t) {
+__device__ __forceinline__ void moe_table_build(const MoeParams& p, const MoeTable& t) {
   __shared__ uint32_t s_wave[2][NTH / 64];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, E = p.experts;
   for (uint32_t e = tid; e <= E; e += NTH) t.off[e] = p.offsets[e];
@@ -534,14 +538,17 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   s_lds = __builtin_amdgcn_readfirstlane(s_lds);
   const bool s_scratch = wv > 2;
   const uint32_t a_lds = __builtin_amdgcn_readfirstlane(wv * 2048), w_lds = __builtin_amdgcn_readfirstlane(A_BYTES + wv * 4096);
-  auto issue = [&](uint32_t stage, uint32_t kb, const Ops& o) __attribute__((always_inline)) {
+  auto issue = [&](uint32_t stage, uint32_t kb, const Ops& o, auto NT) __attribute__((always_inline)) {
     const uint32_t base = lds0 + stage * STAGE;
     const uint8_t* ab = uniform_ptr(p.a + (uint64_t)kb * 128);
     const uint8_t* wb = uniform_ptr(o.w_base + (uint64_t)kb * 128);
 #pragma unroll
     for (int i = 0; i < 2; ++i) dma16(ab, o.a_off[i], base + a_lds + i * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(wb, o.w_off[i], base + w_lds + i * 1024);
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (decltype(NT)::value) dma16nt(wb, o.w_off[i], base + w_lds + i * 1024);
+      else dma16(wb, o.w_off[i], base + w_lds + i * 1024);
+    }
     // scales: a per-lane pointer (UE8M0 bytes come in their aligned dword)
     if constexpr (!kBf) {
       uintptr_t sp = reinterpret_cast<uintptr_t>(o.s_src) + (uint64_t)kb * ESZ;
@@ -553,8 +560,8 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   Ops cur;
   make_ops(expert, row0, rows, nt, cur);
   const uint32_t last = KB - 1;
-  issue(0, 0, cur);
-  issue(1, min(1u, last), cur);
+  issue(0, 0, cur, std::false_type{});
+  issue(1, min(1u, last), cur, std::false_type{});
   // Persistent blocks: the epilogue's kStoreOps stores of one tile follow
   // the next tile's first two steps' loads, so those two steps wait with
   // vmcnt(loads per step + kStoreOps); the first tile gets as many loads
@@ -697,7 +704,9 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       // UE8M0 scales ride in the MFMA's E8M0 operands and the MFMAs chain on
       // the accumulator; a 255 scale raises the scale bit and runs as 0
       // (2^-127), contributing nothing, as the reference skips the block
-      const uint32_t wsh0 = 8 * ((w_byte0[wsel0] + kb) & 3u), wsh1 = 8 * ((w_byte0[wsel1] + kb) & 3u);
+      // (selects, not an index: a runtime index would put the array in scratch)
+      const uint32_t wb0 = wsel0 ? w_byte0[1] : w_byte0[0], wb1 = wsel1 ? w_byte0[1] : w_byte0[0];
+      const uint32_t wsh0 = 8 * ((wb0 + kb) & 3u), wsh1 = 8 * ((wb1 + kb) & 3u);
       uint32_t wsb0 = (sw0 >> wsh0) & 0xffu, wsb1 = (sw1 >> wsh1) & 0xffu;
       if (wsb0 == 0xffu || wsb1 == 0xffu) bad |= kErrScale;
       wsb0 = wsb0 == 0xffu ? 0u : wsb0;
@@ -746,7 +755,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // persistent blocks run steps 0 .. KB - 3 in the unrolled loop and the
   // last two, which load the next tile's first two, after it (KB >= 4)
   const uint32_t KBm = PERSIST ? KB - 2 : KB;
-  auto run = [&](auto FULL) __attribute__((always_inline)) {
+  auto run = [&](auto FULL, auto NT) __attribute__((always_inline)) {
     auto steps = [&]() __attribute__((always_inline)) {
 #define PIH_MOE_STEP(J, TAIL, WAIT)                                                                  \
   {                                                                                                  \
@@ -755,10 +764,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     __builtin_amdgcn_s_waitcnt(WAIT);                                                                \
     __builtin_amdgcn_s_barrier();                                                                    \
     if constexpr (PERSIST) {                                                                         \
-      issue((J) % 3 == 0 ? st2 : (J) % 3 == 1 ? st0 : st1, j + 2, cur);                              \
+      issue((J) % 3 == 0 ? st2 : (J) % 3 == 1 ? st0 : st1, j + 2, cur, NT);                              \
       compute((J) % 3 == 0 ? st0 : (J) % 3 == 1 ? st1 : st2, j, FULL);                               \
     } else {                                                                                         \
-      issue(((J) + 2) % 3, min(j + 2, last), cur);                                                   \
+      issue(((J) + 2) % 3, min(j + 2, last), cur, NT);                                                   \
       compute((J) % 3, j, FULL);                                                                     \
     }                                                                                                \
   }
@@ -800,13 +809,25 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
         const uint32_t sj = (rot + j) % 3;
         __builtin_amdgcn_s_waitcnt(kWaitStep);
         __builtin_amdgcn_s_barrier();
-        issue(sj == 0 ? 2u : sj - 1, has_next ? f : last, nxt);
+        issue(sj == 0 ? 2u : sj - 1, has_next ? f : last, nxt, std::false_type{});
         compute(sj, j, FULL);
       }
     }
   };
-  if (rb_live == 4) run(std::true_type{});
-  else run(std::false_type{});
+  // an expert with one M tile reads each weight byte once: its weight
+  // loads are non-temporal, so they do not evict the weight tiles that the
+  // multi-tile experts' M tiles share in L2 (the tile's first two steps,
+  // loaded before this choice, use the default policy)
+  bool once = false;
+  if (!p.dense_m_tiles && rows) {
+    uint32_t lo, hi;
+    if constexpr (PERSIST) lo = tab.off[expert], hi = tab.off[expert + 1];
+    else lo = p.offsets[expert], hi = p.offsets[expert + 1];
+    once = hi >= lo && hi - lo <= BM;
+  }
+  if (__builtin_amdgcn_readfirstlane(once ? 1u : 0u)) run(std::false_type{}, std::true_type{});
+  else if (rb_live == 4) run(std::true_type{}, std::false_type{});
+  else run(std::false_type{}, std::false_type{});
   // no DMA may still target this block's LDS when its waves end (a
   // persistent block's loads of its next tile stay in flight)
   if (!PERSIST || !has_next) __builtin_amdgcn_s_waitcnt(kWaitVm0);
