@@ -154,8 +154,9 @@ __device__ __forceinline__ v8i cat8(v4i x, v4i y) {
 // steps up (L streaming tiles of T), and each XCD (blocks b % 8) walks one
 // contiguous range of the sequence, so its CUs run both kinds at once.
 // Streaming experts are ordered by expert index, one M tile x all N tiles
-// each; multi-tile experts are expert-major, in groups of up to 32 M tiles
-// walked M-fastest, so concurrently running tiles share W in L2.
+// each; multi-tile experts are expert-major, in groups of up to GROUP_M M
+// tiles (kTableGroupM in the persistent walk) walked M-fastest, so
+// concurrently running tiles share W in L2.
 // The per-expert tile counts are scanned by the whole block (wave-level
 // shuffle scans plus the eight wave totals).
 __device__ bool moe_tile(const MoeParams& p, uint32_t vb, uint32_t& expert, uint32_t& row0, uint32_t& rows,
