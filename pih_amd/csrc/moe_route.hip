@@ -227,6 +227,13 @@ __global__ __launch_bounds__(256) void accumulate_kernel(const uint16_t* out, co
   if (bad) atomicOr(err, bad);
 }
 
+// 16 bytes by a non-temporal load (data read once)
+__device__ __forceinline__ uint4 load16_nt(const uint4* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // out[t, :] = bf16(sum of t's expert rows in ascending row order (= ascending
 // expert id) + shared).  The fp32 adds run in the order the reference's
 // accumulator oracle applies them (src/model/
@@ -254,6 +261,7 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* expert_out
   }
   uint32_t bad = 0;
   const uint32_t vec = hidden / 8u;
+  // every row is read once: non-temporal loads
   // rows past n (n <= 8 in the unrolled path) repeat row r[0]; their values
   // are replaced by +0.0f, which leaves the sum unchanged (it starts at +0.0f
   // and so is never -0.0f), so the sum keeps the ascending row order exactly
@@ -273,14 +281,15 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* expert_out
       uint4 x[kUnroll];
 #pragma unroll
       for (uint32_t j = 0; j < kUnroll; ++j)
-        x[j] = reinterpret_cast<const uint4*>(expert_out)[(uint64_t)r[j < n ? j : 0] * vec + c];
+        x[j] = load16_nt(reinterpret_cast<const uint4*>(expert_out) + (uint64_t)r[j < n ? j : 0] * vec + c);
 #pragma unroll
       for (uint32_t j = 0; j < kUnroll; ++j) add(x[j], j < n);
     } else {
-      for (uint32_t j = 0; j < n; ++j) add(reinterpret_cast<const uint4*>(expert_out)[(uint64_t)r[j] * vec + c], true);
+      for (uint32_t j = 0; j < n; ++j)
+        add(load16_nt(reinterpret_cast<const uint4*>(expert_out) + (uint64_t)r[j] * vec + c), true);
     }
     if (shared) {
-      const uint4 x = reinterpret_cast<const uint4*>(shared)[(uint64_t)t * vec + c];
+      const uint4 x = load16_nt(reinterpret_cast<const uint4*>(shared) + (uint64_t)t * vec + c);
       const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
