@@ -227,13 +227,6 @@ __global__ __launch_bounds__(256) void accumulate_kernel(const uint16_t* out, co
   if (bad) atomicOr(err, bad);
 }
 
-// 16 bytes by a non-temporal load (data read once)
-__device__ __forceinline__ uint4 load16_nt(const uint4* p) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-
 // out[t, :] = bf16(sum of t's expert rows in ascending row order (= ascending
 // expert id) + shared).  The fp32 adds run in the order the reference's
 // accumulator oracle applies them (src/model/
