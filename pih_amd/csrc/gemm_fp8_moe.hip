@@ -38,6 +38,7 @@
 // an 8 M x 4 N grouping of the multi-tile ones cut the L2-miss bytes by
 // 9 % but ran 3 % slower than M-fastest groups of 32).
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -707,25 +708,34 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       if (live(3)) fma4(3, tB);
     } else {
       // UE8M0 scales ride in the MFMA's E8M0 operands and the MFMAs chain on
-      // the accumulator; a 255 scale raises the scale bit and runs as 0
-      // (2^-127), contributing nothing, as the reference skips the block
+      // the accumulator.  A 255 scale raises the scale bit and its block adds
+      // nothing, as the reference skips the block: a W block's MFMAs run with
+      // both E8M0 scales 0 (2^-254 times a sum below 2^25 is below the fp32
+      // range: exactly zero is added), an A row's fragment bytes become 0.
       // (selects, not an index: a runtime index would put the array in scratch)
       const uint32_t wb0 = wsel0 ? w_byte0[1] : w_byte0[0], wb1 = wsel1 ? w_byte0[1] : w_byte0[0];
       const uint32_t wsh0 = 8 * ((wb0 + kb) & 3u), wsh1 = 8 * ((wb1 + kb) & 3u);
       uint32_t wsb0 = (sw0 >> wsh0) & 0xffu, wsb1 = (sw1 >> wsh1) & 0xffu;
-      if (wsb0 == 0xffu || wsb1 == 0xffu) bad |= kErrScale;
-      wsb0 = wsb0 == 0xffu ? 0u : wsb0;
-      wsb1 = wsb1 == 0xffu ? 0u : wsb1;
-      auto mma = [&](int r, const v8i& af) {
+      const bool wff0 = wsb0 == 0xffu, wff1 = wsb1 == 0xffu;  // wave-uniform
+      if (wff0 || wff1) bad |= kErrScale;
+      wsb0 = wff0 ? 0u : wsb0;
+      wsb1 = wff1 ? 0u : wsb1;
+      auto mma = [&](int r, v8i af) {
         uint32_t sb = ((uint32_t)sa4[r] >> (8 * ((a_byte0[r] + kb) & 3u))) & 0xffu;
-        if (sb == 0xffu) {
-          bad |= kErrScale;
-          sb = 0;
+        const bool aff = sb == 0xffu;
+        if (__builtin_amdgcn_ballot_w64(aff)) {  // rare: an invalid A-row scale in the wave
+          if (aff) {
+            bad |= kErrScale;
+            sb = 127;
+            af = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          }
         }
+        const uint32_t sb0 = wff0 ? 0u : sb, sb1 = wff1 ? 0u : sb;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
           acc[nb][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-              wf[nb], af, acc[nb][r], 0, 0, 0, (int)((kSwi && nb >= 2) ? wsb1 : wsb0), 0, (int)sb);
+              wf[nb], af, acc[nb][r], 0, 0, 0, (int)((kSwi && nb >= 2) ? wsb1 : wsb0), 0,
+              (int)((kSwi && nb >= 2) ? sb1 : sb0));
       };
       // A fragments one block ahead (at most four LDS reads in flight)
       v8i af = a_frag(0);
@@ -1174,16 +1184,20 @@ void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out, 
 
 // Blocks of a persistent launch: one per CU, a multiple of 8 (the tile
 // sequence is split into 8 XCD ranges by blockIdx % 8); 0 if unknown.
+// (Per-device cache in relaxed atomics: concurrent host threads store the
+// same value.)
 uint32_t PersistentBlocks() {
-  static uint32_t cached[64] = {};
+  static std::atomic<uint32_t> cached[kHostMaxDevices] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (!cached[dev]) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kHostMaxDevices) return 0;
+  uint32_t v = cached[dev].load(std::memory_order_relaxed);
+  if (!v) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) return 0;
-    cached[dev] = (uint32_t)cus / 8 * 8;
+    v = (uint32_t)cus / 8 * 8;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return v;
 }
 
 // Plain (bf16 / fp32) outputs without an A gather run persistent: a block

@@ -193,6 +193,20 @@ __device__ __forceinline__ uint32_t ff_bytes(uint32_t w) {
   return (n - 0x01010101u) & ~n & 0x80808080u;
 }
 
+// An operand fragment whose E8M0 block scale is 0xFF (the reference skips
+// that block) becomes zeros with scale 127, so its products add exactly 0;
+// the test is wave-wide, and the select runs only in a wave that has one.
+template <typename S>
+__device__ __forceinline__ void zero_ff_row(S& scale, v8i& frag) {
+  const bool ff = (uint32_t)scale == 0xffu;
+  if (__builtin_amdgcn_ballot_w64(ff)) {
+    if (ff) {
+      scale = 127;
+      frag = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+  }
+}
+
 // 8 e2m1 nibbles of `w` (low nibble first) times the power of two `scale`
 // as 8 bf16 values.  v_cvt_scalef32_pk_bf16_fp4 converts one byte (two
 // nibbles, low first) per instruction; the product is exact for every UE8M0
@@ -330,23 +344,19 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
       if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
     } else if constexpr (ASCALE) {
       if constexpr (E8M0_A) {
-        // a 0xFF scale raises the scale bit; its block then runs with
-        // 2^-127, so it adds (almost) nothing, as the reference skips it
+        // a 0xFF scale raises the scale bit and stays 0xFF in LDS: the
+        // compute zeroes that row's fragment, so its block adds nothing, as
+        // the reference skips it
         rsa = static_cast<const uint8_t*>(p.a_scale)[s_src * (K / 128) + kb];
-        if (rsa == 0xffu) {
-          if (tid < rows) bad |= kErrScale;
-          rsa = 0;
-        }
+        if (rsa == 0xffu && tid < rows) bad |= kErrScale;
       } else {
         rsa = __float_as_uint(static_cast<const float*>(p.a_scale)[s_src * (K / 128) + kb]);
       }
     }
     if constexpr (KIND == kFp4) {
       rsb = *reinterpret_cast<const uint32_t*>(ws_row + (uint64_t)kb * 4);
+      // 0xFF bytes stay: the compute zeroes the fragment they scale
       if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
-      // 0xFF bytes (exactly those) -> E8M0 0
-      const uint32_t ff = ((rsb & 0x7f7f7f7fu) + 0x01010101u) & rsb & 0x80808080u;
-      rsb &= ~((ff >> 7) * 0xffu);
     } else if constexpr (KIND == kBf16Fp4) {
       rsb = *reinterpret_cast<const uint16_t*>(ws_row + (uint64_t)kb * 2);
       if (ff_bytes(rsb) && tid < BN) bad |= kErrScale;
@@ -446,6 +456,12 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
         if (ws0b == 0xffu || ws1b == 0xffu) bad |= kErrScale;
       }
     }
+    // a 0xFF W block scale: that block's MFMAs run with both E8M0 scales 0
+    // (2^-254 times a sum below 2^25 is below the fp32 range, so exactly
+    // zero is added), as the reference skips the block
+    const bool wff0 = ws0b == 0xffu, wff1 = ws1b == 0xffu;
+    ws0b = wff0 ? 0u : ws0b;
+    ws1b = wff1 ? 0u : ws1b;
 
     if (ms_live) {
       // W operands for this wave's four 16-column blocks
@@ -465,6 +481,7 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
         } else if constexpr (KIND == kFp4 || KIND == kMx4) {
           bv[ns] = cat8(*reinterpret_cast<const v4i*>(&sB[buf][lds_at<64>(brow, lg)]), v4i{0, 0, 0, 0});
           bsc[ns] = (sBs[buf][brow] >> (8 * lg)) & 0xffu;
+          if constexpr (KIND == kFp4) zero_ff_row(bsc[ns], bv[ns]);
         } else {  // kBf16Fp4: 16 nibbles = k 16*lg .. 16*lg+15 of the step
           const uint2 w2 = *reinterpret_cast<const uint2*>(pb + lg * 8);
           const float sc = ue8m0_value((sBs[buf][brow] >> (8 * (lg >> 1))) & 0xffu);
@@ -497,17 +514,20 @@ __global__ __launch_bounds__(THREADS, 2) void mfma_gemm_kernel(GemmParams p) {
               acc[ms][ns][i] = __builtin_fmaf(t[i], __uint_as_float((uint32_t)s4[i]) * wsv, acc[ms][ns][i]);
           }
         } else if constexpr (KIND == kFp8) {
-          const int sab = (int)sAs[buf][arow];
-          const v8i av = cat8(a0, a1);
+          int sab = (int)sAs[buf][arow];
+          v8i av = cat8(a0, a1);
+          zero_ff_row(sab, av);
 #pragma unroll
           for (int ns = 0; ns < 4; ++ns) {
+            const bool wff = (OUT == kOutSwiGlu && ns >= 2) ? wff1 : wff0;
             const int wsb = (int)((OUT == kOutSwiGlu && ns >= 2) ? ws1b : ws0b);
-            acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv[ns], acc[ms][ns], 0, 0, 0, sab,
-                                                                           0, wsb);
+            acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv[ns], acc[ms][ns], 0, 0, 0,
+                                                                           wff ? 0 : sab, 0, wsb);
           }
         } else if constexpr (KIND == kFp4) {
-          const int sab = (int)sAs[buf][arow];
-          const v8i av = cat8(a0, a1);
+          int sab = (int)sAs[buf][arow];
+          v8i av = cat8(a0, a1);
+          zero_ff_row(sab, av);
 #pragma unroll
           for (int ns = 0; ns < 4; ++ns)
             acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv[ns], acc[ms][ns], 0, 4, 0, sab,

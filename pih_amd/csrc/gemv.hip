@@ -900,12 +900,15 @@ void launch_mt(const GemvParams& p, int waves, hipStream_t s) {
 template <int FMT, int WAVES, int U, bool ONE_ROW>
 St launch_lds(const GemvGroup& g, uint32_t spw, hipStream_t s) {
   const uint32_t lds = small_m_lds<FMT>(g.prob[0].m, spw, WAVES, U);
-  static bool raised = false;  // LDS above 64 KB must be allowed once per kernel
-  if (lds > 65536 && !raised) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_lds_kernel<FMT, WAVES, U, ONE_ROW>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-      return Internal("gemv_lds_attribute_failed");
-    raised = true;
+  static PerDeviceOnce raised;  // LDS above 64 KB must be allowed once per kernel and device
+  if (lds > 65536) {
+    const St r = raised.run([] {
+      return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_lds_kernel<FMT, WAVES, U, ONE_ROW>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess
+                 ? Ok()
+                 : Internal("gemv_lds_attribute_failed");
+    });
+    if (!r.ok()) return r;
   }
   hipLaunchKernelGGL((gemv_lds_kernel<FMT, WAVES, U, ONE_ROW>), dim3(g.block_start[g.count]), dim3(WAVES * 64), lds, s,
                      g, spw);
@@ -998,13 +1001,14 @@ St launch_mid(const GemvGroup& g, uint32_t spw, hipStream_t s) {
   constexpr uint32_t lds = mid_lds_bytes<FMT, MT, NW, WAVES, U>();
   static_assert(lds <= 160 * 1024, "mid GEMV tiles exceed the LDS");
   if constexpr (lds > 65536) {
-    static bool raised = false;  // LDS above 64 KB must be allowed once per kernel
-    if (!raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_mid_kernel<FMT, MT, NW, WAVES, U>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-        return Internal("gemv_mid_attribute_failed");
-      raised = true;
-    }
+    static PerDeviceOnce raised;  // LDS above 64 KB must be allowed once per kernel and device
+    const St r = raised.run([] {
+      return hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_mid_kernel<FMT, MT, NW, WAVES, U>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess
+                 ? Ok()
+                 : Internal("gemv_mid_attribute_failed");
+    });
+    if (!r.ok()) return r;
   }
   hipLaunchKernelGGL((gemv_mid_kernel<FMT, MT, NW, WAVES, U>), dim3(g.block_start[g.count]), dim3(WAVES * 64), lds,
                      s, g, spw);

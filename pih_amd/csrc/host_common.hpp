@@ -8,6 +8,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <atomic>
 #include <new>
 
 #include "pih/plugin_sdk/status.h"
@@ -53,6 +54,27 @@ template <typename T>
 inline T* Ptr(uintptr_t p) {
   return reinterpret_cast<T*>(p);
 }
+
+// A one-time host step per device (raising a kernel's LDS limit): run()
+// performs the step on the current device until it has succeeded there
+// once.  Host threads that arrive together may both perform it (every such
+// step is idempotent); the flags are atomics, so there is no data race.
+constexpr int kHostMaxDevices = 64;
+class PerDeviceOnce {
+ public:
+  template <typename F>
+  St run(F&& step) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kHostMaxDevices) return step();
+    if (done_[dev].load(std::memory_order_acquire)) return Ok();
+    const St s = step();
+    if (s.ok()) done_[dev].store(true, std::memory_order_release);
+    return s;
+  }
+
+ private:
+  std::atomic<bool> done_[kHostMaxDevices] = {};
+};
 
 // struct_size / abi_version gate shared by every entry point.
 template <typename R>

@@ -17,6 +17,7 @@
 // Error bits: 1 expert id out of range, 2 expert repeated within a token,
 // 4 route weight non-finite or negative.  An invalid route gets no row
 // (token_rows = 0xffffffff) and is left out of the offsets.
+#include <atomic>
 #include <mutex>
 
 #include "device_common.hpp"
@@ -398,22 +399,36 @@ namespace {
 constexpr int kMaxDevices = 64;
 
 struct ScratchSlot {
-  std::once_flag once;
-  void* ptr = nullptr;
-  hipError_t err = hipErrorNotInitialized;
+  std::mutex lock;
+  std::atomic<void*> ptr{nullptr};
 };
 ScratchSlot g_scratch[kMaxDevices];
 
-// The scratch array's address on the current device, looked up once per
-// device (with that device current) and kept.
+// The scratch array's address on the current device, looked up with that
+// device current and kept once the lookup has succeeded (a failed lookup is
+// retried on the next call).
 St NoAllocScratch(void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return Internal("route_plan_noalloc_device_unavailable");
   ScratchSlot& slot = g_scratch[dev];
-  std::call_once(slot.once, [&slot] { slot.err = hipGetSymbolAddress(&slot.ptr, HIP_SYMBOL(scratch)); });
-  if (slot.err != hipSuccess || slot.ptr == nullptr) return Internal("route_plan_noalloc_scratch_unavailable");
-  *out = slot.ptr;
+  void* p = slot.ptr.load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> guard(slot.lock);
+    p = slot.ptr.load(std::memory_order_relaxed);
+    if (!p) {
+      const St clean = RequireCleanLastError();  // an earlier error stays reported, not cleared below
+      if (!clean.ok()) return clean;
+      void* found = nullptr;
+      if (hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)) != hipSuccess || found == nullptr) {
+        (void)hipGetLastError();  // this lookup's own error: a later call may retry
+        return Internal("route_plan_noalloc_scratch_unavailable");
+      }
+      slot.ptr.store(found, std::memory_order_release);
+      p = found;
+    }
+  }
+  *out = p;
   return Ok();
 }
 

@@ -265,6 +265,108 @@ def test_w4a16_asymmetric_reduces_to_symmetric():
     np.testing.assert_array_equal(w, (v * np.repeat(np.ldexp(1.0, e), 128, axis=1)).astype(np.float32))
 
 
+def _pack_nibbles_u32(vals: np.ndarray) -> np.ndarray:
+    """[rows, 8 j] nibbles -> u32 words, value 8 w + i in nibble i of word w
+    (bits 4i .. 4i + 3): the BASELINE layout the test declares."""
+    rows, cnt = vals.shape
+    v = np.zeros((rows, -(-cnt // 8) * 8), np.uint32)
+    v[:, :cnt] = vals
+    v = v.reshape(rows, -1, 8)
+    out = np.zeros(v.shape[:2], np.uint32)
+    for i in range(8):
+        out |= v[:, :, i] << np.uint32(4 * i)
+    return out
+
+
+def test_w4a16_asymmetric_distinct_zero_points():
+    """Asymmetric INT4 with a different zero point in every group, over two
+    zero-point words (16 groups at K = 2048), packed here from unpacked
+    values by the declared layout (weight k in nibble k % 8 of word k / 8,
+    zero point of group g in nibble g % 8 of zero word g / 8): the dequant
+    must return (q - z) * s exactly, and a one-hot activation e_k must read
+    bf16((q[n, k] - z[n, k / 128]) * s[n, k / 128]) back through the GEMV.
+    A nibble order reversed in either word, or a zero point indexed by k / 8
+    or g / 16, changes the answer (checked on the same data)."""
+    n, k = 6, 2048
+    groups = k // 128
+    q = (synth.splitmix64(80, n * k) % np.uint64(16)).astype(np.int64).reshape(n, k)
+    z = ((np.arange(groups)[None, :] * 5 + 3 * np.arange(n)[:, None] + 1) % 16).astype(np.int64)
+    assert len(np.unique(z[0])) == groups  # every group of a row has its own zero point
+    # bf16 scales with few mantissa bits: (q - z) * s is exact in fp32 and bf16
+    s = (np.ldexp(1.0, -(synth.splitmix64(81, n * groups) % np.uint64(6)).astype(np.int64) - 6) *
+         (1.0 + (synth.splitmix64(82, n * groups) % np.uint64(4)).astype(np.float64) / 4)).reshape(n, groups)
+    s_bits = oracle.f32_to_bf16_bits(s.astype(np.float32))
+    assert (oracle.bf16_bits_to_f32(s_bits) == s).all()
+    qweight = _pack_nibbles_u32(q.astype(np.uint32))
+    zeros = _pack_nibbles_u32(z.astype(np.uint32))
+    assert qweight.shape == (n, k // 8) and zeros.shape == (n, 2)
+    want = ((q - np.repeat(z, 128, 1)) * np.repeat(s, 128, 1)).astype(np.float32)
+    got = oracle.w4a16_asym_dequant(qweight, s_bits, zeros, k)
+    np.testing.assert_array_equal(got, want)
+    # one-hot activations through the GEMV, one per position class: every
+    # nibble slot of a weight word, every group of both zero words
+    ks = np.array(sorted({g * 128 + (g * 37) % 128 for g in range(groups)} | set(range(8)) |
+                         {8 * 129 + j for j in range(8)}))
+    x = np.zeros((ks.size, k), np.float32)
+    x[np.arange(ks.size), ks] = 1.0
+    out = oracle.w4a16_asym(oracle.f32_to_bf16_bits(x), qweight, s_bits, zeros)
+    np.testing.assert_array_equal(out, oracle.f32_to_bf16_bits(want[:, ks].T.copy()))
+    # the same data read with a reversed zero-point nibble order or the
+    # zero point of word k / 8 gives other weights: the check discriminates
+    z_rev = np.concatenate([z[:, 7::-1], z[:, 15:7:-1]], 1)
+    assert (np.repeat(z_rev, 128, 1) != np.repeat(z, 128, 1)).any()
+    assert ((q - np.repeat(z_rev, 128, 1)) * np.repeat(s, 128, 1) != want).any()
+
+
+def test_qwen_mlp_small_integer_composition():
+    """cfg1's checker: gate and up through the BF16 linear (bf16 RNE at the
+    output), SiLU-mul in fp32 rounded once, then down.  Integer inputs make
+    both first GEMMs exact; their sums exceed 256, so the bf16 rounding of
+    gate and up changes them.  A composition that rounds gate and up to
+    bf16, takes SiLU-mul in fp32 (numpy; its exp may differ from the C
+    library's in the last bit, so no SiLU product of a gate with |g| < 24
+    may lie within 4e-6 relative of a bf16 tie, asserted below), rounds
+    it, and sums the down GEMM in float64 (no output closer to a tie than
+    the fp32 accumulation's error bound) must agree exactly; the compositions with gate and up swapped or
+    without rounding gate and up must not."""
+    m, hdim, idim = 2, 128, 32
+    rng = np.random.default_rng(17)
+    x = rng.integers(-8, 9, (m, hdim)).astype(np.float32)
+    wg = rng.integers(-8, 9, (idim, hdim)).astype(np.float32)
+    wu = rng.integers(-8, 9, (idim, hdim)).astype(np.float32)
+    b = oracle.f32_to_bf16_bits
+    wd = oracle.bf16_bits_to_f32(b(rng.normal(0.0, 0.05, (hdim, idim)).astype(np.float32)))
+    got = oracle.bf16_bits_to_f32(oracle.qwen_mlp(b(x), b(wg), b(wu), b(wd))).astype(np.float64)
+
+    rnd = lambda v: oracle.bf16_bits_to_f32(b(np.asarray(v, np.float32))).astype(np.float64)
+
+    def near_tie(v, tol):
+        # within tol of a bf16 rounding midpoint
+        v = np.abs(np.asarray(v, np.float64))
+        q = np.ldexp(1.0, (np.floor(np.log2(v + 1e-300)) - 7).astype(int))
+        frac = v / q - np.floor(v / q)
+        return (v > 0) & (np.abs(frac - 0.5) * q <= tol)
+
+    X = x.astype(np.float64)
+    g_raw, u_raw = X @ wg.T.astype(np.float64), X @ wu.T.astype(np.float64)
+    assert (np.abs(g_raw) > 256).any() and (rnd(g_raw) != g_raw).any()  # the rounding bites
+
+    def chain(g, u, premise=True):
+        g32, u32 = g.astype(np.float32), u.astype(np.float32)
+        with np.errstate(over="ignore"):
+            h = (g32 / (np.float32(1.0) + np.exp(-g32))) * u32
+        assert not premise or not (near_tie(h, 4e-6 * np.abs(h)) & (np.abs(g32) < 24)).any()
+        y = rnd(h) @ wd.T.astype(np.float64)
+        # fp32 strict-k accumulation error bound: k * 2^-24 * sum |terms|
+        assert not premise or not near_tie(y, idim * 2.0 ** -24 * (np.abs(rnd(h)) @ np.abs(wd.T.astype(np.float64)))).any()
+        return rnd(y)
+
+    want = chain(rnd(g_raw), rnd(u_raw))
+    np.testing.assert_array_equal(got, want)
+    assert (chain(rnd(u_raw), rnd(g_raw), False) != got).any()  # gate/up swapped
+    assert (chain(g_raw, u_raw, False) != got).any()  # gate/up not rounded to bf16
+
+
 def test_bf16_gemm_exact_on_small_integers():
     m, n, k = 4, 8, 256
     a = (synth.splitmix64(60, m * k) % np.uint64(9)).astype(np.float32).reshape(m, k) - 4
@@ -336,6 +438,23 @@ def test_ordered_accumulate_reference_kats(gold):
     # golden: reference accumulator (experts ascending) + shared
     acc = oracle.ordered_accumulate(gold["acc_rows"], gold["plan_token"], 2)
     np.testing.assert_array_equal((acc + f32(gold["acc_shared"])).view(np.uint32), gold["acc_out"].view(np.uint32))
+
+
+def test_finalize_with_shared_rows(gold):
+    """po_finalize with a shared-expert row: the reference's finalize
+    (deepseek_expert_accumulator_oracle.cpp:69-85) returns acc + shared in
+    fp32 (the golden acc_out, written by the compiled reference), and the
+    device entry stores it as bf16 (deepseek_expert_accumulate.cu:41-56):
+    the oracle must give bf16(acc_out) bit for bit; without the shared row
+    it gives bf16(acc); a non-finite sum is an error."""
+    acc = oracle.ordered_accumulate(gold["acc_rows"], gold["plan_token"], 2)
+    got = oracle.finalize(acc, np.ascontiguousarray(gold["acc_shared"]))
+    np.testing.assert_array_equal(got, oracle.f32_to_bf16_bits(gold["acc_out"]))
+    assert (got != oracle.finalize(acc)).any()  # the shared rows change the result
+    np.testing.assert_array_equal(oracle.finalize(acc), oracle.f32_to_bf16_bits(acc))
+    big = np.full((1, 4), 3.0e38, np.float32)
+    with pytest.raises(oracle.OracleError):
+        oracle.finalize(big, oracle.f32_to_bf16_bits(big))
 
 
 def test_routed_expert_reference_kat_and_golden(gold):
@@ -703,6 +822,36 @@ def test_v41_fp4_to_fp8_reference_vectors(gold):
         w, s, st = oracle.v41_fp4_block_to_fp8(gold["v41_fp4_packed"][b], gold["v41_fp4_scales"][b])
         assert st == 0 and s == gold["v41_fp8_scale"][b]
         np.testing.assert_array_equal(w.ravel(), gold["v41_fp8_weight"][b])
+
+
+def test_v41_fp4_to_fp8_tensor_tiling(gold):
+    """The tensor form (weight_expert_convert.cpp:64-100) on a 64 x 128
+    tensor: 2 x 4 blocks of 32 x 32, block (br, bc) taken from golden block
+    (4 br + bc) % 6 of the compiled reference's ConvertExpertFp4Block
+    (packed rows of 64 bytes, row scales [64, 4]).  Every output block and
+    its shared scale must equal that golden block's, so a transposed block
+    grid, a wrong packed-row stride or a wrong scale index fails."""
+    rows, cols = 64, 128
+    packed = np.zeros((rows, cols // 2), np.uint8)
+    scales = np.zeros((rows, cols // 32), np.uint8)
+    src = lambda br, bc: (4 * br + bc) % gold["v41_fp4_packed"].shape[0]
+    for br in range(2):
+        for bc in range(4):
+            b = src(br, bc)
+            packed[32 * br:32 * br + 32, 16 * bc:16 * bc + 16] = gold["v41_fp4_packed"][b].reshape(32, 16)
+            scales[32 * br:32 * br + 32, bc] = gold["v41_fp4_scales"][b]
+    w, s = oracle.v41_fp4_to_fp8(packed, scales)
+    assert w.shape == (rows, cols) and s.shape == (2, 4)
+    for br in range(2):
+        for bc in range(4):
+            b = src(br, bc)
+            assert s[br, bc] == gold["v41_fp8_scale"][b]
+            np.testing.assert_array_equal(w[32 * br:32 * br + 32, 32 * bc:32 * bc + 32].ravel(),
+                                          gold["v41_fp8_weight"][b])
+            wb, sb, st = oracle.v41_fp4_block_to_fp8(gold["v41_fp4_packed"][b], gold["v41_fp4_scales"][b])
+            assert st == 0 and sb == s[br, bc]
+    # the golden blocks differ, so a swapped block placement is visible
+    assert len({gold["v41_fp8_weight"][src(br, bc)].tobytes() for br in range(2) for bc in range(4)}) > 1
 
 
 def test_v41_fp4_to_fp8_closed_forms():
