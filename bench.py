@@ -429,6 +429,69 @@ def bench_mxfp4(torch, iters: int):
     return out
 
 
+V4_H, V4_I, V4_TOPK = 4096, 2048, 6
+
+
+def v4_router_inputs(tokens: int):
+    """Router logits ~N(0, 1) and a selection bias (N(0, 0.05) with +1.5 on
+    three experts, so a batch holds both light and multi-tile experts)."""
+    from pih_amd import synth
+
+    raw = synth.normal(synth.config_seed(6, tokens), tokens * E).astype(np.float32).reshape(tokens, E)
+    bias = (0.05 * synth.normal(synth.config_seed(6, 1), E)).astype(np.float32)
+    bias[[3, 77, 140]] += np.float32(1.5)
+    return raw, bias
+
+
+def bench_v4flash(torch, iters: int):
+    """The reference's production MoE geometry, DeepSeek-V4-Flash
+    (include/pih/model/deepseek_v4_config.h:22-27: hidden 4096, 256 routed
+    experts, 6 active; intermediate 2048; MXFP4 experts x e4m3 activations):
+    the device router (sqrt-softplus + bias, weights x 1.5) and the layer
+    entry at decode batches of 64 and 512 tokens.  HBM-bound: bytes =
+    touched experts x 13,369,344 (the reference's expert bundle: W1/W3/W2
+    e2m1 + UE8M0) + token activations in and out; the router is timed on
+    its own (it reads the f32 logits)."""
+    from pih_amd import abi, synth
+    from pih_amd.linear import MoeLayer, router_topk
+
+    H4, I4, K6 = V4_H, V4_I, V4_TOPK
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x50494806)
+    w13 = torch.randint(0, 256, (E, 2 * I4, H4 // 2), dtype=torch.uint8, device=dev, generator=gen)
+    s13 = torch.randint(118, 127, (E, 2 * I4, H4 // 32), dtype=torch.uint8, device=dev, generator=gen)
+    w2 = torch.randint(0, 256, (E, H4, I4 // 2), dtype=torch.uint8, device=dev, generator=gen)
+    s2 = torch.randint(118, 127, (E, H4, I4 // 32), dtype=torch.uint8, device=dev, generator=gen)
+    per_expert = 3 * I4 * H4 // 2 + 3 * I4 * H4 // 32
+    out = {}
+    for tokens in (64, 512):
+        raw, bias = v4_router_inputs(tokens)
+        raw_d = torch.from_numpy(raw).to(dev)
+        bias_d = torch.from_numpy(bias).to(dev)
+        ids_d, wts_d, rflag = router_topk(raw_d, K6, abi.ROUTER_SQRT_SOFTPLUS, 1.5, bias_d)
+        router_ms = _timed(torch, lambda i: router_topk(raw_d, K6, abi.ROUTER_SQRT_SOFTPLUS, 1.5, bias_d,
+                                                         flag=rflag, out=(ids_d, wts_d)), iters)
+        ids = ids_d.cpu().numpy()
+        touched = int((np.bincount(ids.ravel(), minlength=E) > 0).sum())
+        x = torch.from_numpy(synth.bf16_normal(synth.config_seed(6, tokens + 1), (tokens, H4)).view(np.int16))
+        x = x.to(dev).view(torch.bfloat16)
+        layer = MoeLayer(w13, s13, w2, s2, tokens, K6, weight_format=abi.WEIGHT_MXFP4,
+                         activation_type=abi.ACTIVATION_E4M3, swiglu_limit=10.0)
+        ms = _timed(torch, lambda i: layer.forward(x, ids_d, wts_d), iters)
+        if int(layer.flag.item()) or int(rflag.item()):
+            raise RuntimeError(f"v4-flash error flags {int(layer.flag.item())} {int(rflag.item())}")
+        algo = touched * per_expert + tokens * H4 * 2 * 2
+        flop = 2.0 * tokens * K6 * 3 * I4 * H4
+        gbs = algo / (ms * 1e-3) / 1e9
+        out[f"t{tokens}_e4m3"] = {"us_per_layer": round(ms * 1e3, 1), "gbs": round(gbs, 1),
+                                  "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                  "tflops": round(flop / (ms * 1e-3) / 1e12, 2), "touched_experts": touched,
+                                  "algorithmic_bytes": algo, "router_us": round(router_ms * 1e3, 1)}
+        del layer
+    return out
+
+
 def _rotation(torch, gen, per_bytes: int, min_total: int = 600_000_000):
     """One uint8 buffer of random bytes holding enough weight sets of
     ``per_bytes`` (each 256-byte aligned) that cycling through them exceeds
@@ -807,6 +870,7 @@ def main() -> int:
                      "mfma_frac": round(flop_gu / (gu_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)},
         "expert_buckets": buckets,
         "moe_mxfp4_decode": side.get("mxfp4"),
+        "moe_mxfp4_v4_flash": side.get("v4flash"),
         "decode_gemv": side.get("decode"),
         "drop_in": side.get("dropin"),
         "cpu_baseline": cpu,
@@ -815,7 +879,7 @@ def main() -> int:
     return 0
 
 
-LEGS = ("moe_fp8", "buckets", "mxfp4", "decode", "dropin", "cpu")
+LEGS = ("moe_fp8", "buckets", "mxfp4", "v4flash", "decode", "dropin", "cpu")
 
 
 def run_side_legs(torch, legs, args) -> dict:
@@ -826,6 +890,7 @@ def run_side_legs(torch, legs, args) -> dict:
     iters = max(10, args.steps)
     out = {}
     for leg, fn, what in (("mxfp4", bench_mxfp4, "MXFP4 MoE decode (configs[4])"),
+                          ("v4flash", bench_v4flash, "MXFP4 MoE at the DeepSeek-V4-Flash geometry"),
                           ("decode", bench_decode, "decode GEMV / prefill (configs[1], [2])"),
                           ("dropin", bench_dropin, "drop-in entries at the reference's call shapes")):
         if leg not in legs:

@@ -527,12 +527,15 @@ void launch_kb(const StreamParams& sp, uint32_t grid, hipStream_t s, OutKind out
     hipLaunchKernelGGL((fp4_moe_stream_kernel<ACT, kOutBf16, KBT>), dim3(grid), dim3(NTH), 0, s, sp);
 }
 
-// fully unrolled K loops for the DeepSeek shapes (K = 7168: 28 steps,
-// K = 2048: 8 steps), a loop otherwise
+// fully unrolled K loops for the DeepSeek shapes (K = 7168: 28 steps, the
+// V3-shaped gate/up of BASELINE configs[4]; K = 4096: 16 steps, the
+// V4-Flash gate/up at hidden 4096, include/pih/model/deepseek_v4_config.h:22;
+// K = 2048: 8 steps, both down projections), a loop otherwise
 template <int ACT>
 void launch_out(const StreamParams& sp, uint32_t grid, hipStream_t s, OutKind out) {
   const uint32_t kb = sp.k / KSTEP;
   if (kb == 28) launch_kb<ACT, 28>(sp, grid, s, out);
+  else if (kb == 16) launch_kb<ACT, 16>(sp, grid, s, out);
   else if (kb == 8) launch_kb<ACT, 8>(sp, grid, s, out);
   else launch_kb<ACT, 0>(sp, grid, s, out);
 }

@@ -368,3 +368,97 @@ def test_grouped_fp8_gemm_stores_nonfinite(eng, t, ng):
     assert flag == 2048
     vals = oracle.bf16_bits_to_f32(out).reshape(t, g, ng)
     assert np.all(np.isinf(vals[:, 3])) and np.all(np.isfinite(np.delete(vals, 3, axis=1)))
+
+
+# ------------------------------- DeepSeek-V4-Flash geometry (the reference's own)
+V4_H, V4_I, V4_TOPK = 4096, 2048, 6
+
+
+@pytest.fixture(scope="module")
+def v4_zero_layer(eng):
+    import torch
+
+    w13 = torch.zeros(E, 2 * V4_I, V4_H // 2, dtype=torch.uint8, device="cuda")
+    s13 = torch.full((E, 2 * V4_I, V4_H // 32), 127, dtype=torch.uint8, device="cuda")
+    w2 = torch.zeros(E, V4_H, V4_I // 2, dtype=torch.uint8, device="cuda")
+    s2 = torch.full((E, V4_H, V4_I // 32), 127, dtype=torch.uint8, device="cuda")
+    yield w13, s13, w2, s2
+    del w13, s13, w2, s2
+    torch.cuda.empty_cache()
+
+
+def v4_router_inputs(tokens: int):
+    """Router logits ~N(0, 1) and a selection bias that sends most tokens
+    to a few experts (so one layer holds light and multi-tile experts)."""
+    raw = synth.normal(synth.config_seed(6, tokens), tokens * E).astype(np.float32).reshape(tokens, E)
+    bias = (0.05 * synth.normal(synth.config_seed(6, 1), E)).astype(np.float32)
+    bias[[3, 77, 140]] += np.float32(1.5)
+    return raw, bias
+
+
+@pytest.mark.parametrize("tokens", [64, 512])
+def test_v4_flash_mxfp4_layer(eng, v4_zero_layer, tokens):
+    """The reference's production MoE geometry (include/pih/model/
+    deepseek_v4_config.h:22-27: hidden 4096, 256 routed experts, 6 active;
+    expert intermediate 2048): the device V4 router (sqrt-softplus + bias
+    selection, weights x 1.5, learned_router.cpp:21-105) feeds the layer
+    entry with MXFP4 experts and e4m3 activations, at decode batches of 64
+    and 512 tokens.  The router's ids equal the oracle's and its weights
+    agree to rtol 1e-5 (device expf / log1pf / sqrtf against the host's, as
+    in tests/test_gpu_router.py); the chain below takes the device's
+    weights.  Every expert outside a checked set has zero weights, and the
+    layer's output equals the reference's routed-expert chain (clamp 10)
+    over the checked experts, which cover <= 16 rows, 17-64 rows (the
+    streaming kernel, fully unrolled at K = 4096 and 2048) and, at 512
+    tokens, a multi-tile expert."""
+    import torch
+
+    from pih_amd.linear import MoeLayer, router_topk
+
+    H, I = V4_H, V4_I
+    w13, s13, w2, s2 = v4_zero_layer
+    raw, bias = v4_router_inputs(tokens)
+    ids_d, wts_d, rflag = router_topk(to_dev(raw), V4_TOPK, abi.ROUTER_SQRT_SOFTPLUS, 1.5, to_dev(bias))
+    _sync()
+    ids, wts = to_host(ids_d).view(np.uint32), to_host(wts_d)
+    rid, rw = oracle.router_topk(raw, V4_TOPK, oracle.ROUTER_SQRT_SOFTPLUS, 1.5, bias)
+    assert _flag(rflag) == 0
+    np.testing.assert_array_equal(ids, rid)
+    np.testing.assert_allclose(wts, rw, rtol=1e-5, atol=0)
+    x = synth.bf16_normal(synth.config_seed(6, tokens + 1), (tokens, H))
+    o_ref, rt_ref, rw_ref, _ = oracle.route_plan(rid, wts, E)
+    counts = np.diff(o_ref.astype(np.int64))
+    checked = _pick(counts, 1, 16, 3) + _pick(counts, 17, 64, 2) + _pick(counts, 65, 4096, 1)
+    if tokens >= 512:
+        assert any(counts[e] > 64 for e in checked), counts.max()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(6000 + tokens)
+    host = {}
+    for e in checked:
+        w13[e] = torch.randint(0, 256, (2 * I, H // 2), dtype=torch.uint8, device="cuda", generator=gen)
+        s13[e] = torch.randint(118, 125, (2 * I, H // 32), dtype=torch.uint8, device="cuda", generator=gen)
+        w2[e] = torch.randint(0, 256, (H, I // 2), dtype=torch.uint8, device="cuda", generator=gen)
+        s2[e] = torch.randint(118, 125, (H, I // 32), dtype=torch.uint8, device="cuda", generator=gen)
+        host[e] = [to_host(t[e]) for t in (w13, s13, w2, s2)]
+    try:
+        layer = MoeLayer(w13, s13, w2, s2, tokens, V4_TOPK, weight_format=abi.WEIGHT_MXFP4,
+                         activation_type=abi.ACTIVATION_E4M3, swiglu_limit=10.0)
+        got = to_host(layer.forward(to_dev(x), ids_d, wts_d))
+        _sync()
+        assert _flag(layer.flag) == 0
+        y = np.zeros((tokens * V4_TOPK, H), np.uint16)
+        for e in checked:
+            b, en = int(o_ref[e]), int(o_ref[e + 1])
+            w13p, w13s, w2p, w2s = host[e]
+            y[b:en] = oracle.routed_expert_fp4(np.ascontiguousarray(x[rt_ref[b:en]]), rw_ref[b:en], H, I,
+                                               np.ascontiguousarray(w13p[:I]), np.ascontiguousarray(w13s[:I]), w2p,
+                                               w2s, np.ascontiguousarray(w13p[I:]), np.ascontiguousarray(w13s[I:]))
+        ref = oracle.finalize(oracle.ordered_accumulate(y, rt_ref, tokens))
+        touched = np.isin(rid, checked).any(axis=1)
+        assert np.all(oracle.bf16_bits_to_f32(got[~touched]) == 0), "unchecked experts not zero"
+        assert_close(oracle.bf16_bits_to_f32(got), oracle.bf16_bits_to_f32(ref),
+                     f"V4-Flash T={tokens} (experts {[(e, int(counts[e])) for e in checked]})")
+    finally:
+        for e in checked:
+            w13[e].zero_()
+            w2[e].zero_()

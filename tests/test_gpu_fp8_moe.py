@@ -282,9 +282,11 @@ def test_moe_fp8_layer(eng, tokens, experts, topk, hidden, inter, limit):
 
 def test_moe_fp8_layer_full_shape_cold_experts(eng):
     """BASELINE cfg4 geometry (T=4096, E=256, top-8, H=7168, I=2048): the
-    route plan is checked bit-exact in full and the expert rows of the
-    coldest touched experts against the oracle chain (the hot experts hold
-    thousands of rows, too slow for the scalar CPU oracle)."""
+    route plan is checked bit-exact in full, the expert rows of the coldest
+    touched experts against the oracle chain, and 48 sampled rows of each of
+    the two hottest experts (3997 and 3612 rows: the multi-tile path with
+    its 256-row tiles, rows on both sides of tile boundaries and the last
+    partial tile) against the same chain."""
     import torch
 
     from pih_amd.linear import MoeFp8Layer
@@ -324,6 +326,17 @@ def test_moe_fp8_layer_full_shape_cold_experts(eng):
         a, sa, bw, sb = host[e]
         ref = oracle.expert_fp8(np.ascontiguousarray(x[rt_ref[b:en]]), rw_ref[b:en], hidden, inter, a, sa, bw, sb)
         assert_close(oracle.bf16_bits_to_f32(y[b:en]), oracle.bf16_bits_to_f32(ref), f"expert {e} rows")
+    hot = [int(e) for e in np.argsort(-counts, kind="stable")[:2]]
+    for e in hot:
+        b, en = int(o_ref[e]), int(o_ref[e + 1])
+        n = en - b
+        edges = [j for t in range(256, n, 256) for j in (t - 1, t)]
+        pick = np.unique(np.concatenate([[0, 1, n - 2, n - 1], edges[:: max(1, len(edges) // 24)][:30],
+                                         np.linspace(0, n - 1, 14).astype(np.int64)]))[:48]
+        rows = b + pick
+        hw = [t[e].cpu().numpy() for t in (w13, s13, w2, s2)]
+        ref = oracle.expert_fp8(np.ascontiguousarray(x[rt_ref[rows]]), rw_ref[rows], hidden, inter, *hw)
+        assert_close(oracle.bf16_bits_to_f32(y[rows]), oracle.bf16_bits_to_f32(ref), f"hot expert {e} sampled rows")
 
 
 def test_moe_gemm_plain_output_forms_and_bad_segment(eng):

@@ -3,11 +3,13 @@
 The reference's kernels raise bit 2 and skip that scale block
 (`continue` in plugins/kernels/deepseek-v4-sm89/native/deepseek_fp8_gemm.cu:48
 and deepseek_fp4_gemm.cu:53-56): the other operand's scale must not leak
-into the sum.  Each case pairs the 0xFF scale with the largest scale on the
-other operand in the same k block (254, against 0 on the other rows of that
-block, so that every block of the k step contributes at the same scale), so
-a block that were run with the 0xFF replaced by 2^-127 would add as much as
-a valid one.  Expected: the oracle on the same operands with the skipped
+into the sum.  Each case pairs the 0xFF scale with a large scale on the
+other operand in the same k block (228, against 0 on the other rows of that
+block, so that every block of the k step contributes 2^-26 times its sum;
+228 keeps the oracle's left-to-right product local * 2^101 finite), and
+every other block uses scales near 100 (2^-54 times its sum), so a block
+that were run with the 0xFF replaced by 2^-127 would add as much as a
+valid one.  Expected: the oracle on the same operands with the skipped
 block's codes zeroed (and a valid scale in its place).  Cases:
 
 * big-tile kernel (M = 2048, 128 x 256 tiles): a W block scale and an A-row
@@ -53,13 +55,13 @@ def _fp8_case(m, n, k, seed):
     0xFF, and the skip-equivalent operands for the oracle."""
     a = _codes(synth.config_seed(5, seed), (m, k))
     w = _codes(synth.config_seed(5, seed + 1), (n, k))
-    sa = (118 + synth.splitmix64(seed + 2, m * (k // 128)) % np.uint64(6)).astype(np.uint8).reshape(m, k // 128)
-    sw = (112 + synth.splitmix64(seed + 3, (n // 128) * (k // 128)) % np.uint64(6)).astype(np.uint8)
+    sa = (100 + synth.splitmix64(seed + 2, m * (k // 128)) % np.uint64(6)).astype(np.uint8).reshape(m, k // 128)
+    sw = (100 + synth.splitmix64(seed + 3, (n // 128) * (k // 128)) % np.uint64(6)).astype(np.uint8)
     sw = sw.reshape(n // 128, k // 128)
     ff_rows = np.array([1, 17, m // 2 + 3, m - 1])
-    sa[:, 5], sw[:, 5] = 254, 0
+    sa[:, 5], sw[:, 5] = 228, 0
     sw[3, 5] = 0xFF
-    sw[:, 2], sa[:, 2] = 254, 0
+    sw[:, 2], sa[:, 2] = 228, 0
     sa[ff_rows, 2] = 0xFF
     a0, w0, sa0, sw0 = a.copy(), w.copy(), sa.copy(), sw.copy()
     a0[ff_rows, 256:384] = 0
@@ -111,12 +113,14 @@ def test_fp4_ff_scale_skips_the_block(eng):
 
     m, n, k = 512, 2048, 4096
     x = synth.bf16_normal(synth.config_seed(5, 950), (m, k))
-    a, sa = oracle.fp8_quant_ue8m0(oracle.bf16_bits_to_f32(x))
-    packed, sw = synth.mxfp4_weight(synth.config_seed(5, 951), n, k)
+    a, _ = oracle.fp8_quant_ue8m0(oracle.bf16_bits_to_f32(x))
+    packed, _ = synth.mxfp4_weight(synth.config_seed(5, 951), n, k)
+    sa = (100 + synth.splitmix64(952, m * (k // 128)) % np.uint64(6)).astype(np.uint8).reshape(m, k // 128)
+    sw = (100 + synth.splitmix64(953, n * (k // 32)) % np.uint64(6)).astype(np.uint8).reshape(n, k // 32)
     ff_rows = np.array([2, 300])
-    sa[:, 2], sw[:, 8:12] = 254, 0  # 128-k block 2 = 32-k blocks 8..11
+    sa[:, 2], sw[:, 8:12] = 228, 0  # 128-k block 2 = 32-k blocks 8..11
     sw[77, 9] = 0xFF
-    sw[:, 4:8], sa[:, 1] = 254, 0  # 128-k block 1 = 32-k blocks 4..7
+    sw[:, 4:8], sa[:, 1] = 228, 0  # 128-k block 1 = 32-k blocks 4..7
     sa[ff_rows, 1] = 0xFF
     a0, sa0, p0, sw0 = a.copy(), sa.copy(), packed.copy(), sw.copy()
     a0[ff_rows, 128:256] = 0
