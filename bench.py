@@ -599,7 +599,10 @@ def bench_dropin(torch, iters: int):
         out[f"ds_grouped_fp8_t{t}_8x1024x4096"] = _line(ms, wb + ws + t * g * kg * 2 + t * g * ng * 2,
                                                        2.0 * t * g * ng * kg, FP8_PEAK_TFLOPS)
     del buf
-    # ---- Qwen code object, W4A16 compat kernel by name, Qwen3-0.6B shapes
+    # ---- Qwen code object by name through the C++ kernel-module driver,
+    # Qwen3-0.6B shapes, M = 1: the compatibility kernel in the reference's
+    # geometry and the gfx950 plan's kernel (launches prepared once, as a
+    # model's decode loop holds them)
     co = QwenCodeObject()
     for n, k in ((2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072)):
         wb, ws = n * k // 2, (n * k // 128) * 2
@@ -610,11 +613,12 @@ def bench_dropin(torch, iters: int):
         x = torch.randn(1, k, device=dev, generator=gen).to(torch.bfloat16)
         o = torch.empty(1, n, dtype=torch.bfloat16, device=dev)
         s = stream_handle()
-        ms = _timed(torch, lambda i: co.w4a16_gemm(ptr(x), ptr(buf) + (i % nsets) * stride,
-                                                   ptr(buf) + (i % nsets) * stride + wb, ptr(o), ptr(flag), 1, n,
-                                                   k, s), iters)
-        out[f"qwen_compat_w4a16_m1_{k}to{n}"] = _line(ms, wb + ws + k * 2 + n * 2, 2.0 * n * k, 2516.6)
-        del buf
+        for variant, name in ((abi.QWEN_INT4_COMPAT, "qwen_compat"), (abi.QWEN_INT4_GFX950, "qwen_gfx950_plan")):
+            launches = [co.prepare_w4a16(ptr(x), ptr(buf) + j * stride, ptr(buf) + j * stride + wb, ptr(o), ptr(flag),
+                                         1, n, k, s, variant) for j in range(nsets)]
+            ms = _timed(torch, lambda i: launches[i % nsets](), iters)
+            out[f"{name}_w4a16_m1_{k}to{n}"] = _line(ms, wb + ws + k * 2 + n * 2, 2.0 * n * k, 2516.6)
+        del buf, launches
     # ---- configs[0] MLP block (BF16 GemmPlan x3 + SiLU-mul), M = 16
     per = 3 * 3072 * 1024 * 2
     nsets = max(2, -(-600_000_000 // per))

@@ -262,6 +262,59 @@ LN_API = _struct("AmdLinearKernelsApi", [("struct_size", U32), ("contract_versio
 QWEN_API = _struct("QwenKernelsApi", [("struct_size", U32), ("contract_version", U32), ("target_sm", U32),
                                       ("root", C.CFUNCTYPE(Status, C.POINTER(C.c_char_p)))])
 
+# kernel-module driver and Qwen W4A16 plan (include/pih/backend/hip/
+# kernel_module_v1.h, include/pih/contracts/qwen_int4_plan_gfx950_v1.h),
+# libpih_hip_kernel_module.so
+KERNEL_MODULE_LIB = os.path.join(LIB_DIR, "libpih_hip_kernel_module.so")
+WIRE_U64, WIRE_DEVICE_POINTER_U64 = 3, 10
+KM_PARAMETER = _struct("HipKernelParameter", [("wire_type", U32), ("offset", U32)])
+KM_SIGNATURE = _struct("HipKernelSignature", [("struct_size", U32), ("abi_version", U32), ("symbol", C.c_char_p),
+                                              ("logical_id", C.c_char_p), ("code_object_sha256", C.c_char_p),
+                                              ("parameter_abi_sha256", C.c_char_p),
+                                              ("parameters", C.POINTER(KM_PARAMETER)), ("parameter_count", U32),
+                                              ("total_parameter_bytes", U32)])
+KM_GEOMETRY = _struct("HipLaunchGeometry", [("struct_size", U32), ("grid_x", U32), ("grid_y", U32), ("grid_z", U32),
+                                            ("block_x", U32), ("block_y", U32), ("block_z", U32),
+                                            ("dynamic_shared_bytes", U32)])
+KM_ARGUMENTS = _struct("HipKernelArguments", [("struct_size", U32), ("abi_version", U32), ("logical_id", C.c_char_p),
+                                              ("parameter_abi_sha256", C.c_char_p), ("packet", C.c_void_p),
+                                              ("packet_bytes", U32)])
+QWEN_INT4_COMPAT, QWEN_INT4_GFX950 = 1, 2
+QWEN_INT4_PLAN = _struct("QwenInt4GemmPlan", [("struct_size", U32), ("abi_version", U32), ("variant", U32),
+                                              ("reserved", U32), ("kernel_symbol", C.c_char_p),
+                                              ("logical_id", C.c_char_p), ("parameter_abi_sha256", C.c_char_p),
+                                              ("geometry", KM_GEOMETRY), ("tokens", U64), ("output_features", U64),
+                                              ("input_features", U64), ("input_bytes", U64), ("packed_bytes", U64),
+                                              ("scale_bytes", U64), ("output_bytes", U64)])
+
+_kernel_module = None
+
+
+def kernel_module_lib() -> C.CDLL:
+    """libpih_hip_kernel_module.so with its seven entries typed."""
+    global _kernel_module
+    if _kernel_module is None:
+        if not os.path.exists(KERNEL_MODULE_LIB):
+            raise PackError(f"kernel-module driver not built: {KERNEL_MODULE_LIB}")
+        L = C.CDLL(KERNEL_MODULE_LIB)
+        P = C.c_void_p
+        sigs = {
+            "pih_hip_code_object_verify_v1": [C.c_char_p, C.POINTER(KM_SIGNATURE), U32],
+            "pih_hip_kernel_module_load_v1": [C.c_char_p, C.POINTER(KM_SIGNATURE), U32, C.POINTER(P)],
+            "pih_hip_kernel_module_find_v1": [P, C.c_char_p, C.POINTER(U32)],
+            "pih_hip_kernel_submit_v1": [P, U32, C.POINTER(KM_GEOMETRY), UPTR, C.POINTER(KM_ARGUMENTS)],
+            "pih_hip_kernel_module_unload_v1": [P],
+            "pih_qwen_int4_gemm_plan_create_v1": [U64, U64, U64, U32, C.POINTER(QWEN_INT4_PLAN)],
+            "pih_qwen_int4_gemm_signature_v1": [U32, C.c_char_p, C.POINTER(KM_PARAMETER), C.POINTER(KM_SIGNATURE)],
+        }
+        for name, args in sigs.items():
+            fn = getattr(L, name)
+            fn.restype = Status
+            fn.argtypes = args
+        _kernel_module = L
+    return _kernel_module
+
+
 SCALE_F32, SCALE_UE8M0 = 1, 2
 OUTPUT_BF16, OUTPUT_F32, OUTPUT_SWIGLU_BF16, OUTPUT_SWIGLU_E4M3 = 1, 2, 3, 4
 ACTIVATION_E4M3, ACTIVATION_BF16 = 1, 2

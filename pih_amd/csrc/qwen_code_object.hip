@@ -255,6 +255,102 @@ extern "C" __global__ __launch_bounds__(256) void pih_qwen_w4a16_gemm_compat_v1(
   }
 }
 
+// pih_qwen_w4a16_gemm_gfx950_v1: the same operation, packet and error codes
+// in the launch geometry the gfx950 plan chooses (pih_qwen_int4_gemm_plan_
+// create_v1, replacing qwen3_int4_gemm_plan.cpp:44-63 at the model's call
+// site): grid (n / 16, ceil(m / 16)), 64 * waves threads (1..16 waves).
+// Block (bx, by) computes x rows 16 by .. 16 by + 15 (rows past m read row
+// m - 1 and are not stored) against W rows 16 bx .. 16 bx + 15; wave w
+// takes the 128-deep groups [w G / waves, (w + 1) G / waves) with its next
+// group's loads in flight, and the waves' partial tiles meet in LDS in wave
+// order.  n % 16, k % 128, m <= 4096 and the geometry are checked; a
+// mismatch publishes 11.
+extern "C" __global__ __launch_bounds__(1024) void pih_qwen_w4a16_gemm_gfx950_v1(
+    const uint16_t* input, const uint8_t* packed_weight, const uint16_t* scales, uint16_t* output,
+    uint32_t* error_flag, uint64_t m, uint64_t n, uint64_t k) {
+  const uint32_t waves = blockDim.x / 64u;
+  if (error_flag == nullptr || input == nullptr || packed_weight == nullptr || scales == nullptr ||
+      output == nullptr || m == 0 || m > 4096 || n == 0 || (n & 15u) != 0 || k == 0 || (k & 127u) != 0 ||
+      blockDim.x % 64u != 0 || waves == 0 || waves > 16 || blockDim.y != 1 || blockDim.z != 1 ||
+      gridDim.x != n / 16u || gridDim.y != (m + 15u) / 16u || gridDim.z != 1) {
+    if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0) publish(error_flag, kErrLaunch);
+    return;
+  }
+  __shared__ float s_acc[16][4][64];
+  __shared__ uint32_t s_bad[16][16];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t lr = lane & 15, lg = lane >> 4;
+  const uint64_t kb = k / 2u, groups = k / 128u;
+  const uint64_t xr0 = (uint64_t)blockIdx.y * 16u, wr0 = (uint64_t)blockIdx.x * 16u;
+  const uint64_t xrow_i = xr0 + lr < m ? xr0 + lr : m - 1;
+  const uint16_t* xrow = input + xrow_i * k + lg * 32u;
+  const uint8_t* wrow = packed_weight + (wr0 + lr) * kb + lg * 16u;
+  const uint16_t* srow = scales + (wr0 + lr) * groups;
+  const uint64_t g0 = wave * groups / waves, g1 = (wave + 1) * groups / waves;
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  uint32_t bad_nib = 0, bad_scale = 0;
+  // two groups of loads in flight (a decode wave has one or two groups)
+  const v4i z4 = v4i{0, 0, 0, 0};
+  v4i wn[2] = {z4, z4}, xn[2][4] = {{z4, z4, z4, z4}, {z4, z4, z4, z4}};
+  uint32_t sn[2] = {0, 0};
+  auto load = [&](int b, uint64_t g) {
+    wn[b] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wrow + g * 64u));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xn[b][j] = *reinterpret_cast<const v4i*>(xrow + g * 128u + j * 8u);
+    sn[b] = srow[g];
+  };
+  if (g0 < g1) load(0, g0);
+  if (g0 + 1 < g1) load(1, g0 + 1);
+  for (uint64_t g = g0; g < g1; ++g) {
+    const int b = (int)((g - g0) & 1u);
+    const v4i w = b ? wn[1] : wn[0];
+    v4i x[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = b ? xn[1][j] : xn[0][j];
+    const float s = f16_to_f32(b ? sn[1] : sn[0]);
+    if (g + 2 < g1) {
+      if (b) load(1, g + 2);
+      else load(0, g + 2);
+    }
+    // the group's x sum of A row lr, then of the rows 4lg + t this lane
+    // holds results for
+    float part = sum8(x[0]) + sum8(x[1]) + sum8(x[2]) + sum8(x[3]);
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    v4f xs;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xs[t] = __shfl(part, (int)(4u * lg + t), 64);
+    group_mma(w, x, xs, s, acc, bad_nib, bad_scale);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) s_acc[wave][t][lane] = acc[t];
+  const uint32_t flags = (bad_nib ? 1u : 0u) | (bad_scale ? 2u : 0u);
+  if (lg == 0) s_bad[wave][lr] = 0;
+  __syncthreads();
+  if (flags) atomicOr(&s_bad[wave][lr], flags);
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t rf = 0;
+    for (uint32_t w = 0; w < waves; ++w) rf |= s_bad[w][lr];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint64_t row = xr0 + 4u * lg + t;
+      float y = s_acc[0][t][lane];
+      for (uint32_t w = 1; w < waves; ++w) y += s_acc[w][t][lane];
+      if (row >= m) continue;
+      uint32_t code = 0;
+      if (rf & 1u) code = kErrReservedNibble;
+      else if (rf & 2u) code = kErrScale;
+      else if (!__builtin_isfinite(y)) code = kErrNonFinite;
+      if (code) {
+        publish(error_flag, code);
+        continue;
+      }
+      output[row * n + wr0 + lr] = (uint16_t)f32_to_bf16(y);
+    }
+  }
+}
+
 extern "C" __global__ __launch_bounds__(256) void pih_qwen_silu_mul_bf16_v1(const uint16_t* gate, const uint16_t* up,
                                                                           uint16_t* output, uint64_t elements) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;

@@ -29,6 +29,7 @@ LN_C["w4a16"] = "pih_amd_w4a16_launch_v1"
 def _layout_program():
     lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "pih/contracts/deepseek_kernels_v1.h"',
              '#include "pih/contracts/amd_linear_kernels_v1.h"', '#include "pih/contracts/qwen_kernels_v1.h"',
+             '#include "pih/backend/hip/kernel_module_v1.h"', '#include "pih/contracts/qwen_int4_plan_gfx950_v1.h"',
              "int main(void) {", 'printf("{");']
     first = True
 
@@ -52,6 +53,12 @@ def _layout_program():
     emit("ln_api", "pih_amd_linear_kernels_api_v1", [f[0] for f in abi.LN_API._fields_])
     emit("qwen_api", "pih_qwen_kernels_api_v1", [f[0] for f in abi.QWEN_API._fields_])
     emit("w4a16_problem", "pih_amd_w4a16_problem_v1", [f[0] for f in abi.W4A16_PROBLEM._fields_])
+    for key, ctype, t in (("km_parameter", "pih_hip_kernel_parameter_v1", abi.KM_PARAMETER),
+                          ("km_signature", "pih_hip_kernel_signature_v1", abi.KM_SIGNATURE),
+                          ("km_geometry", "pih_hip_launch_geometry_v1", abi.KM_GEOMETRY),
+                          ("km_arguments", "pih_hip_kernel_arguments_v1", abi.KM_ARGUMENTS),
+                          ("qwen_int4_plan", "pih_qwen_int4_gemm_plan_v1", abi.QWEN_INT4_PLAN)):
+        emit(key, ctype, [f[0] for f in t._fields_])
     lines += ['printf("}\\n");', "return 0; }"]
     return "\n".join(lines)
 
@@ -72,7 +79,9 @@ def test_c_struct_layouts_match_ctypes_mirror():
     want.update({"ln." + n: mirror(t) for n, t in abi.LN.items()})
     want.update(status=mirror(abi.Status), identity=mirror(abi.Identity), api=mirror(abi.PackApi),
                 ds_api=mirror(abi.DS_API), ln_api=mirror(abi.LN_API), qwen_api=mirror(abi.QWEN_API),
-                w4a16_problem=mirror(abi.W4A16_PROBLEM))
+                w4a16_problem=mirror(abi.W4A16_PROBLEM), km_parameter=mirror(abi.KM_PARAMETER),
+                km_signature=mirror(abi.KM_SIGNATURE), km_geometry=mirror(abi.KM_GEOMETRY),
+                km_arguments=mirror(abi.KM_ARGUMENTS), qwen_int4_plan=mirror(abi.QWEN_INT4_PLAN))
     assert got == want
     assert got["status"][0] == 268
     assert len(abi.DS_ORDER) == 29
