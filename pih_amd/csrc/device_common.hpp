@@ -22,6 +22,38 @@ __device__ __forceinline__ uint4 load16_nt(const uint4* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// LDS byte address of a __shared__ object (wave-uniform)
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+
+// Global -> LDS DMA of 16 (dma16) or 4 (dma4) bytes per lane: lane l's data
+// lands at LDS byte lds + 16 l (resp. 4 l); lds is wave-uniform and goes to
+// M0.  Issued as inline asm so that the compiler, which cannot tell which
+// LDS bytes a DMA writes, adds no conservative vmcnt waits before LDS reads;
+// the kernel orders the waits itself (an explicit s_waitcnt vmcnt, or a
+// compiler wait for a load issued after the DMA: loads complete in issue
+// order, and the compiler's count, which omits the DMA, only waits longer).
+// M0 is written here only; nothing else in these kernels uses it.
+// The address is a wave-uniform base (SGPRs) plus a per-lane 32-bit offset,
+// or (dma4v) a per-lane 64-bit address.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off), "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void dma16nt(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt" ::"s"(lds), "v"(off), "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds), "v"(off), "s"(base)
+               : "memory");
+}
+__device__ __forceinline__ void dma4v(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds), "v"(src) : "memory");
+}
+
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));

@@ -17,7 +17,8 @@
 // that (the 128-row tiles of gemm_mfma.hip spend most of their loads on
 // dead activation rows when an expert has a few rows):
 //   * a block of 4 waves owns 128 W rows of one light expert (<= 64 rows)
-//     and up to 64 (e4m3) or 32 (bf16) of its rows; each wave owns 32
+//     and up to 32 of its rows (an expert with 33-64 rows is two items);
+//     each wave owns 32
 //     W rows (two 16-row MFMA fragments) and loads them into registers,
 //     non-temporal, 3-4 steps of 256 k ahead, as whole 128-byte lines (8
 //     rows x 128 B per instruction, four per step: the MFMA operand layout,
@@ -34,6 +35,11 @@
 //     ahead together with the weights -- every vector load shares one
 //     in-order completion counter, so a younger activation load would make
 //     its wait cover every older weight load too;
+//   * block scales (unrolled K loops) come 4 steps at a time through LDS:
+//     one global->LDS DMA per wave carries its 32 rows x 32 B of weight
+//     scales, one of wave 0 the 32 activation rows x 8 B (e4m3).  Loaded
+//     per step, 8 bytes of 16 rows per instruction, they touched as many
+//     cache lines as the weights themselves (t64 gate/up 178 -> 157 us);
 //   * the output is computed transposed (C^T = W . A^T): a lane owns 4
 //     consecutive output columns of one row; for the SwiGLU epilogue a
 //     wave's fragment 0 holds 16 gate rows and fragment 1 the 16 matching
@@ -55,8 +61,11 @@ constexpr uint32_t kWPitch = 144;  // W tile row: one 128-byte step + pad
 
 template <int ACT>
 struct Act {
-  // rows per pass (a light expert with more rows is done in row chunks)
-  static constexpr uint32_t MAXR = ACT == kActBf16 ? 32 : kMoeLightRows;
+  // rows per pass: a light expert with more rows is done in row chunks
+  // (adjacent items, so the second pass over the weights meets them in the
+  // caches).  32 keeps the unrolled e4m3 loops at 3 blocks per CU (<= 168
+  // registers, ~42 KB of LDS); 64 would hold them at 2.
+  static constexpr uint32_t MAXR = 32;
   static constexpr uint32_t ROW = ACT == kActBf16 ? 512 : 256;  // activation bytes per row and step
   static constexpr uint32_t CHUNKS = MAXR * ROW / 16 / NTH;     // 16-byte chunks per thread and step
   static constexpr uint32_t RPI = NTH * 16 / ROW;               // rows per staging instruction
@@ -174,6 +183,7 @@ template <int ACT, int OUT, int KBT>
 __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) {
   using C = Act<ACT>;
   constexpr uint32_t MAXR = C::MAXR, ROW = C::ROW, CH = C::CHUNKS, NA = MAXR / 16;
+  static_assert(NA == 2, "two 16-row activation fragments per chunk");
   // steps in flight per wave: 3 with an unrolled K loop (the ring then fits
   // the 256 registers of two waves per SIMD), 4 in the generic loop (whose
   // 8-step body needs a depth dividing 8)
@@ -187,8 +197,17 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   __shared__ __align__(16) uint8_t sA[2][MAXR * ROW];
   __shared__ __align__(16) uint32_t sSa[2][MAXR];  // e4m3: the row's 2 scale bytes of the step
   __shared__ __align__(16) uint8_t sW[NTH / 64][32 * kWPitch];  // per wave: its 32 W rows of one step
+  // weight scales, unrolled K loops: per wave two buffers of [32 rows][32 B]
+  // (4 steps each), filled by one global->LDS DMA per 4 steps
+  constexpr bool kScaleDma = KBT > 0 && KBT % 4 == 0;
+  __shared__ __align__(16) uint8_t sWs[kScaleDma ? NTH / 64 : 1][2][32 * 32];
+  // e4m3 activation scales of the same 4 steps, [MAXR rows][8 B], two
+  // buffers filled by wave 0 (one 4-byte DMA per lane: row lane / 2)
+  constexpr bool kActScaleDma = kScaleDma && ACT == kActE4m3;
+  __shared__ __align__(16) uint8_t sSaC[kActScaleDma ? 2 : 1][kActScaleDma ? MAXR * 8 : 4];
+  static_assert(!kActScaleDma || MAXR * 2 == 64, "one activation-scale DMA covers the chunk");
 
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t lr = lane & 15, lg = lane >> 4;
 
   uint32_t expert, row0, rows, wb;
@@ -246,6 +265,14 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   const uint32_t w_off = w_row(0, lane >> 3) * (K / 2) + (lane & 7) * 16;
   const uint32_t ws_off = w_row(0, lr) * (K / 32);
   const uint32_t ws_d1 = frag_rows * (K / 32);
+  // scale DMA: lane q carries 16 bytes of tile row q / 2 (fragment q / 32)
+  const uint32_t sq_row = lane >> 1;
+  const uint32_t ws_dma = w_row(sq_row >> 4, sq_row & 15) * (K / 32) + 16 * (lane & 1);
+  const uint32_t ws_lds0 = kScaleDma ? lds_addr(&sWs[kScaleDma ? wave : 0][0][0]) : 0u;
+  // activation scale DMA: lane q carries the 4 bytes [4 (q & 1), +4) of row
+  // q / 2's 8 bytes of the chunk (K / 128 is a multiple of 4 when KBT is)
+  const uint32_t sa_dma = kActScaleDma ? a_source(lane >> 1) * (K / 128) + 4 * (lane & 1) : 0u;
+  const uint32_t sa_lds0 = kActScaleDma ? lds_addr(&sSaC[0][0]) : 0u;
   uint8_t* wtile = sW[wave];
 
   v4i rl[kDepth][4];     // weight lines of the step (tile rows 8i .. 8i + 7)
@@ -254,15 +281,26 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
   uint32_t rsa[kDepth];  // activation scales (e4m3)
   auto load = [&](int slot, uint32_t kb) __attribute__((always_inline)) {
     const uint32_t kc = min(kb, last);
+    if constexpr (kScaleDma) {
+      // chunk kb / 4 into buffer (kb / 4) & 1, ahead of the step's own loads
+      // (so the wait for them covers it; the compiler does not count it)
+      if (kb % 4 == 0 && kb < KBT) dma16(ws_base + 8 * kb, ws_dma, ws_lds0 + ((kb / 4) & 1) * 1024);
+    }
+    if constexpr (kActScaleDma) {
+      if (kb % 4 == 0 && kb < KBT && wave == 0)
+        dma4(p.a_scale + 2 * kb, sa_dma, sa_lds0 + ((kb / 4) & 1) * (MAXR * 8));
+    }
     const uint8_t* wb8 = w_base + (uint64_t)kc * 128;
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
       const uint8_t* line = wb8 + (uint64_t)((i & 1) * 8 + (i >> 1) * frag_rows) * (K / 2);  // wave-uniform
       rl[slot][i] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(line + w_off));
     }
-    const uint8_t* sb8 = ws_base + (uint64_t)kc * 8;
-    rws[slot][0] = *reinterpret_cast<const uint2*>(sb8 + ws_off);
-    rws[slot][1] = *reinterpret_cast<const uint2*>(sb8 + ws_d1 + ws_off);
+    if constexpr (!kScaleDma) {
+      const uint8_t* sb8 = ws_base + (uint64_t)kc * 8;
+      rws[slot][0] = *reinterpret_cast<const uint2*>(sb8 + ws_off);
+      rws[slot][1] = *reinterpret_cast<const uint2*>(sb8 + ws_d1 + ws_off);
+    }
     // only the staging instructions that cover live rows (the tile rows past
     // the expert's are never stored; their LDS contents are left stale)
     const uint8_t* ab = static_cast<const uint8_t*>(p.a) + (uint64_t)kc * ROW;
@@ -272,7 +310,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
       if (i == 0 || i * RPI < rows) v = *reinterpret_cast<const v4i*>(ab + a_off[i]);
       ra[slot][i] = v;
     }
-    if constexpr (ACT == kActE4m3) {
+    if constexpr (ACT == kActE4m3 && !kActScaleDma) {
       // the 2 scale bytes of the step, from the aligned 32-bit word that
       // holds them (s_off + 2 kc is even): a full-register load, so the
       // compiler cannot pack it into a half register whose wait would then
@@ -285,7 +323,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
 #pragma unroll
     for (uint32_t i = 0; i < CH; ++i)
       if (i == 0 || i * RPI < rows) *reinterpret_cast<v4i*>(&sA[buf][a_st[i]]) = ra[slot][i];
-    if constexpr (ACT == kActE4m3) {
+    if constexpr (ACT == kActE4m3 && !kActScaleDma) {
       if (tid < MAXR) {
         const uint32_t v = rsa[slot] & 0xffffu;
         sSa[buf][tid] = v;
@@ -300,7 +338,14 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
 #pragma unroll
     for (uint32_t r = 0; r < NA; ++r) acc[f][r] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int slot, int buf) __attribute__((always_inline)) {
+  auto compute = [&](int slot, int buf, uint32_t kb) __attribute__((always_inline)) {
+    if constexpr (kScaleDma) {
+      // this step's 8 scale bytes of rows f*16 + lr (the DMA completed before
+      // the step's own loads did, which the staging above waited for)
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+        rws[slot][f] = *reinterpret_cast<const uint2*>(&sWs[wave][(kb / 4) & 1][(f * 16 + lr) * 32 + 8 * (kb % 4)]);
+    }
 #pragma unroll
     for (int f = 0; f < 2; ++f)
       if (ff_bytes(rws[slot][f].x) | ff_bytes(rws[slot][f].y)) bad |= kErrScale;
@@ -325,7 +370,14 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
           const uint32_t c0 = 8 * s + lg, c1 = c0 + 4;
           const v8i af = cat8(*reinterpret_cast<const v4i*>(pa + ((c0 ^ lr) << 4)),
                               *reinterpret_cast<const v4i*>(pa + ((c1 ^ lr) << 4)));
-          const int sa = (int)((sSa[buf][row] >> (8 * s)) & 0xffu);
+          int sa;
+          if constexpr (kActScaleDma) {
+            // rows past the chunk's hold row 0's scales (a_source)
+            sa = sSaC[(kb / 4) & 1][row * 8 + 2 * (kb % 4) + s];
+            if (sa == 0xff) bad |= kErrScale;
+          } else {
+            sa = (int)((sSa[buf][row] >> (8 * s)) & 0xffu);
+          }
 #pragma unroll
           for (int f = 0; f < 2; ++f) {
             const v4i w4 = wfrag(f, s);
@@ -342,8 +394,6 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
       frag(std::integral_constant<int, 0>{});
       if (!kLiveSplit || na_live > 1) {
         frag(std::integral_constant<int, 1>{});
-        frag(std::integral_constant<int, 2>{});
-        frag(std::integral_constant<int, 3>{});
       }
     } else {
       // bf16: MFMA j of sub-step s multiplies k 32lg + 8j .. +7 of the
@@ -407,7 +457,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
     for (int j = 0; j < KBT; ++j) {
       stage(j % kDepth, j & 1);
       __syncthreads();
-      compute(j % kDepth, j & 1);
+      compute(j % kDepth, j & 1, j);
       // keep the next loads after this step's compute (hoisting them would
       // keep two steps' operands live)
       __builtin_amdgcn_sched_barrier(0);
@@ -421,7 +471,7 @@ __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) 
     if ((TAIL) && j >= KB) goto done; \
     stage((J) % kDepth, (J) & 1);     \
     __syncthreads();                  \
-    compute((J) % kDepth, (J) & 1);   \
+    compute((J) % kDepth, (J) & 1, j); \
     load((J) % kDepth, j + kDepth);   \
   }
     uint32_t kb = 0;
