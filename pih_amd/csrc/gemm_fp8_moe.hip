@@ -55,9 +55,9 @@ constexpr uint32_t STAGE = A_BYTES + W_BYTES + SA_BYTES + SW_BYTES, DUMMY_BYTES 
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
 // [6:4], lgkmcnt [11:8]; an all-ones field does not wait)
 constexpr int kWaitVm7 = 0x0F77;     // vmcnt(7)
-constexpr int kWaitVm6 = 0x0F76;     // vmcnt(6)
-// operand kinds: e4m3 with block scales, or bf16 (no scales)
-enum : int { kOpFp8 = 0, kOpBf16 = 1 };
+// operand kinds: e4m3 with block scales, bf16 (no scales), or e4m3 A
+// against MXFP4 W (e2m1 two per byte, UE8M0 per W row and 32 k)
+enum : int { kOpFp8 = 0, kOpBf16 = 1, kOpFp4 = 2 };
 constexpr int kWaitVm0 = 0x0F70;     // vmcnt(0)
 constexpr uint32_t kCodePitch = 144;  // staged e4m3 code rows (128 bytes + 16)
 // s_waitcnt immediate waiting for vmcnt <= n (n < 64; bits [3:0] and [15:14])
@@ -100,6 +100,9 @@ struct MoeParams {
   uint32_t stage_out;        // output rows 16-byte aligned: stores staged in LDS
   const uint32_t* skip_if;   // every block exits at once if (*skip_if & skip_bit)
   uint32_t skip_bit;
+  // MoE: experts with at most this many rows are left out (another kernel
+  // takes them); 0 takes every expert
+  uint32_t light_rows;
   uint64_t out_row_stride;
   uint32_t n_tiles;
   uint32_t vb_end;  // blocks of the one-block-per-tile grid; persistent blocks walk no further
@@ -140,7 +143,7 @@ __device__ bool moe_tile(const MoeParams& p, uint32_t vb, uint32_t& expert, uint
   const uint32_t per_t = (E + NTH - 1) / NTH;
   auto m_tiles = [&](uint32_t e) -> uint32_t {
     const uint32_t lo = p.offsets[e], hi = p.offsets[e + 1];
-    return hi > lo ? (hi - lo + BM - 1) / BM : 0u;
+    return hi > lo && hi - lo > p.light_rows ? (hi - lo + BM - 1) / BM : 0u;
   };
   uint32_t cnt_h = 0, cnt_s = 0;  // this thread's multi-tile M tiles / streaming experts
   for (uint32_t j = 0; j < per_t; ++j) {
@@ -286,7 +289,7 @@ __device__ __forceinline__ void moe_table_build(const MoeParams& p, const MoeTab
   const uint32_t per_t = (E + NTH - 1) / NTH;
   auto m_tiles = [&](uint32_t e) -> uint32_t {
     const uint32_t lo = t.off[e], hi = t.off[e + 1];
-    return hi > lo ? (hi - lo + BM - 1) / BM : 0u;
+    return hi > lo && hi - lo > p.light_rows ? (hi - lo + BM - 1) / BM : 0u;
   };
   uint32_t cnt_h = 0, cnt_s = 0;
   for (uint32_t j = 0; j < per_t; ++j) {
@@ -383,8 +386,19 @@ __device__ bool moe_table_tile(const MoeParams& p, const MoeTable& t, uint32_t v
 
 template <int OP, int SCALE, int OUT, bool PERSIST>
 __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
-  // Stage s at smem + s * STAGE: A tile, W tile, A-row scales, W scales.
+  // Stage s at smem + s * STG: A tile, W tile, A-row scales, W scales.
+  // (FP4 W: 64-byte tile rows and 4 scale bytes per W row; the array keeps
+  // the FP8 size, which the staged epilogue also needs.)
   __shared__ __align__(16) uint8_t smem[STAGES * STAGE + DUMMY_BYTES];
+  constexpr bool kF4 = OP == kOpFp4;
+  constexpr uint32_t W_ROW = kF4 ? 64 : LDS_ROW, WB = BN * W_ROW, SWB = kF4 ? BN * 4 : SW_BYTES;
+  constexpr uint32_t STG = A_BYTES + WB + SA_BYTES + SWB;
+  static_assert(STG <= STAGE, "stage layout");
+  // LDS stages: 4 for FP4 W outside persistent launches (its stage is
+  // 33.5 KB: the loads run three steps ahead), 3 otherwise; the scratch
+  // word of the dummy scale loads follows the last stage
+  constexpr uint32_t NS = kF4 && !PERSIST ? 4 : 3;
+  static_assert(NS * STG + DUMMY_BYTES <= sizeof(smem), "stages fit");
   const uint32_t lds0 = lds_addr(smem);
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -396,9 +410,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // the masked bit is not changed while this kernel runs: one value for every thread
   if (p.skip_if && (__hip_atomic_load(p.skip_if, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & p.skip_bit)) return;
 
-  // a K step is 128 bytes of a row: 128 e4m3 or 64 bf16 values
+  // a K step is 128 bytes of an A row: 128 e4m3 or 64 bf16 values (and
+  // 64 bytes of an FP4 W row)
   constexpr bool kBf = OP == kOpBf16;
-  const uint32_t K = p.k, RB = kBf ? 2 * K : K, KB = RB / 128;
+  const uint32_t K = p.k, RB = kBf ? 2 * K : K, KB = RB / 128, RBW = kF4 ? K / 2 : RB;
   uint32_t bad = 0;
 
   [[maybe_unused]] MoeTable tab{};
@@ -478,7 +493,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // A: a_rows_total rows and W: n rows per expert stay below 2^32 bytes,
   // which the launcher checks
   auto make_ops = [&](uint32_t e, uint32_t r0, uint32_t rs, uint32_t t, Ops& o) __attribute__((always_inline)) {
-    o.w_base = p.w + (uint64_t)e * p.n * RB;
+    o.w_base = p.w + (uint64_t)e * p.n * RBW;
     // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
     uint32_t wblk0, wblk1;
     if constexpr (kSwi) {
@@ -495,13 +510,36 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       const uint32_t R = 16 * wv + 8 * i + lrow;
       o.a_off[i] = (uint32_t)(a_source(R, e, r0, rs) * RB) + ((lslot ^ ((R >> 1) & 7u)) << 4);
     }
+    if constexpr (kF4) {
+      // 64-byte rows: instruction i lands rows 32 wv + 16 i + (l >> 2), slot
+      // l & 3, which holds chunk (l & 3) ^ ((row >> 2) & 3)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t R = 32 * wv + 8 * i + lrow;
-      o.w_off[i] = w_row(R, t) * RB + ((lslot ^ ((R >> 1) & 7u)) << 4);
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t R = 32 * wv + 16 * i + (lane >> 2);
+        o.w_off[i] = w_row(R, t) * RBW + (((lane & 3u) ^ ((R >> 2) & 3u)) << 4);
+      }
+      o.w_off[2] = o.w_off[3] = 0;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t R = 32 * wv + 8 * i + lrow;
+        o.w_off[i] = w_row(R, t) * RB + ((lslot ^ ((R >> 1) & 7u)) << 4);
+      }
     }
     o.s_src = nullptr;
-    if constexpr (!kBf) {
+    if constexpr (kF4) {
+      // waves 0, 1: A-row scales as for FP8; waves 2..5: the 4 scale bytes
+      // of W tile row 64 (w - 2) + l per step; waves 6, 7: a dummy word
+      if (wv < 2) {
+        const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2), e, r0, rs);
+        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB;
+      } else if (wv < 6) {
+        const uint32_t R = 64 * (wv - 2) + lane;
+        o.s_src = static_cast<const uint8_t*>(p.w_scale) + ((uint64_t)e * p.n + w_row(R, t)) * (K / 32);
+      } else {
+        o.s_src = static_cast<const uint8_t*>(p.a_scale);
+      }
+    } else if constexpr (!kBf) {
       if (wv < 2) {
         const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2), e, r0, rs);
         o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB * ESZ;
@@ -511,26 +549,30 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
   };
   uint32_t s_lds = 0;
-  if constexpr (!kBf) s_lds = wv < 2 ? A_BYTES + W_BYTES + 256 * wv : A_BYTES + W_BYTES + SA_BYTES;
+  if constexpr (kF4) s_lds = wv < 2 ? A_BYTES + WB + 256 * wv : A_BYTES + WB + SA_BYTES + 256 * (wv - 2);
+  else if constexpr (!kBf) s_lds = wv < 2 ? A_BYTES + W_BYTES + 256 * wv : A_BYTES + W_BYTES + SA_BYTES;
   s_lds = __builtin_amdgcn_readfirstlane(s_lds);
-  const bool s_scratch = wv > 2;
-  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(wv * 2048), w_lds = __builtin_amdgcn_readfirstlane(A_BYTES + wv * 4096);
+  const bool s_scratch = kF4 ? wv >= 6 : wv > 2;
+  // per-step advance of the scale source: 4 bytes for FP4 W-scale rows
+  const uint32_t s_step = kF4 && wv >= 2 && wv < 6 ? 4u : ESZ;
+  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(wv * 2048),
+                 w_lds = __builtin_amdgcn_readfirstlane(A_BYTES + wv * (32 * W_ROW));
   auto issue = [&](uint32_t stage, uint32_t kb, const Ops& o, auto NT) __attribute__((always_inline)) {
-    const uint32_t base = lds0 + stage * STAGE;
+    const uint32_t base = lds0 + stage * STG;
     const uint8_t* ab = uniform_ptr(p.a + (uint64_t)kb * 128);
-    const uint8_t* wb = uniform_ptr(o.w_base + (uint64_t)kb * 128);
+    const uint8_t* wb = uniform_ptr(o.w_base + (uint64_t)kb * W_ROW);
 #pragma unroll
     for (int i = 0; i < 2; ++i) dma16(ab, o.a_off[i], base + a_lds + i * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < (kF4 ? 2 : 4); ++i) {
       if constexpr (decltype(NT)::value) dma16nt(wb, o.w_off[i], base + w_lds + i * 1024);
       else dma16(wb, o.w_off[i], base + w_lds + i * 1024);
     }
     // scales: a per-lane pointer (UE8M0 bytes come in their aligned dword)
     if constexpr (!kBf) {
-      uintptr_t sp = reinterpret_cast<uintptr_t>(o.s_src) + (uint64_t)kb * ESZ;
+      uintptr_t sp = reinterpret_cast<uintptr_t>(o.s_src) + (uint64_t)kb * s_step;
       if constexpr (ESZ == 1) sp &= ~uintptr_t(3);
-      dma4v(reinterpret_cast<const void*>(sp), s_scratch ? lds0 + STAGES * STAGE : base + s_lds);
+      dma4v(reinterpret_cast<const void*>(sp), s_scratch ? lds0 + NS * STG : base + s_lds);
     }
   };
 
@@ -539,13 +581,14 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   const uint32_t last = KB - 1;
   issue(0, 0, cur, std::false_type{});
   issue(1, min(1u, last), cur, std::false_type{});
+  if constexpr (NS == 4) issue(2, min(2u, last), cur, std::false_type{});
   // Persistent blocks: the epilogue's kStoreOps stores of one tile follow
   // the next tile's first two steps' loads, so those two steps wait with
   // vmcnt(loads per step + kStoreOps); the first tile gets as many loads
   // (into the scratch bytes) in place of stores.
   if constexpr (PERSIST) {
 #pragma unroll
-    for (uint32_t i = 0; i < kStoreOps; ++i) dma4(p.w, lane * 4u, lds0 + STAGES * STAGE);
+    for (uint32_t i = 0; i < kStoreOps; ++i) dma4(p.w, lane * 4u, lds0 + NS * STG);
   }
   uint32_t rot = 0;  // stage of the tile's step 0 (persistent blocks)
 
@@ -584,19 +627,35 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   auto compute = [&](uint32_t stage, uint32_t kb, auto FULL) __attribute__((always_inline)) {
     constexpr bool kFull = decltype(FULL)::value;
     if (!kFull && rb_live == 0) return;
-    const uint8_t* sA = smem + stage * STAGE;
+    const uint8_t* sA = smem + stage * STG;
     const uint8_t* sB = sA + A_BYTES;
-    const uint32_t* sS = reinterpret_cast<const uint32_t*>(sB + W_BYTES);
+    const uint32_t* sS = reinterpret_cast<const uint32_t*>(sB + WB);
     // operand fragments: lane (lr, lg) holds row lr, bytes [16lg, 16lg+16)
     // and [64+16lg, 64+16lg+16) of the step (the same map for both); the
     // fragment rows start at multiples of 16, so the slot of chunk lg is
     // lg ^ (lr >> 1) and that of chunk lg + 4 is the same slot ^ 4
     const uint32_t rd0 = (lg ^ (lr >> 1)) << 4;
     v8i wf[4];
+    [[maybe_unused]] uint32_t wsc[4];
+    [[maybe_unused]] v4i wlo[4];
+    if constexpr (kF4) {
+      // FP4 W (the MFMA's first operand, e2m1): lane (lr, lg) holds the 16
+      // bytes = 32 k [32 lg, 32 lg + 32) of the step of row lr, in slot
+      // lg ^ ((lr >> 2) & 3) of the 64-byte row, and that block's scale byte
+      const uint8_t* sW8 = reinterpret_cast<const uint8_t*>(sS) + SA_BYTES;  // [BN rows][4 B]
+      const uint32_t rdf = (lg ^ ((lr >> 2) & 3u)) << 4;
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const uint8_t* pb = sB + (wn * 64 + nb * 16 + lr) * LDS_ROW;
-      wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb + rd0), *reinterpret_cast<const v4i*>(pb + (rd0 ^ 64)));
+      for (int nb = 0; nb < 4; ++nb) {
+        const uint32_t row = wn * 64 + nb * 16 + lr;
+        wlo[nb] = *reinterpret_cast<const v4i*>(sB + row * 64 + rdf);
+        wsc[nb] = sW8[row * 4 + lg];
+      }
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const uint8_t* pb = sB + (wn * 64 + nb * 16 + lr) * LDS_ROW;
+        wf[nb] = cat8(*reinterpret_cast<const v4i*>(pb + rd0), *reinterpret_cast<const v4i*>(pb + (rd0 ^ 64)));
+      }
     }
     const v4i sa4 = *reinterpret_cast<const v4i*>(sS + wm * 64 + lr * 4);
     // W block scales of this wave's columns: SwiGLU gate (block 0) and up
@@ -677,6 +736,47 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       if (live(2)) fma4(2, tA);
       __builtin_amdgcn_sched_barrier(0);
       if (live(3)) fma4(3, tB);
+    } else if constexpr (kF4) {
+      // e4m3 A against MXFP4 W: both UE8M0 scales ride in the instruction
+      // (the W lane's own 32-k block scale, the A row's 128-k scale) and the
+      // MFMAs chain on the accumulator.  A 255 scale raises the scale bit and
+      // its block adds nothing, as in the 128 x 128 tile kernel: the
+      // fragment becomes zeros with scale 127.
+      // (branch-free: a wave-uniform branch around these selects made the
+      // compiler keep copies of every fragment and spill)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const bool ff = wsc[nb] == 0xffu;
+        bad |= ff ? (uint32_t)kErrScale : 0u;
+        const int keep = ff ? 0 : -1;
+        wlo[nb] &= v4i{keep, keep, keep, keep};
+        wsc[nb] = ff ? 127u : wsc[nb];
+      }
+      auto mma = [&](int r, v8i af) {
+        uint32_t sb = ((uint32_t)sa4[r] >> (8 * ((a_byte0[r] + kb) & 3u))) & 0xffu;
+        const bool aff = sb == 0xffu;
+        if (__builtin_amdgcn_ballot_w64(aff)) {
+          if (aff) {
+            bad |= kErrScale;
+            sb = 127;
+            af = v8i{0, 0, 0, 0, 0, 0, 0, 0};
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[nb][r] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(cat8(wlo[nb], v4i{0, 0, 0, 0}), af,
+                                                                       acc[nb][r], 4, 0, 0, (int)wsc[nb], 0, (int)sb);
+      };
+      v8i af = a_frag(0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (live(r)) {
+          const v8i afn = a_frag(r < 3 ? r + 1 : 3);
+          mma(r, af);
+          af = afn;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else {
       // UE8M0 scales ride in the MFMA's E8M0 operands and the MFMAs chain on
       // the accumulator.  A 255 scale raises the scale bit and its block adds
@@ -722,11 +822,12 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
   };
 
-  // Three LDS stages, loads two steps ahead.  The loads issued at step j are
-  // the seven DMAs of step j + 2.  Step j: wait until at most seven loads
-  // are in flight (step j + 1's: step j's tiles and scales have landed),
-  // barrier (every wave's DMA for step j is visible and step j - 1's compute
-  // is done, so its stage may be refilled), issue, compute step j.  Loads
+  // NS LDS stages, loads NS - 1 steps ahead.  The loads issued at step j
+  // are the DMAs of step j + NS - 1.  Step j: wait until only the loads of
+  // steps j + 1 .. j + NS - 2 are in flight (step j's tiles and scales have
+  // landed), barrier (every wave's DMA for step j is visible and step
+  // j - 1's compute is done, so its stage may be refilled), issue, compute
+  // step j.  Loads
   // past the last step re-read it (into a stage that is never used), or, in
   // a persistent block with a next tile, fetch that tile's first two steps.
   // The loads are issued by inline asm, so the compiler adds no waits of its
@@ -734,8 +835,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // step stays one straight line.  (A per-step L2 prefetch of a later step,
   // one 4-byte load per lane and line, measured slower: the tiles already
   // hit L2 about nine times in ten, and the extra load lengthens every wait.)
-  constexpr int kWaitStep = kBf ? kWaitVm6 : kWaitVm7;
-  constexpr int kWaitFirstEnc = vmcnt_enc((kBf ? 6 : 7) + (int)kStoreOps);
+  // vector loads per wave and step: A 2, W 4 (FP4: 2), scales 1 (bf16: 0)
+  constexpr int kLoads = kBf ? 6 : kF4 ? 5 : 7;
+  constexpr int kWaitStep = vmcnt_enc((int)(NS - 2) * kLoads);
+  constexpr int kWaitFirstEnc = vmcnt_enc(kLoads + (int)kStoreOps);
   // stages of steps kb + 0, 1, 2 (kb a multiple of 3)
   const uint32_t st0 = rot, st1 = rot == 2 ? 0u : rot + 1, st2 = rot == 0 ? 2u : rot - 1;
   // persistent blocks run steps 0 .. KB - 3 in the unrolled loop and the
@@ -753,8 +856,8 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       issue((J) % 3 == 0 ? st2 : (J) % 3 == 1 ? st0 : st1, j + 2, cur, NT);                              \
       compute((J) % 3 == 0 ? st0 : (J) % 3 == 1 ? st1 : st2, j, FULL);                               \
     } else {                                                                                         \
-      issue(((J) + 2) % 3, min(j + 2, last), cur, NT);                                                   \
-      compute((J) % 3, j, FULL);                                                                     \
+      issue(((J) + NS - 1) % NS, min(j + NS - 1, last), cur, NT);                                        \
+      compute((J) % NS, j, FULL);                                                                    \
     }                                                                                                \
   }
       uint32_t kb = 0;
@@ -768,13 +871,19 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
         PIH_MOE_STEP(5, true, kWaitStep)
         kb = 6;
       }
-      for (; kb + 6 < KBm; kb += 6) {
+      // unrolled by a multiple of NS, so that every stage index is a constant
+      constexpr uint32_t U = NS == 4 ? 8 : 6;
+      for (; kb + U < KBm; kb += U) {
         PIH_MOE_STEP(0, false, kWaitStep)
         PIH_MOE_STEP(1, false, kWaitStep)
         PIH_MOE_STEP(2, false, kWaitStep)
         PIH_MOE_STEP(3, false, kWaitStep)
         PIH_MOE_STEP(4, false, kWaitStep)
         PIH_MOE_STEP(5, false, kWaitStep)
+        if constexpr (U == 8) {
+          PIH_MOE_STEP(6, false, kWaitStep)
+          PIH_MOE_STEP(7, false, kWaitStep)
+        }
       }
       PIH_MOE_STEP(0, true, kWaitStep)
       PIH_MOE_STEP(1, true, kWaitStep)
@@ -782,6 +891,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       PIH_MOE_STEP(3, true, kWaitStep)
       PIH_MOE_STEP(4, true, kWaitStep)
       PIH_MOE_STEP(5, true, kWaitStep)
+      if constexpr (U == 8) {
+        PIH_MOE_STEP(6, true, kWaitStep)
+        PIH_MOE_STEP(7, true, kWaitStep)
+      }
 #undef PIH_MOE_STEP
     };
     steps();
@@ -1132,11 +1245,13 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 
 template <int OP, int SCALE>
 void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out, bool persist) {
-  if constexpr (OP == kOpFp8) {
+  if constexpr (OP == kOpFp8 || OP == kOpFp4) {
     if (out == kOutSwiGlu) {
       hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGlu, false>), dim3(grid), dim3(NTH), 0, s, mp);
       return;
     }
+  }
+  if constexpr (OP == kOpFp8) {
     if (out == kOutSwiGluFp8) {
       hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGluFp8, false>), dim3(grid), dim3(NTH), 0, s, mp);
       return;
@@ -1235,6 +1350,56 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
   if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind, persist);
   else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
   return AfterLaunch("fp8_moe_gemm_launch_failed");
+}
+
+// MXFP4 MoE with e4m3 activations: the experts with more than light_rows
+// rows on the 128 x 256 tiles (FP4 W operand).  Called by LaunchFp4Gemm
+// after its checks when Fp4MoeBigTileTakes(a).
+bool Fp4MoeBigTileTakes(const Fp4GemmArgs& a) {
+  const bool swiglu = a.out_kind == kOutSwiGlu;
+  return a.moe && a.act == kActE4m3 && a.k % 128 == 0 && a.k >= 128 && (swiglu ? a.n % 256 == 0 : a.n % 128 == 0) &&
+         (a.out_kind == kOutSwiGlu || a.out_kind == kOutBf16 || a.out_kind == kOutF32) &&
+         reinterpret_cast<uintptr_t>(a.w_scale) % 4 == 0 && (uint64_t)a.a_rows_total * a.k <= 0xffffffffull &&
+         (uint64_t)a.n * (a.k / 2) <= 0xffffffffull;
+}
+
+St LaunchFp4MoeBigTile(const Fp4GemmArgs& a, uint32_t light_rows) {
+  MoeParams mp{};
+  mp.a = static_cast<const uint8_t*>(a.a);
+  mp.a_scale = a.a_scale;
+  mp.a_gather = a.a_gather;
+  mp.w = a.w;
+  mp.w_scale = a.w_scale;
+  mp.out = a.out;
+  mp.row_weight = a.row_weight;
+  mp.offsets = a.offsets;
+  mp.err = a.error_flag;
+  mp.m = a.m;
+  mp.n = a.n;
+  mp.k = a.k;
+  mp.experts = a.problems;
+  mp.a_rows_total = a.a_rows_total;
+  mp.light_rows = light_rows;
+  const bool swiglu = a.out_kind == kOutSwiGlu;
+  mp.out_row_stride = swiglu ? a.n / 2 : a.n;
+  mp.n_tiles = swiglu ? a.n / 256 : (a.n + BN - 1) / BN;
+  mp.stage_out = StageOut(a.out, mp.out_row_stride, 0, a.out_kind);
+  mp.limit = a.swiglu_limit;
+  // the MXFP4 error bits: 1 code, 2 scale, 4 non-finite
+  mp.err_code = 1u;
+  mp.err_scale = 2u;
+  mp.err_nonfinite = 4u;
+  const uint64_t mt = (uint64_t)a.m / BM + (a.problems < a.m ? a.problems : a.m);
+  const uint64_t total = mt * mp.n_tiles;
+  if (total == 0 || total > 0x7fffffffull - 8) return Invalid("fp4_moe_gemm_grid_too_large");
+  const bool persist = Persistent(a.out_kind, a.a_gather != nullptr, false, a.problems, mp.out_row_stride, a.k / 128);
+  uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  mp.vb_end = grid;
+  if (persist) grid = std::min(grid, PersistentBlocks());
+  St s = RequireCleanLastError();
+  if (!s.ok()) return s;
+  launch_out<kOpFp4, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
+  return AfterLaunch("fp4_moe_gemm_launch_failed");
 }
 
 St LaunchBigTileGemm(const BigTileArgs& a) {

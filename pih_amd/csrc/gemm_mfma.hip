@@ -872,11 +872,23 @@ St LaunchFp4Gemm(const Fp4GemmArgs& a) {
   St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, 0, a.moe ? Fp4MoeLightRows(a) : 0);
   if (!s.ok()) return s;
   if (grid) {
-    ForkStreams* f = gp.light_rows ? ForkBegin(a.stream) : nullptr;
+    // The 128 x 256 FP4 tiles and the streaming kernel run one after the
+    // other: a big-tile block needs most of a CU's LDS and cannot start on
+    // a CU the streaming blocks hold, so forked they overlapped worse than
+    // in sequence (512 tokens 800 -> 768 us, 64 tokens 343 -> 305 us).  The
+    // 128 x 128 tiles (bf16 activations) fork beside the streaming kernel.
+    const bool big = a.moe && Fp4MoeBigTileTakes(a);
+    ForkStreams* f = gp.light_rows && !big ? ForkBegin(a.stream) : nullptr;
     const hipStream_t hs = f ? f->aux : a.stream;
-    if (a.act == kActE4m3) dispatch_out<kFp4, kScaleUe8m0>(gp, grid, hs, a.out_kind, a.moe, !a.moe);
-    else dispatch_out<kBf16Fp4, kScaleUe8m0>(gp, grid, hs, a.out_kind, a.moe, false);
-    s = AfterLaunch("fp4_gemm_launch_failed");
+    if (big) {
+      Fp4GemmArgs big = a;
+      big.stream = hs;
+      s = LaunchFp4MoeBigTile(big, gp.light_rows);
+    } else {
+      if (a.act == kActE4m3) dispatch_out<kFp4, kScaleUe8m0>(gp, grid, hs, a.out_kind, a.moe, !a.moe);
+      else dispatch_out<kBf16Fp4, kScaleUe8m0>(gp, grid, hs, a.out_kind, a.moe, false);
+      s = AfterLaunch("fp4_gemm_launch_failed");
+    }
     if (f) {
       if (s.ok()) s = LaunchFp4MoeStream(a);
       const St joined = ForkEnd(f, a.stream);

@@ -124,6 +124,11 @@ St LaunchFp4SmallM(const Fp4GemmArgs& a, bool& taken);
 constexpr uint32_t kMoeLightRows = 64;
 uint32_t Fp4MoeLightRows(const Fp4GemmArgs& a);
 St LaunchFp4MoeStream(const Fp4GemmArgs& a);
+// The other experts of an e4m3 MoE problem run on the 128 x 256 tiles of
+// gemm_fp8_moe.hip with an FP4 W operand when the shape fits
+// (Fp4MoeBigTileTakes), on the 128 x 128 tiles of gemm_mfma.hip otherwise.
+bool Fp4MoeBigTileTakes(const Fp4GemmArgs& a);
+St LaunchFp4MoeBigTile(const Fp4GemmArgs& a, uint32_t light_rows);
 
 // ------------------------------------------------------------- BF16 GEMM
 // C[m,n] = A[m,k] . W[n,k]^T, fp32 accumulate, bf16 or fp32 out.

@@ -143,3 +143,52 @@ def test_fp4_ff_scale_skips_the_block(eng):
     assert_close(got[rows], ref, "0xFF scale fp4")
     assert_close(got[rows][:, 77], ref[:, 77], "0xFF W row")
     assert_close(got[[2, 300]], ref[[1, 3]], "0xFF A rows")
+
+
+@pytest.mark.parametrize("gather", [False, True])
+def test_moe_fp4_ff_scale_skips_the_block(eng, gather):
+    """MXFP4 MoE, e4m3 activations (N = 2048, K = 4096): expert 0 has 300
+    rows (the 128 x 256 tiles with the FP4 W operand; persistent without a
+    gather, one block per tile with one), expert 1 has 40 (the streaming
+    kernel).  Expert 0's W row 77 scale of 32-k block 9 and A rows 2 and 250's
+    scale of 128-k block 1 are 0xFF."""
+    import torch
+
+    from pih_amd import linear
+
+    n, k, heavy, light = 2048, 4096, 300, 40
+    m = heavy + light
+    x = synth.bf16_normal(synth.config_seed(5, 960), (m, k))
+    a, _ = oracle.fp8_quant_ue8m0(oracle.bf16_bits_to_f32(x))
+    packed = np.empty((2, n, k // 2), np.uint8)
+    for e in range(2):
+        packed[e], _ = synth.mxfp4_weight(synth.config_seed(5, 961 + e), n, k)
+    sa = (100 + synth.splitmix64(962, m * (k // 128)) % np.uint64(6)).astype(np.uint8).reshape(m, k // 128)
+    sw = (100 + synth.splitmix64(963, 2 * n * (k // 32)) % np.uint64(6)).astype(np.uint8).reshape(2, n, k // 32)
+    ff_rows = np.array([2, 250])
+    sa[:heavy, 2], sw[0, :, 8:12] = 228, 0
+    sw[0, 77, 9] = 0xFF
+    sw[0, :, 4:8], sa[:heavy, 1] = 228, 0
+    sa[ff_rows, 1] = 0xFF
+    a0, sa0, p0, sw0 = a.copy(), sa.copy(), packed[0].copy(), sw[0].copy()
+    a0[ff_rows, 128:256] = 0
+    sa0[ff_rows, 1] = 127
+    p0[77, 9 * 16:10 * 16] = 0
+    sw0[77, 9] = 127
+    off = np.array([0, heavy, m], np.uint32)
+    # the gather reverses each expert's rows (the 0xFF A rows stay in expert 0)
+    rt = np.concatenate([np.arange(heavy)[::-1], np.arange(heavy, m)[::-1]]).astype(np.uint32) if gather else None
+    src = rt if gather else np.arange(m)
+    out, flag = linear.moe_mxfp4_gemm(to_dev(a), to_dev(sa), to_dev(rt) if gather else None, to_dev(packed),
+                                      to_dev(sw), to_dev(off), m, abi.ACTIVATION_E4M3, abi.OUTPUT_BF16)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 2
+    got = oracle.bf16_bits_to_f32(to_host(out))
+    assert np.isfinite(got).all()
+    rows = np.array([0, 1, 2, 3, 127, 128, 250, 255, 256, 299])
+    ref = oracle.fp4_gemm(np.ascontiguousarray(a0[src[rows]]), np.ascontiguousarray(sa0[src[rows]]), p0, sw0)
+    assert_close(got[rows], ref, "0xFF scale moe fp4")
+    assert_close(got[rows][:, 77], ref[:, 77], "0xFF W row")
+    lrows = np.arange(heavy, m, 7)
+    ref_l = oracle.fp4_gemm(np.ascontiguousarray(a[src[lrows]]), np.ascontiguousarray(sa[src[lrows]]), packed[1], sw[1])
+    assert_close(got[lrows], ref_l, "light expert")
