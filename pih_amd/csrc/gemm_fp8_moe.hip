@@ -55,9 +55,16 @@ constexpr uint32_t STAGE = A_BYTES + W_BYTES + SA_BYTES + SW_BYTES, DUMMY_BYTES 
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
 // [6:4], lgkmcnt [11:8]; an all-ones field does not wait)
 constexpr int kWaitVm7 = 0x0F77;     // vmcnt(7)
-// operand kinds: e4m3 with block scales, bf16 (no scales), or e4m3 A
-// against MXFP4 W (e2m1 two per byte, UE8M0 per W row and 32 k)
-enum : int { kOpFp8 = 0, kOpBf16 = 1, kOpFp4 = 2 };
+// operand kinds: e4m3 with block scales, bf16 (no scales), or e4m3 (kOpFp4)
+// or bf16 (kOpBf16Fp4) A against MXFP4 W (e2m1 two per byte, UE8M0 per W
+// row and 32 k)
+enum : int { kOpFp8 = 0, kOpBf16 = 1, kOpFp4 = 2, kOpBf16Fp4 = 3 };
+// static LDS of a block: the FP8 stages (the staged epilogue needs as
+// much), or three bf16 x FP4 stages (256-byte A rows), plus the scratch word
+template <int OP>
+constexpr uint32_t smem_bytes() {
+  return (OP == kOpBf16Fp4 ? 3 * (BM * 256 + BN * 64 + BN * 4) : STAGES * STAGE) + DUMMY_BYTES;
+}
 constexpr int kWaitVm0 = 0x0F70;     // vmcnt(0)
 constexpr uint32_t kCodePitch = 144;  // staged e4m3 code rows (128 bytes + 16)
 // s_waitcnt immediate waiting for vmcnt <= n (n < 64; bits [3:0] and [15:14])
@@ -389,11 +396,15 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // Stage s at smem + s * STG: A tile, W tile, A-row scales, W scales.
   // (FP4 W: 64-byte tile rows and 4 scale bytes per W row; the array keeps
   // the FP8 size, which the staged epilogue also needs.)
-  __shared__ __align__(16) uint8_t smem[STAGES * STAGE + DUMMY_BYTES];
-  constexpr bool kF4 = OP == kOpFp4;
-  constexpr uint32_t W_ROW = kF4 ? 64 : LDS_ROW, WB = BN * W_ROW, SWB = kF4 ? BN * 4 : SW_BYTES;
-  constexpr uint32_t STG = A_BYTES + WB + SA_BYTES + SWB;
-  static_assert(STG <= STAGE, "stage layout");
+  __shared__ __align__(16) uint8_t smem[smem_bytes<OP>()];
+  constexpr bool kF4 = OP == kOpFp4, kBF4 = OP == kOpBf16Fp4, kW4 = kF4 || kBF4;
+  // A: 128 bytes of a row per step (256 for bf16 x FP4: 128 k per step);
+  // W: 128 bytes (64 for FP4); A-row scales (none for bf16); W scales
+  constexpr uint32_t A_ROW = kBF4 ? 256 : LDS_ROW, AB = BM * A_ROW;
+  constexpr uint32_t W_ROW = kW4 ? 64 : LDS_ROW, WB = BN * W_ROW, SAB = kBF4 ? 0 : SA_BYTES;
+  constexpr uint32_t SWB = kW4 ? BN * 4 : SW_BYTES;
+  constexpr uint32_t STG = AB + WB + SAB + SWB;
+  static_assert(PERSIST ? STG <= STAGE : 3 * STG + DUMMY_BYTES <= sizeof(smem), "stage layout");
   // LDS stages: 4 for FP4 W outside persistent launches (its stage is
   // 33.5 KB: the loads run three steps ahead), 3 otherwise; the scratch
   // word of the dummy scale loads follows the last stage
@@ -410,10 +421,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // the masked bit is not changed while this kernel runs: one value for every thread
   if (p.skip_if && (__hip_atomic_load(p.skip_if, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & p.skip_bit)) return;
 
-  // a K step is 128 bytes of an A row: 128 e4m3 or 64 bf16 values (and
-  // 64 bytes of an FP4 W row)
+  // a K step is 128 bytes of an A row: 128 e4m3 or 64 bf16 values (bf16 x
+  // FP4: 256 bytes, 128 values), and 64 bytes of an FP4 W row
   constexpr bool kBf = OP == kOpBf16;
-  const uint32_t K = p.k, RB = kBf ? 2 * K : K, KB = RB / 128, RBW = kF4 ? K / 2 : RB;
+  const uint32_t K = p.k, RB = kBf || kBF4 ? 2 * K : K, KB = kBF4 ? K / 128 : RB / 128, RBW = kW4 ? K / 2 : RB;
   uint32_t bad = 0;
 
   [[maybe_unused]] MoeTable tab{};
@@ -485,7 +496,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // dword and are picked out by byte offset.  bf16 operands have no scales
   // (six loads per step).
   struct Ops {
-    uint32_t a_off[2], w_off[4];  // byte offsets from the operand bases
+    uint32_t a_off[4], w_off[4];  // byte offsets from the operand bases
     const uint8_t* w_base;        // the expert's (problem's) W
     const uint8_t* s_src;         // this lane's scale source at k step 0
     uint64_t ws_off[2];           // the tile's two W scale blocks (entries)
@@ -505,12 +516,23 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
     o.ws_off[0] = ((uint64_t)e * (p.n / 128) + wblk0) * KB;
     o.ws_off[1] = ((uint64_t)e * (p.n / 128) + wblk1) * KB;
+    if constexpr (kBF4) {
+      // 256-byte rows: instruction i lands rows 16 wv + 4 i + (l >> 4), slot
+      // l & 15, which holds chunk (l & 15) ^ (row & 15)
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t R = 16 * wv + 8 * i + lrow;
-      o.a_off[i] = (uint32_t)(a_source(R, e, r0, rs) * RB) + ((lslot ^ ((R >> 1) & 7u)) << 4);
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t R = 16 * wv + 4 * i + (lane >> 4);
+        o.a_off[i] = (uint32_t)(a_source(R, e, r0, rs) * RB) + (((lane & 15u) ^ (R & 15u)) << 4);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t R = 16 * wv + 8 * i + lrow;
+        o.a_off[i] = (uint32_t)(a_source(R, e, r0, rs) * RB) + ((lslot ^ ((R >> 1) & 7u)) << 4);
+      }
+      o.a_off[2] = o.a_off[3] = 0;
     }
-    if constexpr (kF4) {
+    if constexpr (kW4) {
       // 64-byte rows: instruction i lands rows 32 wv + 16 i + (l >> 2), slot
       // l & 3, which holds chunk (l & 3) ^ ((row >> 2) & 3)
 #pragma unroll
@@ -527,17 +549,19 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       }
     }
     o.s_src = nullptr;
-    if constexpr (kF4) {
-      // waves 0, 1: A-row scales as for FP8; waves 2..5: the 4 scale bytes
-      // of W tile row 64 (w - 2) + l per step; waves 6, 7: a dummy word
-      if (wv < 2) {
-        const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2), e, r0, rs);
-        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB;
-      } else if (wv < 6) {
+    if constexpr (kW4) {
+      // waves 0, 1: A-row scales as for FP8 (bf16 A: a dummy word); waves
+      // 2..5: the 4 scale bytes of W tile row 64 (w - 2) + l per step;
+      // waves 6, 7: a dummy word
+      // (the dummy words read the first W scale bytes: in bounds)
+      if (wv >= 2 && wv < 6) {
         const uint32_t R = 64 * (wv - 2) + lane;
         o.s_src = static_cast<const uint8_t*>(p.w_scale) + ((uint64_t)e * p.n + w_row(R, t)) * (K / 32);
+      } else if (kF4 && wv < 2) {
+        const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2), e, r0, rs);
+        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB;
       } else {
-        o.s_src = static_cast<const uint8_t*>(p.a_scale);
+        o.s_src = static_cast<const uint8_t*>(p.w_scale);
       }
     } else if constexpr (!kBf) {
       if (wv < 2) {
@@ -549,22 +573,22 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     }
   };
   uint32_t s_lds = 0;
-  if constexpr (kF4) s_lds = wv < 2 ? A_BYTES + WB + 256 * wv : A_BYTES + WB + SA_BYTES + 256 * (wv - 2);
+  if constexpr (kW4) s_lds = wv < 2 ? AB + WB + 256 * wv : AB + WB + SAB + 256 * (wv - 2);
   else if constexpr (!kBf) s_lds = wv < 2 ? A_BYTES + W_BYTES + 256 * wv : A_BYTES + W_BYTES + SA_BYTES;
   s_lds = __builtin_amdgcn_readfirstlane(s_lds);
-  const bool s_scratch = kF4 ? wv >= 6 : wv > 2;
+  const bool s_scratch = kW4 ? wv >= 6 || (kBF4 && wv < 2) : wv > 2;
   // per-step advance of the scale source: 4 bytes for FP4 W-scale rows
-  const uint32_t s_step = kF4 && wv >= 2 && wv < 6 ? 4u : ESZ;
-  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(wv * 2048),
-                 w_lds = __builtin_amdgcn_readfirstlane(A_BYTES + wv * (32 * W_ROW));
+  const uint32_t s_step = kW4 && wv >= 2 && wv < 6 ? 4u : ESZ;
+  const uint32_t a_lds = __builtin_amdgcn_readfirstlane(wv * (16 * A_ROW)),
+                 w_lds = __builtin_amdgcn_readfirstlane(AB + wv * (32 * W_ROW));
   auto issue = [&](uint32_t stage, uint32_t kb, const Ops& o, auto NT) __attribute__((always_inline)) {
     const uint32_t base = lds0 + stage * STG;
-    const uint8_t* ab = uniform_ptr(p.a + (uint64_t)kb * 128);
+    const uint8_t* ab = uniform_ptr(p.a + (uint64_t)kb * A_ROW);
     const uint8_t* wb = uniform_ptr(o.w_base + (uint64_t)kb * W_ROW);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(ab, o.a_off[i], base + a_lds + i * 1024);
+    for (int i = 0; i < (kBF4 ? 4 : 2); ++i) dma16(ab, o.a_off[i], base + a_lds + i * 1024);
 #pragma unroll
-    for (int i = 0; i < (kF4 ? 2 : 4); ++i) {
+    for (int i = 0; i < (kW4 ? 2 : 4); ++i) {
       if constexpr (decltype(NT)::value) dma16nt(wb, o.w_off[i], base + w_lds + i * 1024);
       else dma16(wb, o.w_off[i], base + w_lds + i * 1024);
     }
@@ -628,7 +652,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     constexpr bool kFull = decltype(FULL)::value;
     if (!kFull && rb_live == 0) return;
     const uint8_t* sA = smem + stage * STG;
-    const uint8_t* sB = sA + A_BYTES;
+    const uint8_t* sB = sA + AB;
     const uint32_t* sS = reinterpret_cast<const uint32_t*>(sB + WB);
     // operand fragments: lane (lr, lg) holds row lr, bytes [16lg, 16lg+16)
     // and [64+16lg, 64+16lg+16) of the step (the same map for both); the
@@ -638,11 +662,11 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     v8i wf[4];
     [[maybe_unused]] uint32_t wsc[4];
     [[maybe_unused]] v4i wlo[4];
-    if constexpr (kF4) {
+    if constexpr (kW4) {
       // FP4 W (the MFMA's first operand, e2m1): lane (lr, lg) holds the 16
       // bytes = 32 k [32 lg, 32 lg + 32) of the step of row lr, in slot
       // lg ^ ((lr >> 2) & 3) of the 64-byte row, and that block's scale byte
-      const uint8_t* sW8 = reinterpret_cast<const uint8_t*>(sS) + SA_BYTES;  // [BN rows][4 B]
+      const uint8_t* sW8 = reinterpret_cast<const uint8_t*>(sS) + SAB;  // [BN rows][4 B]
       const uint32_t rdf = (lg ^ ((lr >> 2) & 3u)) << 4;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
@@ -736,6 +760,45 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       if (live(2)) fma4(2, tA);
       __builtin_amdgcn_sched_barrier(0);
       if (live(3)) fma4(3, tB);
+    } else if constexpr (kBF4) {
+      // bf16 A against MXFP4 W: 4 x 4 x 4 MFMAs 16x16x32 bf16 per step.
+      // MFMA q takes, in lane group lg, k [32 lg + 8 q, +8): dword q of the
+      // W lane's 16 bytes (8 e2m1 values of block lg, converted exactly to
+      // bf16 times 2^(s-127), one byte per v_cvt_scalef32_pk_bf16_fp4) and
+      // chunk 4 lg + q of the A row (slot (4 lg + q) ^ lr of its 256 bytes).
+      // A 255 W scale raises the scale bit (the block's products are then
+      // not finite, as in the 128 x 128 tile kernel).
+      typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+      float wsf[4];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        bad |= wsc[nb] == 0xffu ? (uint32_t)kErrScale : 0u;
+        wsf[nb] = ue8m0_value(wsc[nb]);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v4i wq[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          const uint32_t wd = (uint32_t)wlo[nb][q];
+          wq[nb] = v4i{__builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, wsf[nb], 0)),
+                       __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, wsf[nb], 1)),
+                       __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, wsf[nb], 2)),
+                       __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wd, wsf[nb], 3))};
+        }
+        const uint32_t slot = ((4 * lg + q) ^ lr) << 4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (live(r)) {
+            const v4i av = *reinterpret_cast<const v4i*>(sA + (wm * 64 + r * 16 + lr) * A_ROW + slot);
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+              acc[nb][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, wq[nb]),
+                                                                   __builtin_bit_cast(v8bf, av), acc[nb][r], 0, 0, 0);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else if constexpr (kF4) {
       // e4m3 A against MXFP4 W: both UE8M0 scales ride in the instruction
       // (the W lane's own 32-k block scale, the A row's 128-k scale) and the
@@ -835,7 +898,8 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // step stays one straight line.  (A per-step L2 prefetch of a later step,
   // one 4-byte load per lane and line, measured slower: the tiles already
   // hit L2 about nine times in ten, and the extra load lengthens every wait.)
-  // vector loads per wave and step: A 2, W 4 (FP4: 2), scales 1 (bf16: 0)
+  // vector loads per wave and step: A 2 (bf16 x FP4: 4), W 4 (FP4: 2),
+  // scales 1 (bf16: 0)
   constexpr int kLoads = kBf ? 6 : kF4 ? 5 : 7;
   constexpr int kWaitStep = vmcnt_enc((int)(NS - 2) * kLoads);
   constexpr int kWaitFirstEnc = vmcnt_enc(kLoads + (int)kStoreOps);
@@ -1245,7 +1309,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 
 template <int OP, int SCALE>
 void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out, bool persist) {
-  if constexpr (OP == kOpFp8 || OP == kOpFp4) {
+  if constexpr (OP == kOpFp8 || OP == kOpFp4 || OP == kOpBf16Fp4) {
     if (out == kOutSwiGlu) {
       hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutSwiGlu, false>), dim3(grid), dim3(NTH), 0, s, mp);
       return;
@@ -1257,11 +1321,14 @@ void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out, 
       return;
     }
   }
-  if (persist) {
-    if (out == kOutF32)
-      hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutF32, true>), dim3(grid), dim3(NTH), 0, s, mp);
-    else hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutBf16, true>), dim3(grid), dim3(NTH), 0, s, mp);
-    return;
+  // (bf16 x FP4 stages leave no LDS for the persistent tile table)
+  if constexpr (OP != kOpBf16Fp4) {
+    if (persist) {
+      if (out == kOutF32)
+        hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutF32, true>), dim3(grid), dim3(NTH), 0, s, mp);
+      else hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutBf16, true>), dim3(grid), dim3(NTH), 0, s, mp);
+      return;
+    }
   }
   if (out == kOutF32)
     hipLaunchKernelGGL((fp8_moe_gemm_kernel<OP, SCALE, kOutF32, false>), dim3(grid), dim3(NTH), 0, s, mp);
@@ -1352,14 +1419,16 @@ St LaunchFp8MoeGemm(const BlockGemmArgs& a) {
   return AfterLaunch("fp8_moe_gemm_launch_failed");
 }
 
-// MXFP4 MoE with e4m3 activations: the experts with more than light_rows
-// rows on the 128 x 256 tiles (FP4 W operand).  Called by LaunchFp4Gemm
-// after its checks when Fp4MoeBigTileTakes(a).
+// MXFP4 MoE: the experts with more than light_rows rows on the 128 x 256
+// tiles (FP4 W operand; e4m3 or bf16 activations).  Called by
+// LaunchFp4Gemm after its checks when Fp4MoeBigTileTakes(a).
 bool Fp4MoeBigTileTakes(const Fp4GemmArgs& a) {
   const bool swiglu = a.out_kind == kOutSwiGlu;
-  return a.moe && a.act == kActE4m3 && a.k % 128 == 0 && a.k >= 128 && (swiglu ? a.n % 256 == 0 : a.n % 128 == 0) &&
+  const uint64_t a_row = a.act == kActBf16 ? 2ull * a.k : a.k;
+  return a.moe && (a.act == kActE4m3 || a.act == kActBf16) && a.k % 128 == 0 && a.k >= 128 &&
+         (swiglu ? a.n % 256 == 0 : a.n % 128 == 0) &&
          (a.out_kind == kOutSwiGlu || a.out_kind == kOutBf16 || a.out_kind == kOutF32) &&
-         reinterpret_cast<uintptr_t>(a.w_scale) % 4 == 0 && (uint64_t)a.a_rows_total * a.k <= 0xffffffffull &&
+         reinterpret_cast<uintptr_t>(a.w_scale) % 4 == 0 && (uint64_t)a.a_rows_total * a_row <= 0xffffffffull &&
          (uint64_t)a.n * (a.k / 2) <= 0xffffffffull;
 }
 
@@ -1392,13 +1461,16 @@ St LaunchFp4MoeBigTile(const Fp4GemmArgs& a, uint32_t light_rows) {
   const uint64_t mt = (uint64_t)a.m / BM + (a.problems < a.m ? a.problems : a.m);
   const uint64_t total = mt * mp.n_tiles;
   if (total == 0 || total > 0x7fffffffull - 8) return Invalid("fp4_moe_gemm_grid_too_large");
-  const bool persist = Persistent(a.out_kind, a.a_gather != nullptr, false, a.problems, mp.out_row_stride, a.k / 128);
+  const bool bf = a.act == kActBf16;
+  const bool persist =
+      !bf && Persistent(a.out_kind, a.a_gather != nullptr, false, a.problems, mp.out_row_stride, a.k / 128);
   uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
   mp.vb_end = grid;
   if (persist) grid = std::min(grid, PersistentBlocks());
   St s = RequireCleanLastError();
   if (!s.ok()) return s;
-  launch_out<kOpFp4, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
+  if (bf) launch_out<kOpBf16Fp4, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, false);
+  else launch_out<kOpFp4, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
   return AfterLaunch("fp4_moe_gemm_launch_failed");
 }
 
