@@ -17,9 +17,9 @@
 // that (the 128-row tiles of gemm_mfma.hip spend most of their loads on
 // dead activation rows when an expert has a few rows):
 //   * a block of 4 waves owns 128 W rows of one light expert (<= 64 rows)
-//     and up to 32 of its rows (an expert with 33-64 rows is two items);
-//     each wave owns 32
-//     W rows (two 16-row MFMA fragments) and loads them into registers,
+//     and up to 32 (e4m3) or 16 (bf16) of its rows (an expert with more
+//     is two to four items); each wave owns 32 W rows (two 16-row MFMA
+//     fragments) and loads them into registers,
 //     non-temporal, 3-4 steps of 256 k ahead, as whole 128-byte lines (8
 //     rows x 128 B per instruction, four per step: the MFMA operand layout,
 //     16 rows x 64 B per instruction, streams ~25 % slower from HBM); a
@@ -62,10 +62,13 @@ constexpr uint32_t kWPitch = 144;  // W tile row: one 128-byte step + pad
 template <int ACT>
 struct Act {
   // rows per pass: a light expert with more rows is done in row chunks
-  // (adjacent items, so the second pass over the weights meets them in the
-  // caches).  32 keeps the unrolled e4m3 loops at 3 blocks per CU (<= 168
-  // registers, ~42 KB of LDS); 64 would hold them at 2.
-  static constexpr uint32_t MAXR = 32;
+  // (adjacent items, so the later passes over the weights meet them in the
+  // caches).  32 (e4m3) and 16 (bf16, 512-byte activation rows) keep the
+  // unrolled loops at 3 blocks per CU (<= 168 registers, ~43 KB of LDS;
+  // bf16 at K = 7168 stays at 2 for its registers); 64 / 32 held them at 2
+  // (64-token layer: e4m3 gate/up 178 -> 148 us with the scale DMA, bf16
+  // 223 -> 188 us).
+  static constexpr uint32_t MAXR = ACT == kActBf16 ? 16 : 32;
   static constexpr uint32_t ROW = ACT == kActBf16 ? 512 : 256;  // activation bytes per row and step
   static constexpr uint32_t CHUNKS = MAXR * ROW / 16 / NTH;     // 16-byte chunks per thread and step
   static constexpr uint32_t RPI = NTH * 16 / ROW;               // rows per staging instruction
@@ -183,7 +186,7 @@ template <int ACT, int OUT, int KBT>
 __global__ __launch_bounds__(NTH, 2) void fp4_moe_stream_kernel(StreamParams p) {
   using C = Act<ACT>;
   constexpr uint32_t MAXR = C::MAXR, ROW = C::ROW, CH = C::CHUNKS, NA = MAXR / 16;
-  static_assert(NA == 2, "two 16-row activation fragments per chunk");
+  static_assert(NA == (ACT == kActBf16 ? 1 : 2), "activation fragments per chunk");
   // steps in flight per wave: 3 with an unrolled K loop (the ring then fits
   // the 256 registers of two waves per SIMD), 4 in the generic loop (whose
   // 8-step body needs a depth dividing 8)
