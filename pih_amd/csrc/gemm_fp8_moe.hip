@@ -1458,9 +1458,14 @@ St LaunchFp4MoeBigTile(const Fp4GemmArgs& a, uint32_t light_rows) {
   mp.err_code = 1u;
   mp.err_scale = 2u;
   mp.err_nonfinite = 4u;
-  const uint64_t mt = (uint64_t)a.m / BM + (a.problems < a.m ? a.problems : a.m);
+  // sum over the taken experts of ceil(rows / BM) <= m / BM + their count,
+  // and at most m / (light_rows + 1) experts have more than light_rows rows
+  // (a launch with none then costs a few hundred blocks, not thousands)
+  const uint64_t taken = std::min<uint64_t>(a.problems, (uint64_t)a.m / ((uint64_t)light_rows + 1));
+  const uint64_t mt = (uint64_t)a.m / BM + taken;
   const uint64_t total = mt * mp.n_tiles;
-  if (total == 0 || total > 0x7fffffffull - 8) return Invalid("fp4_moe_gemm_grid_too_large");
+  if (total == 0) return Ok();  // no expert can have more than light_rows rows
+  if (total > 0x7fffffffull - 8) return Invalid("fp4_moe_gemm_grid_too_large");
   const bool bf = a.act == kActBf16;
   const bool persist =
       !bf && Persistent(a.out_kind, a.a_gather != nullptr, false, a.problems, mp.out_row_stride, a.k / 128);
