@@ -1038,6 +1038,11 @@ St launch_group_mid(GemvGroup g, hipStream_t s, bool& taken) {
   } else {
     if (mt > 2) return Ok();
     if (mt == 2 || rows16 >= 512) waves = 4;
+    // m <= 16 with many row blocks: each x fragment feeds 2 or 4 W blocks,
+    // keeping >= 384 blocks (grouped Qwen3-8B [gate, up] at m = 16: the
+    // pass 54.3 -> 49.3 us; gate or up alone with 4 W blocks per block
+    // left 192 blocks and ran slower than with 2)
+    if (mt == 1 && rows16 >= 512) nw = rows16 >= 1024 ? 4 : 2;
   }
   if (steps % (uint32_t)waves || (steps / waves) % (uint32_t)u) return Ok();
   for (uint32_t i = 0; i < g.count; ++i)
@@ -1052,6 +1057,8 @@ St launch_group_mid(GemvGroup g, hipStream_t s, bool& taken) {
     return nw == 4 ? launch_mid<FMT, 4, 4, 4, 2>(g, spw, s) : launch_mid<FMT, 4, 1, 8, 2>(g, spw, s);
   } else {
     if (mt == 2) return launch_mid<FMT, 2, 1, 4, 2>(g, spw, s);
+    if (nw == 4) return launch_mid<FMT, 1, 4, 4, 2>(g, spw, s);
+    if (nw == 2) return launch_mid<FMT, 1, 2, 4, 2>(g, spw, s);
     return waves == 4 ? launch_mid<FMT, 1, 1, 4, 2>(g, spw, s) : launch_mid<FMT, 1, 1, 8, 2>(g, spw, s);
   }
 }
