@@ -192,3 +192,44 @@ def test_moe_fp4_ff_scale_skips_the_block(eng, gather):
     lrows = np.arange(heavy, m, 7)
     ref_l = oracle.fp4_gemm(np.ascontiguousarray(a[src[lrows]]), np.ascontiguousarray(sa[src[lrows]]), packed[1], sw[1])
     assert_close(got[lrows], ref_l, "light expert")
+
+
+def test_moe_fp4_bf16_ff_weight_scale(eng):
+    """MXFP4 MoE with bf16 activations (N = 2048, K = 4096): expert 0 (300
+    rows, the 128 x 256 tiles) has W row 77's scale of 32-k block 9 at 0xFF.
+    As in the 128 x 128 tile kernel, bf16 activations take the decoded
+    weight times 2^(255 - 127): the scale bit and the non-finite bit are
+    raised, the non-finite outputs of column 77 are left unwritten, and
+    every other output of both experts matches the oracle."""
+    import torch
+
+    from pih_amd import linear
+
+    n, k, heavy, light = 2048, 4096, 300, 40
+    m = heavy + light
+    x = synth.bf16_normal(synth.config_seed(5, 970), (m, k))
+    packed = np.empty((2, n, k // 2), np.uint8)
+    sw = np.empty((2, n, k // 32), np.uint8)
+    for e in range(2):
+        packed[e], sw[e] = synth.mxfp4_weight(synth.config_seed(5, 971 + e), n, k)
+    sw[0, 77, 9] = 0xFF
+    off = np.array([0, heavy, m], np.uint32)
+    sentinel = 0x1234
+    out = torch.full((m, n), sentinel, dtype=torch.int16, device="cuda").view(torch.bfloat16)
+    out, flag = linear.moe_mxfp4_gemm(to_dev(x), None, None, to_dev(packed), to_dev(sw), to_dev(off), m,
+                                      abi.ACTIVATION_BF16, abi.OUTPUT_BF16, out=out)
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 6
+    bits = to_host(out).view(np.uint16)
+    got = oracle.bf16_bits_to_f32(bits)
+    cols = np.r_[0:77, 78:n]
+    rows = np.array([0, 1, 127, 128, 255, 256, 299])
+    sw0 = sw[0].copy()
+    sw0[77, 9] = 127  # the oracle rejects a 0xFF scale; column 77 is not compared
+    ref = oracle.mxfp4_bf16_gemm(np.ascontiguousarray(x[rows]), packed[0], sw0)
+    assert_close(got[rows][:, cols], ref[:, cols], "bf16 moe fp4, other columns")
+    col = bits[:heavy, 77]
+    assert ((col == sentinel) | ~np.isfinite(oracle.bf16_bits_to_f32(col))).all()
+    lrows = np.arange(heavy, m, 7)
+    ref_l = oracle.mxfp4_bf16_gemm(np.ascontiguousarray(x[lrows]), packed[1], sw[1])
+    assert_close(got[lrows], ref_l, "light expert")
