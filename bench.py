@@ -259,6 +259,7 @@ def bench_decode(torch, iters: int):
     (host launch cost included) and replayed from a captured HIP graph."""
     from pih_amd import abi
     from pih_amd.device import ptr, stream_handle
+    from pih_amd.linear import bf16_gemm_workspace
 
     L = abi.linear_pack()
     dev = torch.device("cuda")
@@ -372,9 +373,13 @@ def bench_decode(torch, iters: int):
     m = 2048
     xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for k in (4096, 12288)}
     ys = [torch.empty(m, n, dtype=torch.bfloat16, device=dev) for _, n, _ in QWEN8B]
+    # the workspace each projection queries (a K split of the projections
+    # with fewer tiles than CUs), allocated once like a caller's scratch
+    wsb = [bf16_gemm_workspace(m, n, k) for _, n, k in QWEN8B]
+    scratch = torch.empty(max(wsb) or 1, dtype=torch.uint8, device=dev)
     reqs = [abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xs[k]), w_bf16=ptr(wsets[0][j]), output=ptr(ys[j]),
-                        workspace=0, workspace_bytes=0, stream=stream_handle(), m=m, n=n, k=k,
-                        output_type=abi.OUTPUT_BF16) for j, (_, n, k) in enumerate(QWEN8B)]
+                        workspace=ptr(scratch) if wsb[j] else 0, workspace_bytes=wsb[j], stream=stream_handle(),
+                        m=m, n=n, k=k, output_type=abi.OUTPUT_BF16) for j, (_, n, k) in enumerate(QWEN8B)]
 
     def run_prefill(i):
         for r in reqs:

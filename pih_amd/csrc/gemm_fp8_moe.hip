@@ -111,6 +111,11 @@ struct MoeParams {
   // takes them); 0 takes every expert
   uint32_t light_rows;
   uint64_t out_row_stride;
+  // dense: > 1 splits K into this many equal parts, each a problem of its
+  // own (problem q: K steps [q KB / k_splits, (q + 1) KB / k_splits), the
+  // same A rows and W; its fp32 partial sums at output column offset
+  // q * out_prob_col); 0 or 1 otherwise
+  uint32_t k_splits;
   uint32_t n_tiles;
   uint32_t vb_end;  // blocks of the one-block-per-tile grid; persistent blocks walk no further
   float limit;
@@ -424,7 +429,12 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // a K step is 128 bytes of an A row: 128 e4m3 or 64 bf16 values (bf16 x
   // FP4: 256 bytes, 128 values), and 64 bytes of an FP4 W row
   constexpr bool kBf = OP == kOpBf16;
-  const uint32_t K = p.k, RB = kBf || kBF4 ? 2 * K : K, KB = kBF4 ? K / 128 : RB / 128, RBW = kW4 ? K / 2 : RB;
+  const uint32_t K = p.k, RB = kBf || kBF4 ? 2 * K : K, KBt = kBF4 ? K / 128 : RB / 128, RBW = kW4 ? K / 2 : RB;
+  // K steps per tile (a K split's share with dense k_splits: bf16 only, so
+  // that the other operand kinds carry no split state in their registers)
+  constexpr bool kSplitOk = kBf;
+  const bool ksplit = kSplitOk && p.dense_m_tiles && p.k_splits > 1;
+  const uint32_t KB = ksplit ? KBt / p.k_splits : KBt;
   uint32_t bad = 0;
 
   [[maybe_unused]] MoeTable tab{};
@@ -500,11 +510,14 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     const uint8_t* w_base;        // the expert's (problem's) W
     const uint8_t* s_src;         // this lane's scale source at k step 0
     uint64_t ws_off[2];           // the tile's two W scale blocks (entries)
+    uint32_t kb0;                 // the tile's first K step (its K split's)
   };
   // A: a_rows_total rows and W: n rows per expert stay below 2^32 bytes,
   // which the launcher checks
   auto make_ops = [&](uint32_t e, uint32_t r0, uint32_t rs, uint32_t t, Ops& o) __attribute__((always_inline)) {
-    o.w_base = p.w + (uint64_t)e * p.n * RBW;
+    o.w_base = ksplit ? p.w : p.w + (uint64_t)e * p.n * RBW;
+    if constexpr (kSplitOk) o.kb0 = ksplit ? e * KB : 0u;
+    else o.kb0 = 0u;
     // the tile's two 128-row W scale blocks (SwiGLU: gate block, up block)
     uint32_t wblk0, wblk1;
     if constexpr (kSwi) {
@@ -514,8 +527,9 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       wblk0 = min(2 * t, p.n / 128 - 1);
       wblk1 = min(2 * t + 1, p.n / 128 - 1);
     }
-    o.ws_off[0] = ((uint64_t)e * (p.n / 128) + wblk0) * KB;
-    o.ws_off[1] = ((uint64_t)e * (p.n / 128) + wblk1) * KB;
+    const uint32_t we = ksplit ? 0u : e;
+    o.ws_off[0] = ((uint64_t)we * (p.n / 128) + wblk0) * KBt;
+    o.ws_off[1] = ((uint64_t)we * (p.n / 128) + wblk1) * KBt;
     if constexpr (kBF4) {
       // 256-byte rows: instruction i lands rows 16 wv + 4 i + (l >> 4), slot
       // l & 15, which holds chunk (l & 15) ^ (row & 15)
@@ -559,14 +573,14 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
         o.s_src = static_cast<const uint8_t*>(p.w_scale) + ((uint64_t)e * p.n + w_row(R, t)) * (K / 32);
       } else if (kF4 && wv < 2) {
         const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2), e, r0, rs);
-        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB;
+        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KBt;
       } else {
         o.s_src = static_cast<const uint8_t*>(p.w_scale);
       }
     } else if constexpr (!kBf) {
       if (wv < 2) {
         const uint64_t src = a_source(64 * wv + (lane & 3) * 16 + (lane >> 2), e, r0, rs);
-        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KB * ESZ;
+        o.s_src = static_cast<const uint8_t*>(p.a_scale) + src * KBt * ESZ;
       } else {
         o.s_src = static_cast<const uint8_t*>(p.w_scale) + ((lane & 1) ? o.ws_off[1] : o.ws_off[0]) * ESZ;
       }
@@ -585,8 +599,8 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // (kNW), then the scale dword (none for bf16).  issue_part issues load
   // `part` alone (parts past the last do nothing), issue all of them.
   constexpr int kNA = kBF4 ? 4 : 2, kNW = kW4 ? 2 : 4, kNLoads = kNA + kNW + (kBf ? 0 : 1);
-  auto issue_part = [&](uint32_t stage, uint32_t kb, const Ops& o, auto NT, int part) __attribute__((always_inline)) {
-    const uint32_t base = lds0 + stage * STG;
+  auto issue_part = [&](uint32_t stage, uint32_t kbl, const Ops& o, auto NT, int part) __attribute__((always_inline)) {
+    const uint32_t base = lds0 + stage * STG, kb = kSplitOk ? kbl + o.kb0 : kbl;
     if (part < kNA) {
       dma16(uniform_ptr(p.a + (uint64_t)kb * A_ROW), o.a_off[part], base + a_lds + part * 1024);
     } else if (part < kNA + kNW) {
@@ -639,7 +653,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       a_byte0[r] = (uint32_t)((reinterpret_cast<uintptr_t>(p.a_scale) +
-                               a_source(wm * 64 + r * 16 + lr, expert, row0, rows) * KB) &
+                               a_source(wm * 64 + r * 16 + lr, expert, row0, rows) * KBt) &
                               3u);
     w_byte0[0] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + cur.ws_off[0]) & 3u);
     w_byte0[1] = (uint32_t)((reinterpret_cast<uintptr_t>(p.w_scale) + cur.ws_off[1]) & 3u);
@@ -959,11 +973,12 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     const uint32_t ist = PERSIST ? ((J) % 3 == 0 ? st2 : (J) % 3 == 1 ? st0 : st1) : ((J) + NS - 1) % NS; \
     const uint32_t cst = PERSIST ? ((J) % 3 == 0 ? st0 : (J) % 3 == 1 ? st1 : st2) : (J) % NS;       \
     const uint32_t kbl = PERSIST ? j + 2 : min(j + NS - 1, last);                                    \
+    const uint32_t jg = kSplitOk ? j + cur.kb0 : j; /* the step's index in the whole K */             \
     if constexpr (decltype(FULL)::value) {                                                           \
-      compute(cst, j, FULL, [&](int q) { issue_part(ist, kbl, cur, NT, q); });                       \
+      compute(cst, jg, FULL, [&](int q) { issue_part(ist, kbl, cur, NT, q); });                     \
     } else {                                                                                         \
       issue(ist, kbl, cur, NT);                                                                      \
-      compute(cst, j, FULL, [](int) {});                                                             \
+      compute(cst, jg, FULL, [](int) {});                                                            \
     }                                                                                                \
   }
       uint32_t kb = 0;
@@ -1014,14 +1029,14 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
         const uint32_t sj = (rot + j) % 3;
         __builtin_amdgcn_s_waitcnt(kWaitStep);
         __builtin_amdgcn_s_barrier();
-        const uint32_t ist = sj == 0 ? 2u : sj - 1, kbl = has_next ? f : last;
+        const uint32_t ist = sj == 0 ? 2u : sj - 1, kbl = has_next ? f : last, jg = kSplitOk ? j + cur.kb0 : j;
         // (the UE8M0 FP8 tail issues its loads at the top: interleaved they
         // made the persistent UE8M0 kernels spill)
         if constexpr (decltype(FULL)::value && !(OP == kOpFp8 && SCALE == kScaleUe8m0)) {
-          compute(sj, j, FULL, [&](int q) { issue_part(ist, kbl, nxt, std::false_type{}, q); });
+          compute(sj, jg, FULL, [&](int q) { issue_part(ist, kbl, nxt, std::false_type{}, q); });
         } else {
           issue(ist, kbl, nxt, std::false_type{});
-          compute(sj, j, FULL, [](int) {});
+          compute(sj, jg, FULL, [](int) {});
         }
       }
     }
@@ -1537,6 +1552,10 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   if (a.out_kind != kOutBf16 && a.out_kind != kOutF32) return Invalid("big_tile_gemm_output_type_invalid");
   if (a.problems == 0) return Invalid("big_tile_gemm_shape_invalid");
   const uint64_t rb = bf ? 2ull * a.k : a.k;
+  // K split: one problem, fp32 partial sums, whole K steps of at least 4 per split
+  const uint32_t splits = a.k_splits > 1 ? a.k_splits : 1u, ksteps = (uint32_t)(rb / 128);
+  if (splits > 1 && (a.problems != 1 || a.out_kind != kOutF32 || ksteps % splits || ksteps / splits < 4))
+    return Invalid("big_tile_gemm_split_invalid");
   const uint64_t a_rows = a.a_rows_total ? a.a_rows_total : (uint64_t)a.m * a.problems;
   // the tile loads address A and one problem's W by 32-bit byte offsets
   if (a_rows > 0xffffffffull || a_rows * rb > 0xffffffffull || (uint64_t)a.n * rb > 0xffffffffull)
@@ -1551,13 +1570,14 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.m = a.m;
   mp.n = a.n;
   mp.k = a.k;
-  mp.experts = a.problems;
+  mp.experts = splits > 1 ? splits : a.problems;
+  mp.k_splits = splits;
   mp.a_rows_total = (uint32_t)a_rows;
   mp.dense_m_tiles = (a.m + BM - 1) / BM;
   mp.a_row_stride = a.a_row_stride;
   mp.a_prob_row = a.a_prob_row;
   mp.out_row_stride = a.out_row_stride ? a.out_row_stride : a.n;
-  mp.out_prob_col = a.out_prob_col;
+  mp.out_prob_col = splits > 1 ? (uint64_t)a.m * mp.out_row_stride : a.out_prob_col;
   mp.n_tiles = (a.n + BN - 1) / BN;
   mp.stage_out = StageOut(a.out, mp.out_row_stride, mp.out_prob_col, a.out_kind);
   mp.err_code = a.error_flag ? a.err_code_bit : 0u;
@@ -1566,9 +1586,9 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.write_nonfinite = a.write_nonfinite ? 1u : 0u;
   mp.skip_if = a.skip_if;
   mp.skip_bit = a.skip_bit;
-  const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles * a.problems;
+  const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles * mp.experts;
   if (total > 0x7fffffffull - 8) return Invalid("big_tile_gemm_grid_too_large");
-  const bool persist = Persistent(a.out_kind, false, true, a.problems, mp.out_row_stride, (uint32_t)(rb / 128));
+  const bool persist = Persistent(a.out_kind, false, true, mp.experts, mp.out_row_stride, ksteps / splits);
   uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
   mp.vb_end = grid;
   if (persist) grid = std::min(grid, PersistentBlocks());
@@ -1578,6 +1598,55 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   else if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind, persist);
   else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
   return AfterLaunch("big_tile_gemm_launch_failed");
+}
+
+// ------------------------------------------------ K-split partial-sum reduce
+namespace {
+
+// out[i] = (((ws[0][i] + ws[1][i]) + ws[2][i]) + ...) over `splits` slabs of
+// `slab` floats, four per thread; bf16 (round to nearest even) or fp32
+// stores; a non-finite result is stored and raises `bit` when err is set
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, uint32_t splits, uint64_t slab,
+                                                            uint64_t quads, void* out, uint32_t out_f32, uint32_t* err,
+                                                            uint32_t bit) {
+  bool bad = false;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < quads; i += (uint64_t)gridDim.x * blockDim.x) {
+    v4f s = *reinterpret_cast<const v4f*>(ws + 4 * i);
+    for (uint32_t q = 1; q < splits; ++q) s += *reinterpret_cast<const v4f*>(ws + q * slab + 4 * i);
+    bad |= !(__builtin_isfinite(s[0]) && __builtin_isfinite(s[1]) && __builtin_isfinite(s[2]) && __builtin_isfinite(s[3]));
+    if (out_f32) {
+      *reinterpret_cast<v4f*>(static_cast<float*>(out) + 4 * i) = s;
+    } else {
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + 4 * i) =
+          uint2{f32x2_to_bf16x2(s[0], s[1]), f32x2_to_bf16x2(s[2], s[3])};
+    }
+  }
+  if (err && __builtin_amdgcn_ballot_w64(bad) && (threadIdx.x & 63) == 0) atomicOr(err, bit);
+}
+
+}  // namespace
+
+uint32_t DenseKSplits(uint32_t m, uint32_t n, uint32_t k_steps) {
+  // a split is worth it below one 128 x 256 tile per CU (256 CUs); the
+  // smallest split count that reaches a full round, with at least 8 K steps
+  // per split
+  const uint64_t tiles = (uint64_t)((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  if (tiles == 0 || tiles >= 192) return 1;
+  for (uint32_t s = 2; s <= 8; ++s)
+    if (k_steps % s == 0 && k_steps / s >= 8 && tiles * s >= 192) return s;
+  return 1;
+}
+
+St LaunchSplitKReduce(const float* ws, uint32_t splits, uint32_t m, uint32_t n, void* out, OutKind out_kind,
+                      uint32_t* err, uint32_t bit, hipStream_t stream) {
+  if (!ws || !out || !stream || splits < 2 || m == 0 || n == 0 || n % 4) return Invalid("split_k_reduce_invalid");
+  const uint64_t count = (uint64_t)m * n, quads = count / 4;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>((quads + 255) / 256, 4096);
+  St s = RequireCleanLastError();
+  if (!s.ok()) return s;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, stream, ws, splits, count, quads, out,
+                     out_kind == kOutF32 ? 1u : 0u, err, bit);
+  return AfterLaunch("split_k_reduce_launch_failed");
 }
 
 }  // namespace pih_amd

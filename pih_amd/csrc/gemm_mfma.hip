@@ -925,6 +925,22 @@ St LaunchBf16Gemm(const Bf16GemmArgs& a) {
       b.err_nonfinite_bit = a.nonfinite_bit;
     }
     b.write_nonfinite = true;
+    // fewer tiles than CUs: K split into fp32 partial sums in the caller's
+    // workspace (sized by Bf16GemmWorkspaceBytes), then summed in split order
+    const uint32_t splits = DenseKSplits(a.m, a.n, a.k / 64);
+    const uint64_t ws_bytes = (uint64_t)splits * a.m * a.n * 4;
+    if (splits > 1 && a.workspace && a.workspace_bytes >= ws_bytes && reinterpret_cast<uintptr_t>(a.workspace) % 16 == 0) {
+      BigTileArgs p = b;
+      p.out = a.workspace;
+      p.out_kind = kOutF32;
+      p.out_row_stride = a.n;
+      p.k_splits = splits;
+      p.error_flag = nullptr;
+      St s = LaunchBigTileGemm(p);
+      if (!s.ok()) return s;
+      return LaunchSplitKReduce(static_cast<const float*>(a.workspace), splits, a.m, a.n, a.out, a.out_kind,
+                                b.error_flag, b.err_nonfinite_bit, a.stream);
+    }
     return LaunchBigTileGemm(b);
   }
   GemmParams gp{};
@@ -975,7 +991,12 @@ St LaunchMx32Gemm(const Mx32GemmArgs& a) {
 }
 
 uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k) {
-  return m <= 64 ? Bf16GemvWorkspaceBytes(m, n, k) : 0;
+  if (m <= 64) return Bf16GemvWorkspaceBytes(m, n, k);
+  // the big tiles' K split (fp32 partial sums); without this workspace the
+  // call runs unsplit
+  if (n % 128 || k % 64 || !BigTileWorthIt(m, n)) return 0;
+  const uint32_t splits = DenseKSplits(m, n, k / 64);
+  return splits > 1 ? (uint64_t)splits * m * n * 4 : 0;
 }
 
 }  // namespace pih_amd

@@ -174,8 +174,18 @@ struct BigTileArgs {
   // when set, every block exits at once if (*skip_if & skip_bit) != 0
   const uint32_t* skip_if = nullptr;
   uint32_t skip_bit = 0;
+  // > 1: one problem with K split into this many equal parts; `out` then
+  // holds k_splits fp32 slabs [m][out_row_stride] of partial sums, summed
+  // by LaunchSplitKReduce (out_kind kOutF32)
+  uint32_t k_splits = 1;
 };
 St LaunchBigTileGemm(const BigTileArgs& a);
+// K splits for a dense big-tile GEMM of k_steps 128-byte K steps (1: none):
+// below a round of tiles on the 256 CUs
+uint32_t DenseKSplits(uint32_t m, uint32_t n, uint32_t k_steps);
+// out[m, n] = sum over the splits in order of ws[q][m][n] (bf16 or fp32)
+St LaunchSplitKReduce(const float* ws, uint32_t splits, uint32_t m, uint32_t n, void* out, OutKind out_kind,
+                      uint32_t* err, uint32_t bit, hipStream_t stream);
 
 // ORs `bit` into *error_flag when A or W holds an e4m3 NaN code (0x7F or
 // 0xFF byte) -- the test the big-tile FP8 path runs before it trusts the

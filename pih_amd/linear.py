@@ -44,6 +44,16 @@ def route_plan_workspace(tokens: int, topk: int, experts: int) -> int:
     return int(out[0])
 
 
+def bf16_gemm_workspace(m: int, n: int, k: int) -> int:
+    """Scratch bytes launch_bf16_gemm can use at this shape (query_workspace;
+    0: none)."""
+    out = (abi.C.c_uint64 * 1)()
+    q = abi.request(abi.LN["workspace_query"], kind=abi.WORKSPACE_BF16_GEMM, m=m, n=n, k=k,
+                    bytes_u64=abi.C.addressof(out))
+    _check(_ln().call("query_workspace", q), "query_workspace")
+    return int(out[0])
+
+
 def route_plan(topk_ids: torch.Tensor, topk_weights: torch.Tensor, experts: int,
                flag: Optional[torch.Tensor] = None):
     """Returns (expert_offsets [E+1], row_token [R], row_weight [R],
@@ -186,8 +196,11 @@ def bf16_gemm(a: torch.Tensor, w: torch.Tensor, output_type: int = abi.OUTPUT_BF
     if out is None:
         out = torch.empty(m, n, dtype=torch.bfloat16 if output_type == abi.OUTPUT_BF16 else torch.float32,
                           device=a.device)
-    r = abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(a), w_bf16=ptr(w), output=ptr(out), workspace=0,
-                    workspace_bytes=0, stream=stream_handle(), m=m, n=n, k=k, output_type=output_type)
+    wsb = bf16_gemm_workspace(m, n, k)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=a.device) if wsb else None
+    r = abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(a), w_bf16=ptr(w), output=ptr(out),
+                    workspace=ptr(ws) if ws is not None else 0, workspace_bytes=wsb, stream=stream_handle(),
+                    m=m, n=n, k=k, output_type=output_type)
     _check(_ln().call("launch_bf16_gemm", r), "bf16_gemm")
     return out
 

@@ -162,6 +162,65 @@ def test_bf16_gemm_big_tile(eng, m, n, k, out_type):
     assert_close(got[rows], ref, f"big-tile bf16 {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 1024, 4096), (1000, 2048, 4096), (2048, 1280, 4608)])
+@pytest.mark.parametrize("out_type", [abi.OUTPUT_BF16, abi.OUTPUT_F32])
+def test_bf16_gemm_k_split(eng, m, n, k, out_type):
+    """launch_bf16_gemm with the queried workspace at shapes with fewer big
+    tiles than CUs (the Qwen3-8B k/v projections at M 2048: 4 K splits; M
+    1000: a partial M tile; 4608 -> 1280: 3 splits): the fp32 partial sums go to the
+    workspace (filled with NaN bytes first, so an element no split writes
+    would show) and are summed in split order.  Sampled rows against the
+    oracle, every row's sum against a float64 checksum, and the whole output
+    against the unsplit launch (workspace 0) within the fp32 reordering of
+    the K sum (bf16: one unit in the last place)."""
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    x = synth.bf16_normal(synth.config_seed(5, 700 + m), (m, k))
+    w = synth.bf16_normal(synth.config_seed(5, 701 + n), (n, k), std=0.02)
+    xd, wd = to_dev(x), to_dev(w)
+    cnt = (abi.C.c_uint64 * 1)()
+    qr = abi.request(abi.LN["workspace_query"], kind=abi.WORKSPACE_BF16_GEMM, m=m, n=n, k=k,
+                     bytes_u64=abi.C.addressof(cnt))
+    assert abi.linear_pack().call("query_workspace", qr).code == abi.OK
+    wsb = int(cnt[0])
+    assert wsb > 0 and wsb % (m * n * 4) == 0
+    ws = torch.full((wsb,), 0xFF, dtype=torch.uint8, device="cuda")
+    dt = torch.bfloat16 if out_type == abi.OUTPUT_BF16 else torch.float32
+
+    def run(use_ws):
+        out = torch.empty(m, n, dtype=dt, device="cuda")
+        r = abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(xd), w_bf16=ptr(wd), output=ptr(out),
+                        workspace=ptr(ws) if use_ws else 0, workspace_bytes=wsb if use_ws else 0,
+                        stream=stream_handle(), m=m, n=n, k=k, output_type=out_type)
+        st = abi.linear_pack().call("launch_bf16_gemm", r)
+        assert st.code == abi.OK, st
+        torch.cuda.synchronize()
+        host = to_host(out)
+        return oracle.bf16_bits_to_f32(host) if out_type == abi.OUTPUT_BF16 else host
+
+    split, whole = run(True), run(False)
+    assert np.all(np.isfinite(split))
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 24).astype(np.int64), [127, 128, m - 1]]))
+    ref = oracle.bf16_gemm(np.ascontiguousarray(x[rows]), w)
+    assert_close(split[rows], ref, f"k-split bf16 {m}x{n}x{k}")
+    colsum = oracle.bf16_bits_to_f32(w).astype(np.float64).sum(axis=0)
+    want = oracle.bf16_bits_to_f32(x).astype(np.float64) @ colsum
+    have = split.astype(np.float64).sum(axis=1)
+    bound = np.abs(split).astype(np.float64).sum(axis=1) * 2.0 ** -8 + 1e-3
+    assert np.all(np.abs(have - want) <= bound), "k-split row checksums"
+    if out_type == abi.OUTPUT_F32:
+        # fp32 sums of the same products in two orders (outputs ~1.3 rms)
+        assert np.all(np.abs(split - whole) <= 2e-5 + np.abs(whole) * 1e-5)
+    else:
+        # one bf16 rounding each of two fp32 sums that differ in the order of
+        # their K parts (~1e-6 here): one unit in the last place, plus slack
+        # for results that cancel to near zero
+        ulp = np.maximum(np.abs(whole), np.abs(split)) * 2.0 ** -7 + 1e-4
+        assert np.all(np.abs(split - whole) <= ulp)
+
+
 def test_big_tile_nonfinite_results_skipped(eng):
     """Sums that overflow (UE8M0 weight scale 2^127 on one 128-row block)
     raise bit 4 and leave their elements unwritten, as the reference's

@@ -196,6 +196,33 @@ def test_linear_entries_reject_bad_requests():
     assert ln.call("query_workspace", w).code == abi.INVALID_ARGUMENT
 
 
+def test_bf16_gemm_workspace_sizes():
+    """launch_bf16_gemm's scratch (query_workspace, host only): a K split of
+    the big tiles when a GEMM has fewer 128 x 256 tiles than about a round on
+    the 256 CUs -- 4 fp32 partial-sum slabs for M 2048, 4096 -> 1024 (64
+    tiles, 64 K steps of 64) and M 1000, 4096 -> 2048; 3 for M 2048,
+    4608 -> 1280 (80 tiles, 72 K steps) -- and none for a full round
+    (4096 -> 4096: 256 tiles), decode shapes (m <= 64), shapes below the big
+    tiles (M 1000, 4096 -> 1024: 32 tiles) or K too short to split (at least
+    8 K steps per split)."""
+    ln = abi.linear_pack()
+    out = (C.c_uint64 * 1)()
+
+    def q(m, n, k):
+        w = abi.request(abi.LN["workspace_query"], kind=abi.WORKSPACE_BF16_GEMM, m=m, n=n, k=k,
+                        bytes_u64=C.addressof(out))
+        assert ln.call("query_workspace", w).code == abi.OK
+        return int(out[0])
+
+    assert q(2048, 1024, 4096) == 4 * 2048 * 1024 * 4
+    assert q(1000, 2048, 4096) == 4 * 1000 * 2048 * 4
+    assert q(2048, 1280, 4608) == 3 * 2048 * 1280 * 4
+    assert q(2048, 4096, 4096) == 0
+    assert q(64, 1024, 4096) == 0
+    assert q(1000, 1024, 4096) == 0
+    assert q(2048, 1024, 512) == 0
+
+
 def test_w4a16_grouped_rejects_bad_groups():
     """Group validation happens before any device work: count 0 or above 8,
     a NULL problem array, n not a multiple of 16 or a missing zeros pointer
