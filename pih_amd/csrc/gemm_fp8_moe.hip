@@ -754,11 +754,20 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       // results that finished while the next MFMAs ran (consuming a result
       // right after its MFMA stalls the wave for the MFMA's latency).
       const float fw0 = __uint_as_float(sw0), fw1 = __uint_as_float(sw1);
-      auto mfma4 = [&](const v8i& af, v4f (&t)[4]) __attribute__((always_inline)) {
+      // group `slot` of four MFMAs issues loads 2 slot and 2 slot + 1 after
+      // its second and fourth MFMA (one load per two MFMAs ran 0-2 % faster
+      // than one per group of four)
+      auto mfma4 = [&](const v8i& af, v4f (&t)[4], int slot) __attribute__((always_inline)) {
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int nb = 0; nb < 4; ++nb) {
           t[nb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[nb], af, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
                                                                    127, 0, 127);
+          if (nb & 1) {
+            __builtin_amdgcn_sched_barrier(0);
+            dmas(2 * slot + (nb >> 1));
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
       };
       auto fma4 = [&](int r, const v4f (&t)[4]) __attribute__((always_inline)) {
         const float sa = __uint_as_float((uint32_t)sa4[r]);
@@ -773,30 +782,22 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       // A fragments are read one block ahead
       v4f tA[4], tB[4];
       v8i af = a_frag(0), afn = a_frag(1);
-      mfma4(af, tA);
+      mfma4(af, tA, 0);
       __builtin_amdgcn_sched_barrier(0);
-      dmas(0);
       af = a_frag(2);
-      if (live(1)) mfma4(afn, tB);
+      if (live(1)) mfma4(afn, tB, 1);
       __builtin_amdgcn_sched_barrier(0);
-      dmas(1);
       fma4(0, tA);
       afn = a_frag(3);
       __builtin_amdgcn_sched_barrier(0);
-      dmas(2);
-      if (live(2)) mfma4(af, tA);
+      if (live(2)) mfma4(af, tA, 2);
       __builtin_amdgcn_sched_barrier(0);
-      dmas(3);
       if (live(1)) fma4(1, tB);
       __builtin_amdgcn_sched_barrier(0);
-      dmas(4);
-      if (live(3)) mfma4(afn, tB);
+      if (live(3)) mfma4(afn, tB, 3);
       __builtin_amdgcn_sched_barrier(0);
-      dmas(5);
       if (live(2)) fma4(2, tA);
       __builtin_amdgcn_sched_barrier(0);
-      dmas(6);
-      dmas(7);
       if (live(3)) fma4(3, tB);
     } else if constexpr (kBF4) {
       // bf16 A against MXFP4 W: 4 x 4 x 4 MFMAs 16x16x32 bf16 per step.
