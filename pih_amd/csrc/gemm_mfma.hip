@@ -871,7 +871,10 @@ St LaunchFp4Gemm(const Fp4GemmArgs& a) {
   uint32_t grid;
   St s = prepare(gp, grid, a.m, a.n, a.k, a.problems, a.moe, a.out_kind, 0, a.moe ? Fp4MoeLightRows(a) : 0);
   if (!s.ok()) return s;
-  if (grid) {
+  // every expert within the streaming kernel's rows (a caller's bound): no
+  // tiled launch, whose tile scan alone costs ~4-5 us
+  const bool all_light = a.moe && a.max_expert_rows && a.max_expert_rows <= Fp4MoeLightRows(a);
+  if (grid && !all_light) {
     // The 128 x 256 FP4 tiles and the streaming kernel run one after the
     // other: a big-tile block needs most of a CU's LDS and cannot start on
     // a CU the streaming blocks hold, so forked they overlapped worse than

@@ -100,6 +100,11 @@ struct Fp4GemmArgs {
   ActKind act = kActE4m3;
   OutKind out_kind = kOutBf16;
   float swiglu_limit = 0.0f;
+  // MoE: a bound on every expert's row count that the caller guarantees (0:
+  // none).  The layer passes its token count (the route plan gives an
+  // expert at most one row per token); at or below the light-expert limit
+  // no expert can need the tiled kernels, so they are not launched.
+  uint32_t max_expert_rows = 0;
 };
 St LaunchFp4Gemm(const Fp4GemmArgs& a);
 

@@ -193,6 +193,7 @@ St LaunchMoeLayer(const MoeLayerArgs& a) {
     g.act = a.act;
     g.out_kind = gate_up ? kOutSwiGlu : kOutBf16;
     g.swiglu_limit = a.swiglu_limit;
+    g.max_expert_rows = a.tokens;  // the route plan's rows: at most one per token and expert
     return LaunchFp4Gemm(g);
   };
   if (!(s = gemm(true)).ok()) return s;

@@ -113,6 +113,85 @@ __global__ __launch_bounds__(256) void route_mask_quant_kernel(const uint32_t* i
   if (bad) atomicOr(err, bad);
 }
 
+// A plan of at most 64 tokens (one chunk) in one launch: block 0 builds the
+// chunk's expert masks in LDS, scans their popcounts into the expert offsets
+// (256 threads, 4 experts each) and places every route at offset +
+// popcount(mask & lanes below) -- the three-launch plan's arithmetic with its
+// only chunk base 0, so the same rows -- and, with QFMT >= 0, the blocks after
+// it quantize the token activations as route_mask_quant_kernel's do.
+template <int QFMT>
+__global__ __launch_bounds__(256) void route_plan_one_chunk_kernel(
+    const uint32_t* ids, const float* weights, uint32_t* offsets, uint32_t* row_token, float* row_weight,
+    uint32_t* token_rows, uint32_t* err, uint32_t tokens, uint32_t topk, uint32_t experts, const uint16_t* x,
+    uint8_t* codes, void* scales, uint32_t hidden) {
+  extern __shared__ unsigned long long s_mask[];  // [experts] masks, then [experts] u32 offsets
+  __shared__ uint32_t s_wave[4];
+  if (blockIdx.x != 0) {
+    if constexpr (QFMT >= 0) {
+      const uint64_t seg0 = ((uint64_t)(blockIdx.x - 1) * blockDim.x + threadIdx.x) >> 4;
+      const uint64_t seg_step = ((uint64_t)(gridDim.x - 1) * blockDim.x) >> 4;
+      const uint32_t bad = quant_groups<QFMT, false>(x, nullptr, codes, scales, tokens, hidden, tokens, seg0, seg_step);
+      if (bad) atomicOr(err, bad);
+    }
+    return;
+  }
+  uint32_t* s_off = reinterpret_cast<uint32_t*>(s_mask + experts);
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (uint32_t e = tid; e < experts; e += 256) s_mask[e] = 0ull;
+  __syncthreads();
+  uint32_t bad = 0;
+  if (lane < tokens) {
+    for (uint32_t j = wave; j < topk; j += 4) {
+      const uint32_t e = route_expert(ids, weights, lane, j, topk, experts, bad);
+      if (e != kNoRow) atomicOr(&s_mask[e], 1ull << lane);
+    }
+  }
+  if (bad) atomicOr(err, bad);
+  __syncthreads();
+  // exclusive scan of the popcounts: thread tid owns experts [4 tid, 4 tid + 4)
+  uint32_t pc[4], sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t e = 4 * tid + i;
+    pc[i] = e < experts ? (uint32_t)__popcll(s_mask[e]) : 0u;
+    sum += pc[i];
+  }
+  uint32_t incl = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = __shfl_up(incl, o, 64);
+    if ((int)lane >= o) incl += v;
+  }
+  if (lane == 63) s_wave[wave] = incl;
+  __syncthreads();
+  uint32_t run = incl - sum;
+  for (uint32_t w = 0; w < wave; ++w) run += s_wave[w];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t e = 4 * tid + i;
+    if (e < experts) {
+      s_off[e] = run;
+      offsets[e] = run;
+    }
+    run += pc[i];
+  }
+  if (tid == 255) offsets[experts] = run;  // the total, every expert counted
+  __syncthreads();
+  for (uint32_t r = tid; r < tokens * topk; r += 256) {
+    const uint32_t t = r / topk, j = r % topk;
+    uint32_t ignored = 0;  // reported above
+    const uint32_t e = route_expert(ids, weights, t, j, topk, experts, ignored);
+    uint32_t row = kNoRow;
+    if (e != kNoRow) {
+      const unsigned long long below = t ? (~0ull >> (64 - t)) : 0ull;
+      row = s_off[e] + (uint32_t)__popcll(s_mask[e] & below);
+      row_token[row] = t;
+      row_weight[row] = weights[r];
+    }
+    token_rows[r] = row;
+  }
+}
+
 // One block, one thread per expert: chunk bases by a walk over the chunks
 // (the masks of 16 chunks loaded before they are summed, so the walk waits
 // on memory once per 16 chunks), then a block-wide exclusive scan of the
@@ -360,6 +439,28 @@ St EnqueueRoutePlan(const RoutePlanArgs& a, const Fp8QuantArgs* quant) {
   const uint32_t lds = a.experts * 8u;
   St clean = RequireCleanLastError();
   if (!clean.ok()) return clean;
+  if (chunks == 1) {
+    // one chunk of tokens (decode batches): the whole plan in one launch
+    const uint32_t lds1 = a.experts * 12u;
+    if (!quant) {
+      hipLaunchKernelGGL(route_plan_one_chunk_kernel<-1>, dim3(1), dim3(256), lds1, a.stream, a.topk_ids,
+                         a.topk_weights, a.expert_offsets, a.row_token, a.row_weight, a.token_rows, a.error_flag,
+                         a.tokens, a.topk, a.experts, nullptr, nullptr, nullptr, 0u);
+    } else {
+      const uint32_t grid = 1 + QuantBlocks((uint64_t)quant->row_count * (quant->k / 128u));
+      if (quant->fmt == kScaleUe8m0)
+        hipLaunchKernelGGL(route_plan_one_chunk_kernel<kScaleUe8m0>, dim3(grid), dim3(256), lds1, a.stream,
+                           a.topk_ids, a.topk_weights, a.expert_offsets, a.row_token, a.row_weight, a.token_rows,
+                           a.error_flag, a.tokens, a.topk, a.experts, quant->input, quant->codes, quant->scales,
+                           quant->k);
+      else
+        hipLaunchKernelGGL(route_plan_one_chunk_kernel<kScaleF32>, dim3(grid), dim3(256), lds1, a.stream,
+                           a.topk_ids, a.topk_weights, a.expert_offsets, a.row_token, a.row_weight, a.token_rows,
+                           a.error_flag, a.tokens, a.topk, a.experts, quant->input, quant->codes, quant->scales,
+                           quant->k);
+    }
+    return AfterLaunch("route_plan_launch_failed");
+  }
   if (!quant) {
     hipLaunchKernelGGL(route_mask_kernel, dim3(chunks), dim3(256), lds, a.stream, a.topk_ids, a.topk_weights, masks,
                        a.error_flag, a.tokens, a.topk, a.experts);

@@ -207,8 +207,12 @@ def test_grouped_fp8_gemm_deepseek_table(eng):
 
 
 # ---------------------------------------------------------- route plan
-@pytest.mark.parametrize("tokens,experts,topk", [(1, 8, 2), (65, 16, 4), (4096, 256, 8), (300, 1024, 6)])
+@pytest.mark.parametrize("tokens,experts,topk", [(1, 8, 2), (64, 1024, 8), (33, 256, 6), (64, 256, 32), (65, 16, 4),
+                                                 (4096, 256, 8), (300, 1024, 6)])
 def test_route_plan_bit_exact(eng, tokens, experts, topk):
+    """The device route plan against the oracle, bit for bit: up to 64 tokens
+    the one-launch plan (one chunk: masks, offsets and rows in one block),
+    above it the three-launch plan."""
     from pih_amd import linear
 
     ids, wts = synth.zipf_router(synth.config_seed(4, 7000 + tokens), tokens, experts, topk)
