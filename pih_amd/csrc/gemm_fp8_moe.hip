@@ -101,6 +101,9 @@ struct MoeParams {
   // i * a_row_stride + q * a_prob_row, its output row starts at
   // i * out_row_stride + q * out_prob_col); 0 for MoE segments
   uint32_t dense_m_tiles;
+  // dense: rows per M tile (BM, or 64 / 32 for GEMMs with too few 128-row
+  // tiles to fill the CUs: the dead row blocks skip their MFMAs)
+  uint32_t dense_tile_rows;
   uint32_t a_row_stride, a_prob_row;
   uint64_t out_prob_col;
   uint32_t write_nonfinite;  // store a non-finite result (and flag it)
@@ -275,9 +278,9 @@ __device__ bool dense_tile(const MoeParams& p, uint32_t vb, uint32_t& prob, uint
   const uint32_t mg = (uint32_t)(t / ((uint64_t)kTableGroupM * NTL));
   const uint32_t gsize = min(kTableGroupM, MT - mg * kTableGroupM);
   const uint32_t r = (uint32_t)(t - (uint64_t)mg * kTableGroupM * NTL);
-  row0 = (mg * kTableGroupM + r % gsize) * BM;
+  row0 = (mg * kTableGroupM + r % gsize) * p.dense_tile_rows;
   nt = r / gsize;
-  rows = min((uint32_t)BM, p.m - row0);
+  rows = min(p.dense_tile_rows, p.m - row0);
   return true;
 }
 
@@ -1574,7 +1577,16 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   mp.experts = splits > 1 ? splits : a.problems;
   mp.k_splits = splits;
   mp.a_rows_total = (uint32_t)a_rows;
-  mp.dense_m_tiles = (a.m + BM - 1) / BM;
+  // fewer 128-row tiles than about a round on the CUs (and no K split):
+  // 64- or 32-row M tiles, up to four times the tiles at the same K depth
+  // (same arithmetic per element; the tiles stream their W tile from L2)
+  uint32_t tile_rows = BM;
+  if (splits == 1) {
+    const uint64_t nt = (a.n + BN - 1) / BN;
+    while (tile_rows > 32 && (uint64_t)((a.m + tile_rows - 1) / tile_rows) * nt * a.problems < 192) tile_rows /= 2;
+  }
+  mp.dense_tile_rows = tile_rows;
+  mp.dense_m_tiles = (a.m + tile_rows - 1) / tile_rows;
   mp.a_row_stride = a.a_row_stride;
   mp.a_prob_row = a.a_prob_row;
   mp.out_row_stride = a.out_row_stride ? a.out_row_stride : a.n;
