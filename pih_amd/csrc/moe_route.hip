@@ -17,6 +17,7 @@
 // Error bits: 1 expert id out of range, 2 expert repeated within a token,
 // 4 route weight non-finite or negative.  An invalid route gets no row
 // (token_rows = 0xffffffff) and is left out of the offsets.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -339,7 +340,10 @@ __global__ __launch_bounds__(512) void combine_kernel(const uint16_t* expert_out
   // are replaced by +0.0f, which leaves the sum unchanged (it starts at +0.0f
   // and so is never -0.0f), so the sum keeps the ascending row order exactly
   constexpr uint32_t kUnroll = 8;
-  for (uint32_t c = threadIdx.x; c < vec; c += blockDim.x) {
+  // block (t, y) covers part y of the row's chunks (few tokens: the rows are
+  // split over gridDim.y blocks so that every CU has one)
+  const uint32_t per = (vec + gridDim.y - 1) / gridDim.y, c_end = min(vec, (blockIdx.y + 1) * per);
+  for (uint32_t c = blockIdx.y * per + threadIdx.x; c < c_end; c += blockDim.x) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     auto add = [&](const uint4& x, bool live) {
       const uint32_t w[4] = {x.x, x.y, x.z, x.w};
@@ -583,12 +587,15 @@ St LaunchMoeCombine(const CombineArgs& a) {
     return Invalid("moe_combine_shape_invalid");
   St clean = RequireCleanLastError();
   if (!clean.ok()) return clean;
-  // one block per token; its threads cover the row's 16-byte chunks in
-  // equal passes (hidden 7168: 896 chunks = 2 passes of 448 threads, where
-  // 256 threads left the fourth pass half empty)
-  const uint32_t vec = a.hidden / 8u, passes = (vec + 511u) / 512u;
-  const uint32_t threads = ((vec + passes - 1) / passes + 63u) / 64u * 64u;
-  hipLaunchKernelGGL(combine_kernel, dim3(a.tokens), dim3(threads), 0, a.stream, a.expert_out,
+  // one block per token (below 256 tokens: per part of a token's row, up to
+  // a block per CU, at least 64 chunks each); its threads cover the part's
+  // 16-byte chunks in equal passes (hidden 7168: 896 chunks = 2 passes of
+  // 448 threads, where 256 threads left the fourth pass half empty)
+  const uint32_t vec = a.hidden / 8u;
+  const uint32_t parts = a.tokens < 256u ? std::min((256u + a.tokens - 1) / a.tokens, std::max(1u, vec / 64u)) : 1u;
+  const uint32_t pvec = (vec + parts - 1) / parts, passes = (pvec + 511u) / 512u;
+  const uint32_t threads = ((pvec + passes - 1) / passes + 63u) / 64u * 64u;
+  hipLaunchKernelGGL(combine_kernel, dim3(a.tokens, parts), dim3(threads), 0, a.stream, a.expert_out,
                      a.token_rows, a.shared, a.out, a.error_flag, a.tokens, a.topk, a.hidden,
                      a.rows);
   return AfterLaunch("moe_combine_launch_failed");

@@ -240,10 +240,14 @@ def test_route_plan_flags_bad_routes(eng):
 
 
 # -------------------------------------------------------------- combine
-def test_combine_bit_exact(eng):
+@pytest.mark.parametrize("tokens,hidden", [(200, 512), (64, 7168), (3, 4104), (1, 7168)])
+def test_combine_bit_exact(eng, tokens, hidden):
+    """The ordered combine + shared add, bit-exact against the oracle; below
+    256 tokens a token's row is split over several blocks (64 tokens x 7168:
+    4 parts; 3 x 4104: 8 ragged parts of 65 / 58 chunks; 1 token: 14)."""
     from pih_amd import linear
 
-    tokens, experts, topk, hidden = 200, 32, 4, 512
+    experts, topk = 32, 4
     ids, wts = synth.zipf_router(synth.config_seed(4, 8000), tokens, experts, topk)
     o, rt, rw, tr = oracle.route_plan(ids, wts, experts)
     y = synth.bf16_normal(synth.config_seed(4, 8001), (tokens * topk, hidden))
