@@ -1558,7 +1558,8 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   const uint64_t rb = bf ? 2ull * a.k : a.k;
   // K split: one problem, fp32 partial sums, whole K steps of at least 4 per split
   const uint32_t splits = a.k_splits > 1 ? a.k_splits : 1u, ksteps = (uint32_t)(rb / 128);
-  if (splits > 1 && (a.problems != 1 || a.out_kind != kOutF32 || ksteps % splits || ksteps / splits < 4))
+  if (splits > 1 && (a.problems != 1 || a.a_prob_row != 0 || a.out_kind != kOutF32 || ksteps % splits ||
+                     ksteps / splits < 4))
     return Invalid("big_tile_gemm_split_invalid");
   const uint64_t a_rows = a.a_rows_total ? a.a_rows_total : (uint64_t)a.m * a.problems;
   // the tile loads address A and one problem's W by 32-bit byte offsets

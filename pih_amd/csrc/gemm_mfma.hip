@@ -929,10 +929,14 @@ St LaunchBf16Gemm(const Bf16GemmArgs& a) {
     }
     b.write_nonfinite = true;
     // fewer tiles than CUs: K split into fp32 partial sums in the caller's
-    // workspace (sized by Bf16GemmWorkspaceBytes), then summed in split order
+    // workspace (sized by Bf16GemmWorkspaceBytes), then summed in split
+    // order; the reduce stores 8 or 16 bytes per lane, so the workspace and
+    // the output must start on 16-byte boundaries (torch allocations do)
     const uint32_t splits = DenseKSplits(a.m, a.n, a.k / 64);
     const uint64_t ws_bytes = (uint64_t)splits * a.m * a.n * 4;
-    if (splits > 1 && a.workspace && a.workspace_bytes >= ws_bytes && reinterpret_cast<uintptr_t>(a.workspace) % 16 == 0) {
+    const bool aligned =
+        reinterpret_cast<uintptr_t>(a.workspace) % 16 == 0 && reinterpret_cast<uintptr_t>(a.out) % 16 == 0;
+    if (splits > 1 && a.workspace && a.workspace_bytes >= ws_bytes && aligned) {
       BigTileArgs p = b;
       p.out = a.workspace;
       p.out_kind = kOutF32;
