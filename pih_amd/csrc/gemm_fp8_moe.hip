@@ -20,7 +20,9 @@
 //   * three LDS stages (149 KB), loads issued two steps ahead, one barrier
 //     per step; the DMAs are inline asm and the waits explicit vmcnt counts
 //     (seven loads per wave and step), so the compiler adds no waits of its
-//     own before LDS reads;
+//     own before LDS reads; tiles with every row block live issue the
+//     step's loads between its MFMA groups (issued together after the
+//     barrier they stalled the waves' in-order MFMA issue);
 //   * the output is computed transposed, C^T = W . A^T: the MFMA's first
 //     operand is a 16-row W block and its second a 16-row A block, so a lane
 //     owns four consecutive output columns of one row.  That makes the fp32
