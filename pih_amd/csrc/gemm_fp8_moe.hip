@@ -61,6 +61,9 @@ constexpr int kWaitVm7 = 0x0F77;     // vmcnt(7)
 // or bf16 (kOpBf16Fp4) A against MXFP4 W (e2m1 two per byte, UE8M0 per W
 // row and 32 k)
 enum : int { kOpFp8 = 0, kOpBf16 = 1, kOpFp4 = 2, kOpBf16Fp4 = 3 };
+// added to kOutBf16 / kOutF32 in the kernel's output-kind argument: the
+// dense FP8 GEMM with the NaN-code check in its tiles
+constexpr int kOutCodeCheck = 16;
 // static LDS of a block: the FP8 stages (the staged epilogue needs as
 // much), or three bf16 x FP4 stages (256-byte A rows), plus the scratch word
 template <int OP>
@@ -401,8 +404,20 @@ __device__ bool moe_table_tile(const MoeParams& p, const MoeTable& t, uint32_t v
   return true;
 }
 
-template <int OP, int SCALE, int OUT, bool PERSIST>
+// OUT_ARG: the output kind, or kOutBf16 / kOutF32 + kOutCodeCheck for the
+// dense FP8 GEMM with the reference's NaN-code check in its persistent tiles
+// (CODES): an e4m3 NaN code (0x7F / 0xFF) decodes to NaN in the MFMA, so
+// every sum over its A row or W row is NaN; a wave whose 64 x 64 block holds
+// a non-finite value looks for codes in the A and W rows that feed it and
+// raises the code bit instead of the non-finite bit when it finds one.  The
+// launch is followed by the checking 128 x 128 kernel, which runs when the
+// bit is set (decoding codes as zeros, as the reference does) and rewrites
+// every output.
+template <int OP, int SCALE, int OUT_ARG, bool PERSIST>
 __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
+  constexpr bool CODES = OUT_ARG > kOutCodeCheck;
+  constexpr int OUT = CODES ? OUT_ARG - kOutCodeCheck : OUT_ARG;
+  static_assert(!CODES || (OP == kOpFp8 && PERSIST && (OUT == kOutBf16 || OUT == kOutF32)), "code check: dense FP8");
   // Stage s at smem + s * STG: A tile, W tile, A-row scales, W scales.
   // (FP4 W: 64-byte tile rows and 4 scale bytes per W row; the array keeps
   // the FP8 size, which the staged epilogue also needs.)
@@ -1189,6 +1204,11 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // otherwise the per-element path below.
   bool stored = false;
   [[maybe_unused]] bool slow = false;  // wave-uniform
+  // CODES: whether an e4m3 NaN code sits in the A rows or W rows of this
+  // wave's 64 x 64 block (wave-uniform), and the flags before its stores
+  [[maybe_unused]] bool codes = false;
+  [[maybe_unused]] const uint32_t bad0 = CODES ? bad : 0u;
+  [[maybe_unused]] uint32_t codes_bad = 0;  // CODES: the recomputed block's flag bits
   if constexpr (OUT == kOutBf16 || OUT == kOutF32) {
     bool nonfin = false;
 #pragma unroll
@@ -1201,6 +1221,38 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
                       __builtin_isfinite(v[3])))
           nonfin = true;
       }
+    if constexpr (CODES) {
+      // Only a block with a non-finite value can have met a code.  The
+      // block's 64 A rows and 64 W rows (K bytes each), four rows of each at
+      // a time, lane l reading bytes [16 c, 16 c + 16) for c = l, l + 64, ...
+      // (eight loads in flight).  The launcher allows the check on one
+      // problem of contiguous rows (tile row R is A row row0 + R < m) with
+      // 16-byte aligned operands.  Its values are defined here (behind
+      // empty asm statements) so that nothing of this rare path is computed
+      // ahead of the K loop and kept live across it.
+      if (__builtin_amdgcn_ballot_w64(nonfin)) {
+        uint32_t Kc = K, r_base = wm * 64, c_base = nt * BN + wn * 64, c0 = lane * 16;
+        asm volatile("" : "+s"(Kc), "+s"(r_base), "+s"(c_base), "+v"(c0));
+        uint32_t hit = 0;
+        for (uint32_t i0 = 0; i0 < 64; i0 += 4) {
+          for (uint32_t c = c0; c < Kc; c += 64 * 16) {
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+              const uint32_t R = r_base + i0 + u, C = c_base + i0 + u;
+              if (R < rows) {
+                const v4u v = *reinterpret_cast<const v4u*>(p.a + (uint64_t)(row0 + R) * Kc + c);
+                hit |= e4m3_nan_bytes(v.x) | e4m3_nan_bytes(v.y) | e4m3_nan_bytes(v.z) | e4m3_nan_bytes(v.w);
+              }
+              if (C < p.n) {
+                const v4u v = *reinterpret_cast<const v4u*>(p.w + (uint64_t)C * Kc + c);
+                hit |= e4m3_nan_bytes(v.x) | e4m3_nan_bytes(v.y) | e4m3_nan_bytes(v.z) | e4m3_nan_bytes(v.w);
+              }
+            }
+          }
+        }
+        codes = __builtin_amdgcn_ballot_w64(hit != 0) != 0;
+      }
+    }
     if (nonfin) bad |= kErrNonFinite;
     const bool keep_finite = nonfin && p.err_nonfinite && !p.write_nonfinite;
     if constexpr (PERSIST) {
@@ -1210,6 +1262,74 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       // tile's first waits count them; a wave that must skip non-finite
       // elements stores per element below and then drains its stores.
       slow = __builtin_amdgcn_ballot_w64(keep_finite) != 0;
+      if constexpr (CODES) {
+        if (codes) {
+          // The block again, the reference's way: lane l computes row
+          // wm * 64 + l, column by column; each 128-k block is an fp32 sum
+          // of decoded products in k order (NaN codes as 0), scaled by the
+          // row's and the W block's scales and added in block order; a
+          // block with a 0xFF UE8M0 scale adds nothing (bit 2); a
+          // non-finite result raises bit 4 and is not stored (the
+          // reference's fp8_gemm_kernel, deepseek_fp8_gemm.cu:11-70).  Its
+          // stores replace the block's; the wait below drains them.
+          uint32_t Kc = K, rb = wm * 64, cb = nt * BN + wn * 64;
+          asm volatile("" : "+s"(Kc), "+s"(rb), "+s"(cb));
+          const uint32_t KBc = Kc / 128, R = rb + lane;
+          const bool live_r = R < rows;
+          const uint32_t arow = row0 + (live_r ? R : 0u);
+          uint32_t rbad = 0;
+          for (uint32_t j = 0; j < 64; ++j) {
+            const uint32_t C = cb + j;
+            if (C >= p.n) break;
+            float sum = 0.0f;
+            for (uint32_t kb = 0; kb < KBc; ++kb) {
+              float sca, scw;
+              if constexpr (SCALE == kScaleUe8m0) {
+                const uint32_t ba = static_cast<const uint8_t*>(p.a_scale)[(uint64_t)arow * KBc + kb];
+                const uint32_t bw = static_cast<const uint8_t*>(p.w_scale)[(uint64_t)(C / 128) * KBc + kb];
+                if (ba == 0xffu || bw == 0xffu) {
+                  rbad |= kErrScale;
+                  continue;
+                }
+                sca = ue8m0_value(ba);
+                scw = ue8m0_value(bw);
+              } else {
+                sca = reinterpret_cast<const float*>(p.a_scale)[(uint64_t)arow * KBc + kb];
+                scw = reinterpret_cast<const float*>(p.w_scale)[(uint64_t)(C / 128) * KBc + kb];
+              }
+              const uint8_t* ap = p.a + (uint64_t)arow * Kc + kb * 128;
+              const uint8_t* wp = p.w + (uint64_t)C * Kc + kb * 128;
+              float local = 0.0f;
+              for (uint32_t i = 0; i < 128; i += 16) {
+                v4u av = *reinterpret_cast<const v4u*>(ap + i), wv = *reinterpret_cast<const v4u*>(wp + i);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  const uint32_t na = e4m3_nan_bytes(av[q]), nw = e4m3_nan_bytes(wv[q]);
+                  if (na | nw) rbad |= kErrCode;
+                  const uint32_t xa = e4m3_nan_to_zero(av[q], na), xw = e4m3_nan_to_zero(wv[q], nw);
+#pragma unroll
+                  for (int t = 0; t < 4; ++t) local = local + e4m3_decode((xa >> (8 * t)) & 0xffu) *
+                                                                  e4m3_decode((xw >> (8 * t)) & 0xffu);
+                }
+              }
+              sum = sum + local * sca * scw;
+            }
+            if (!live_r) continue;
+            const uint64_t o = (uint64_t)arow * p.out_row_stride + C;
+            if (!__builtin_isfinite(sum)) {
+              rbad |= kErrNonFinite;
+            } else if constexpr (OUT == kOutF32) {
+              static_cast<float*>(p.out)[o] = sum;
+            } else {
+              static_cast<uint16_t*>(p.out)[o] = (uint16_t)f32_to_bf16_bits(sum);
+            }
+          }
+          // rows past the tile's end computed row row0's values: not theirs
+          codes_bad = live_r ? rbad : 0u;
+          slow = true;
+          stored = true;
+        }
+      }
       if (!slow) {
         stored = true;
         constexpr uint32_t OSZ = OUT == kOutF32 ? 4 : 2;
@@ -1356,6 +1476,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
       }
     }
   }
+  if constexpr (CODES) {
+    // a recomputed block's flags replace those of its first pass
+    if (codes) bad = bad0 | codes_bad;
+  }
   if constexpr (!PERSIST) {
     break;
   } else {
@@ -1376,6 +1500,7 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
     if (bits) atomicOr(p.err, bits);
   }
 }
+
 
 template <int OP, int SCALE>
 void launch_out(const MoeParams& mp, uint32_t grid, hipStream_t s, OutKind out, bool persist) {
@@ -1549,7 +1674,8 @@ St LaunchFp4MoeBigTile(const Fp4GemmArgs& a, uint32_t light_rows) {
   return AfterLaunch("fp4_moe_gemm_launch_failed");
 }
 
-St LaunchBigTileGemm(const BigTileArgs& a) {
+St LaunchBigTileGemm(const BigTileArgs& a, bool* codes_in_tiles) {
+  if (codes_in_tiles) *codes_in_tiles = false;
   const bool bf = a.bf16;
   if (!a.a || !a.w || !a.out || !a.stream || (!bf && (!a.a_scale || !a.w_scale || !a.error_flag)))
     return Invalid("big_tile_gemm_null_argument");
@@ -1563,6 +1689,13 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   if (splits > 1 && (a.problems != 1 || a.a_prob_row != 0 || a.out_kind != kOutF32 || ksteps % splits ||
                      ksteps / splits < 4))
     return Invalid("big_tile_gemm_split_invalid");
+  if (a.code_check) {
+    if (bf || splits > 1 || a.problems != 1 || a.a_row_stride != 1 || a.a_prob_row != 0 || !a.err_code_bit ||
+        (a.a_rows_total && a.a_rows_total < a.m))
+      return Invalid("big_tile_gemm_code_check_invalid");
+    if ((reinterpret_cast<uintptr_t>(a.a) | reinterpret_cast<uintptr_t>(a.w)) % 16)
+      return Invalid("nan_code_scan_alignment_invalid");
+  }
   const uint64_t a_rows = a.a_rows_total ? a.a_rows_total : (uint64_t)a.m * a.problems;
   // the tile loads address A and one problem's W by 32-bit byte offsets
   if (a_rows > 0xffffffffull || a_rows * rb > 0xffffffffull || (uint64_t)a.n * rb > 0xffffffffull)
@@ -1610,6 +1743,44 @@ St LaunchBigTileGemm(const BigTileArgs& a) {
   if (persist) grid = std::min(grid, PersistentBlocks());
   St s = RequireCleanLastError();
   if (!s.ok()) return s;
+  if (a.code_check && persist) {
+    // the tiles compute the result with NaN codes as zeros themselves; the
+    // code bit may be raised while they run: no skip test
+    mp.skip_if = nullptr;
+    mp.skip_bit = 0;
+    if (codes_in_tiles) *codes_in_tiles = true;
+    constexpr int kF32c = kOutF32 + kOutCodeCheck, kBf16c = kOutBf16 + kOutCodeCheck;
+    if (a.scale_fmt == kScaleF32) {
+      if (a.out_kind == kOutF32)
+        hipLaunchKernelGGL((fp8_moe_gemm_kernel<kOpFp8, kScaleF32, kF32c, true>), dim3(grid), dim3(NTH), 0, a.stream, mp);
+      else
+        hipLaunchKernelGGL((fp8_moe_gemm_kernel<kOpFp8, kScaleF32, kBf16c, true>), dim3(grid), dim3(NTH), 0, a.stream,
+                           mp);
+    } else {
+      if (a.out_kind == kOutF32)
+        hipLaunchKernelGGL((fp8_moe_gemm_kernel<kOpFp8, kScaleUe8m0, kF32c, true>), dim3(grid), dim3(NTH), 0, a.stream,
+                           mp);
+      else
+        hipLaunchKernelGGL((fp8_moe_gemm_kernel<kOpFp8, kScaleUe8m0, kBf16c, true>), dim3(grid), dim3(NTH), 0,
+                           a.stream, mp);
+    }
+    return AfterLaunch("big_tile_gemm_launch_failed");
+  }
+  if (a.code_check) {
+    // a scan of exactly the A and W bytes the tiles read raises the bit
+    // first, and the tiles exit at once if it is set
+    NanCodeScanArgs sc;
+    sc.a = a.a;
+    sc.a_bytes = (uint64_t)a.m * a.k;
+    sc.w = a.w;
+    sc.w_bytes = (uint64_t)a.n * a.k;
+    sc.error_flag = a.error_flag;
+    sc.bit = a.err_code_bit;
+    sc.stream = a.stream;
+    if (!(s = LaunchNanCodeScan(sc)).ok()) return s;
+    mp.skip_if = a.error_flag;
+    mp.skip_bit = a.err_code_bit;
+  }
   if (bf) launch_out<kOpBf16, kScaleF32>(mp, grid, a.stream, a.out_kind, persist);
   else if (a.scale_fmt == kScaleF32) launch_out<kOpFp8, kScaleF32>(mp, grid, a.stream, a.out_kind, persist);
   else launch_out<kOpFp8, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);

@@ -743,14 +743,18 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
   if (a.moe && !a.offsets) return Invalid("fp8_gemm_offsets_missing");
   if (a.a_rows_total == 0) return Invalid("fp8_gemm_a_rows_invalid");
   if (a.moe && !a.check_codes) return LaunchFp8MoeGemm(a);
-  // One large dense problem: the MoE kernel's big tiles.  Those do not
-  // decode NaN codes as zeros, so with check_codes a scan first raises the
-  // code bit if A or W holds one; the big-tile kernel then exits at once
-  // and the checking 128 x 128 kernel enqueued after it (which otherwise
-  // exits at once) computes the result.  The bit may also have been set
-  // before the call: the checking kernel then runs, with the same result.
-  // (With check_codes only one problem of contiguous rows: the scan then
-  // covers exactly the bytes the GEMM reads.)
+  // One large dense problem: the MoE kernel's big tiles.  Their MFMAs do
+  // not decode NaN codes as zeros.  With check_codes a persistent launch
+  // handles codes in its tiles: a code's NaN reaches every sum over its A
+  // or W row, so a block whose sums came out non-finite looks for codes in
+  // its operand rows and, finding one, computes itself again the
+  // reference's way.  Otherwise a scan raises the code bit first if A or W
+  // holds a code, the big-tile kernel then exits at once, and the checking
+  // 128 x 128 kernel enqueued after it (which otherwise exits at once)
+  // computes the result; a bit set before the call takes the checking
+  // kernel too, with the same result.  (With check_codes only one problem
+  // of contiguous rows: the tiles then read exactly the bytes the check
+  // covers.)
   const bool contiguous1 = a.problems == 1 && a.a_row_stride == 1 && a.a_prob_row == 0 && a.out_prob_col == 0 &&
                            (a.out_row_stride == 0 || a.out_row_stride == a.n) && a.a_rows_total >= a.m;
   const bool dense1 = !a.moe && !a.a_gather && (a.out_kind == kOutBf16 || a.out_kind == kOutF32) &&
@@ -781,19 +785,10 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
     b.err_nonfinite_bit = a.err_nonfinite_bit;
     b.write_nonfinite = a.write_nonfinite;
     if (!a.check_codes || !a.err_code_bit) return LaunchBigTileGemm(b);
-    NanCodeScanArgs sc;
-    sc.a = a.a;
-    sc.a_bytes = (uint64_t)a.m * a.k;
-    sc.w = a.w;
-    sc.w_bytes = (uint64_t)a.n * a.k;
-    sc.error_flag = a.error_flag;
-    sc.bit = a.err_code_bit;
-    sc.stream = a.stream;
-    St s = LaunchNanCodeScan(sc);
-    if (!s.ok()) return s;
-    b.skip_if = a.error_flag;
-    b.skip_bit = a.err_code_bit;
-    if (!(s = LaunchBigTileGemm(b)).ok()) return s;
+    b.code_check = true;
+    bool done = false;
+    St s = LaunchBigTileGemm(b, &done);
+    if (!s.ok() || done) return s;
   }
   if (!a.moe && a.m <= kSmallMRows && (a.out_kind == kOutBf16 || a.out_kind == kOutF32)) {
     // a few activation rows: weight streaming over 16-row blocks

@@ -183,8 +183,16 @@ struct BigTileArgs {
   // holds k_splits fp32 slabs [m][out_row_stride] of partial sums, summed
   // by LaunchSplitKReduce (out_kind kOutF32)
   uint32_t k_splits = 1;
+  // FP8, one problem of contiguous rows, A and W on 16-byte boundaries:
+  // the reference's NaN-code semantics (a code decodes as 0 and raises
+  // err_code_bit).  A persistent launch handles them in its tiles
+  // (*codes_in_tiles set); otherwise a scan raises the bit before the tiles,
+  // which then exit at once if it is set, and the caller enqueues the
+  // checking kernel, which computes the result when the bit is set.
+  // skip_if is not used.
+  bool code_check = false;
 };
-St LaunchBigTileGemm(const BigTileArgs& a);
+St LaunchBigTileGemm(const BigTileArgs& a, bool* codes_in_tiles = nullptr);
 // K splits for a dense big-tile GEMM of k_steps 128-byte K steps (1: none):
 // below a round of tiles on the 256 CUs
 uint32_t DenseKSplits(uint32_t m, uint32_t n, uint32_t k_steps);

@@ -4,11 +4,15 @@
   `launch_fp8_gemm` (fp32 scales) at shapes whose tile grid fills the GPU:
   sampled rows against the oracle.
 * The reference decodes an e4m3 NaN code as 0 and raises bit 1
-  (deepseek_fp8_gemm.cu:11-17); the big-tile kernel does not decode codes, so
-  a scan raises the bit first and the big-tile kernel steps aside for the
-  checking 128 x 128 kernel.  Checked with a NaN code planted in A and one in
-  W (the rows they reach against the oracle, which zeroes them), and with
-  the bit already set before the call (the checking kernel computes it all).
+  (deepseek_fp8_gemm.cu:11-17); the big tiles' MFMAs do not decode codes,
+  but a code's NaN reaches every sum over its A or W row, so a persistent
+  tile whose block came out non-finite looks for codes in its operand rows
+  and, finding one, computes the block again the reference's way.  Checked
+  with NaN codes planted in A and in W (the rows they reach against the
+  oracle, with the codes zeroed), with UE8M0 and fp32 scales, at 128- and
+  32-row M tiles, next to overflowing sums (bit 4, elements unwritten), in
+  a block a 0xFF scale skips (bit 2 only: the reference never decodes it),
+  and with the bit already set before the call.
 * BF16 `launch_bf16_gemm` at M = 1024 and 2048 (prefill sizes) with bf16
   and fp32 output against the fp32-accumulate oracle.
 
@@ -77,7 +81,7 @@ def test_deepseek_fp8_gemm_big_tile(eng, m, n, k):
     assert_close(got[rows], ref, f"big-tile fp8 {m}x{n}x{k}")
 
 
-def test_nan_codes_take_the_checking_kernel(eng):
+def test_nan_codes_in_a_and_w(eng):
     m, n, k = 2048, 4096, 1024
     a, sa, w, sw = _ue8m0_operands(m, n, k, 300)
     a[5, 77] = 0x7F   # NaN code in A (row 5)
@@ -94,9 +98,118 @@ def test_nan_codes_take_the_checking_kernel(eng):
     assert_close(got[rows], ref, "nan codes as zero")
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 1024, 4096), (2048, 4096, 1024), (2048, 4096, 384)])
+@pytest.mark.parametrize("where", ["a", "w"])
+def test_nan_code_found_in_tiles(eng, m, n, k, where):
+    """One NaN code in A (last M tile, last K block) or in W: the persistent
+    big tiles (32-row M tiles at 2048 x 1024 x 4096) find it in the operand
+    rows of the blocks whose sums it turned into NaN, raise bit 1 only and
+    compute those blocks again with the code as 0.  K = 384 (three K steps)
+    is too short for the persistent tiles: a scan raises the bit, the big
+    tiles exit and the checking kernel computes the result."""
+    a, sa, w, sw = _ue8m0_operands(m, n, k, 600 + k + (where == "w"))
+    a0, w0 = a.copy(), w.copy()
+    if where == "a":
+        a[m - 3, k - 5] = 0xFF
+    else:
+        w[n - 7, 1] = 0x7F
+    got, flag = _ds_fp8(a, sa, w, sw, m, n, k)
+    assert flag == 1, flag
+    assert np.isfinite(got).all()
+    rows = np.array([0, 31, 32, m // 2, m - 3, m - 1])
+    ref = oracle.fp8_gemm_ue8m0(np.ascontiguousarray(a0[rows]), np.ascontiguousarray(sa[rows]), w0, sw)
+    assert_close(got[rows], ref, f"nan code in {where} as zero")
+
+
+def test_nan_code_in_a_skipped_block(eng):
+    """A NaN code in a 128-k block whose UE8M0 activation scale is 0xFF: the
+    reference skips the block before decoding it, so the flag holds bit 2
+    only, and that block adds nothing to its row."""
+    m, n, k = 2048, 1024, 4096
+    a, sa, w, sw = _ue8m0_operands(m, n, k, 650)
+    a[100, 1000] = 0x7F
+    sa[100, 1000 // 128] = 0xFF
+    got, flag = _ds_fp8(a, sa, w, sw, m, n, k)
+    assert flag == 2, flag
+    a0, sa0 = a.copy(), sa.copy()
+    a0[100, 896:1024] = 0  # the skipped block
+    sa0[100, 7] = 127
+    rows = np.array([0, 99, 100, 101, m - 1])
+    ref = oracle.fp8_gemm_ue8m0(np.ascontiguousarray(a0[rows]), np.ascontiguousarray(sa0[rows]), w, sw)
+    assert np.isfinite(got).all()
+    assert_close(got[rows], ref, "code in a skipped block")
+
+
+def test_nan_code_with_overflow_elsewhere(eng):
+    """A NaN code in A row 7 and, in other columns, sums that overflow: bit 1
+    from the code and bit 4 from the overflow (the overflowing elements are
+    left unwritten, as the reference does, row 7's among them); the other
+    elements hold the oracle's values with the code as 0."""
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    m, n, k = 2048, 1024, 4096
+    a = np.zeros((m, k), np.uint8)
+    a[:, :128] = 0x7E  # 448
+    w = np.zeros((n, k), np.uint8)
+    w[:, :128] = 0x7E
+    a[7, 2000] = 0x7F
+    sa = np.full((m, k // 128), 127, np.uint8)
+    sw = np.full((n // 128, k // 128), 127, np.uint8)
+    sw[5, 0] = 254  # W rows 640..767: 448 * 448 * 128 * 2^127 overflows
+    sentinel = 0x7FC1
+    out = torch.full((m, n), sentinel, dtype=torch.int16, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ad, sad, wd, swd = to_dev(a), to_dev(sa), to_dev(w), to_dev(sw)
+    r = abi.request(abi.DS["fp8_gemm"], activation_e4m3=ptr(ad), activation_scale_bits=ptr(sad),
+                    weight_e4m3=ptr(wd), weight_scale_bits=ptr(swd), output=ptr(out), error_flag=ptr(flag),
+                    stream=stream_handle(), m=m, n=n, k=k, output_type=1)
+    st = abi.deepseek_pack().call("launch_fp8_gemm", r)
+    assert st.code == abi.OK, st
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 5
+    got = to_host(out).view(np.uint16)
+    assert np.all(got[:, 640:768] == sentinel)
+    want = oracle.f32_to_bf16_bits(np.float32(448.0 * 448 * 128))
+    assert np.all(got[:, :640] == want) and np.all(got[:, 768:] == want)
+
+
+def test_linear_fp8_gemm_nan_code_f32_scales(eng):
+    """The linear pack's fp32-scale entry on the persistent big tiles: a NaN
+    code in W raises bit 1 and the result has it as 0."""
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    m, n, k = 2048, 1024, 4096
+    a = _codes(synth.config_seed(5, 700), (m, k))
+    w = _codes(synth.config_seed(5, 701), (n, k))
+    w0 = w.copy()
+    w[300, 4000] = 0xFF
+    rng = np.random.default_rng(702)
+    sa = (rng.uniform(0.5, 2.0, (m, k // 128)) / 448).astype(np.float32)
+    sw = (rng.uniform(0.5, 2.0, (n // 128, k // 128)) / 448).astype(np.float32)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ad, sad, wd, swd = to_dev(a), to_dev(sa), to_dev(w), to_dev(sw)
+    r = abi.request(abi.LN["fp8_gemm"], activation_e4m3=ptr(ad), activation_scale=ptr(sad), weight_e4m3=ptr(wd),
+                    weight_scale=ptr(swd), output=ptr(out), error_flag_u32=ptr(flag), stream=stream_handle(),
+                    m=m, n=n, k=k, scale_format=abi.SCALE_F32, output_type=abi.OUTPUT_BF16)
+    st = abi.linear_pack().call("launch_fp8_gemm", r)
+    assert st.code == abi.OK, st
+    torch.cuda.synchronize()
+    assert int(flag.item()) == 1
+    got = oracle.bf16_bits_to_f32(to_host(out))
+    assert np.isfinite(got).all()
+    rows = np.unique(np.linspace(0, m - 1, 16).astype(np.int64))
+    ref = oracle.fp8_gemm_f32(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows]), w0, sw)
+    assert_close(got[rows], ref, "f32-scale nan code as zero")
+
+
 def test_code_bit_already_set(eng):
-    """A flag that already holds bit 1 (a poisoned lane) sends the call to
-    the checking kernel; the result is the same."""
+    """A flag that already holds bit 1 (a poisoned lane) before the call:
+    the bit stays, and the result is the same."""
     m, n, k = 2048, 4096, 1024
     a, sa, w, sw = _ue8m0_operands(m, n, k, 400)
     clean, flag0 = _ds_fp8(a, sa, w, sw, m, n, k)
@@ -105,7 +218,7 @@ def test_code_bit_already_set(eng):
     assert flag1 == 1
     rows = np.unique(np.linspace(0, m - 1, 16).astype(np.int64))
     ref = oracle.fp8_gemm_ue8m0(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows]), w, sw)
-    assert_close(again[rows], ref, "checking kernel")
+    assert_close(again[rows], ref, "bit set before the call")
     assert_close(clean[rows], ref, "big-tile kernel")
 
 
