@@ -1269,9 +1269,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
           // of decoded products in k order (NaN codes as 0), scaled by the
           // row's and the W block's scales and added in block order; a
           // block with a 0xFF UE8M0 scale adds nothing (bit 2); a
-          // non-finite result raises bit 4 and is not stored (the
-          // reference's fp8_gemm_kernel, deepseek_fp8_gemm.cu:11-70).  Its
-          // stores replace the block's; the wait below drains them.
+          // non-finite result raises bit 4 and, unless write_nonfinite, is
+          // not stored (the reference's fp8_gemm_kernel,
+          // deepseek_fp8_gemm.cu:11-70).  Its stores replace the block's;
+          // the wait below drains them.
           uint32_t Kc = K, rb = wm * 64, cb = nt * BN + wn * 64;
           asm volatile("" : "+s"(Kc), "+s"(rb), "+s"(cb));
           const uint32_t KBc = Kc / 128, R = rb + lane;
@@ -1316,12 +1317,13 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
             }
             if (!live_r) continue;
             const uint64_t o = (uint64_t)arow * p.out_row_stride + C;
-            if (!__builtin_isfinite(sum)) {
-              rbad |= kErrNonFinite;
-            } else if constexpr (OUT == kOutF32) {
-              static_cast<float*>(p.out)[o] = sum;
-            } else {
-              static_cast<uint16_t*>(p.out)[o] = (uint16_t)f32_to_bf16_bits(sum);
+            const bool fin = __builtin_isfinite(sum);
+            if (!fin) rbad |= kErrNonFinite;
+            // the first pass's rule: a non-finite result is stored only
+            // when the caller asks for it (or keeps no non-finite bit)
+            if (fin || !p.err_nonfinite || p.write_nonfinite) {
+              if constexpr (OUT == kOutF32) static_cast<float*>(p.out)[o] = sum;
+              else static_cast<uint16_t*>(p.out)[o] = (uint16_t)f32_to_bf16_bits(sum);
             }
           }
           // rows past the tile's end computed row row0's values: not theirs
