@@ -175,9 +175,11 @@ def test_nan_code_with_overflow_elsewhere(eng):
     assert np.all(got[:, :640] == want) and np.all(got[:, 768:] == want)
 
 
-def test_linear_fp8_gemm_nan_code_f32_scales(eng):
-    """The linear pack's fp32-scale entry on the persistent big tiles: a NaN
-    code in W raises bit 1 and the result has it as 0."""
+@pytest.mark.parametrize("out_type", [1, 2])
+def test_linear_fp8_gemm_nan_code_f32_scales(eng, out_type):
+    """The linear pack's fp32-scale entry on the persistent big tiles, bf16
+    and fp32 output: a NaN code in W raises bit 1 and the result has it as
+    0."""
     import torch
 
     from pih_amd.device import ptr, stream_handle
@@ -190,17 +192,19 @@ def test_linear_fp8_gemm_nan_code_f32_scales(eng):
     rng = np.random.default_rng(702)
     sa = (rng.uniform(0.5, 2.0, (m, k // 128)) / 448).astype(np.float32)
     sw = (rng.uniform(0.5, 2.0, (n // 128, k // 128)) / 448).astype(np.float32)
-    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    dt = torch.bfloat16 if out_type == abi.OUTPUT_BF16 else torch.float32
+    out = torch.empty(m, n, dtype=dt, device="cuda")
     flag = torch.zeros(1, dtype=torch.int32, device="cuda")
     ad, sad, wd, swd = to_dev(a), to_dev(sa), to_dev(w), to_dev(sw)
     r = abi.request(abi.LN["fp8_gemm"], activation_e4m3=ptr(ad), activation_scale=ptr(sad), weight_e4m3=ptr(wd),
                     weight_scale=ptr(swd), output=ptr(out), error_flag_u32=ptr(flag), stream=stream_handle(),
-                    m=m, n=n, k=k, scale_format=abi.SCALE_F32, output_type=abi.OUTPUT_BF16)
+                    m=m, n=n, k=k, scale_format=abi.SCALE_F32, output_type=out_type)
     st = abi.linear_pack().call("launch_fp8_gemm", r)
     assert st.code == abi.OK, st
     torch.cuda.synchronize()
     assert int(flag.item()) == 1
-    got = oracle.bf16_bits_to_f32(to_host(out))
+    host = to_host(out)
+    got = oracle.bf16_bits_to_f32(host) if out_type == abi.OUTPUT_BF16 else host
     assert np.isfinite(got).all()
     rows = np.unique(np.linspace(0, m - 1, 16).astype(np.int64))
     ref = oracle.fp8_gemm_f32(np.ascontiguousarray(a[rows]), np.ascontiguousarray(sa[rows]), w0, sw)
