@@ -1065,8 +1065,10 @@ __global__ __launch_bounds__(NTH, 1) void fp8_moe_gemm_kernel(MoeParams p) {
   // an expert with one M tile reads each weight byte once: its weight
   // loads are non-temporal, so they do not evict the weight tiles that the
   // multi-tile experts' M tiles share in L2 (the tile's first two steps,
-  // loaded before this choice, use the default policy)
-  bool once = false;
+  // loaded before this choice, use the default policy); so does a dense
+  // GEMM of one M tile (a decode batch against a wide weight), whose A tile
+  // every tile reads again
+  bool once = p.dense_m_tiles == 1;
   if (!p.dense_m_tiles && rows) {
     uint32_t lo, hi;
     if constexpr (PERSIST) lo = tab.off[expert], hi = tab.off[expert + 1];
