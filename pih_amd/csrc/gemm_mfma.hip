@@ -901,15 +901,18 @@ St LaunchBf16Gemm(const Bf16GemmArgs& a) {
   if (!a.a || !a.w || !a.out || !a.stream) return Invalid("bf16_gemm_null_argument");
   if (a.m == 0 || a.n == 0 || a.k == 0) return Invalid("bf16_gemm_shape_invalid");
   if (a.out_kind != kOutBf16 && a.out_kind != kOutF32) return Invalid("bf16_gemm_output_type_invalid");
-  // Decode batches of 17..64 rows against very wide weights (the LM heads:
-  // a round of 256-column tiles without a K split) take the big tiles, which
-  // stream the weights once with the batch in one M tile, where the GEMV
-  // re-reads the batch's rows from L2 for every 16 weight rows (m / 16 times
-  // the weight bytes).
-  const bool wide_decode = a.m >= 17 && a.m <= 64 && a.n % 128 == 0 && a.k % 64 == 0 && a.n / 256 >= 192;
-  if (a.m <= 64 && !wide_decode) return LaunchBf16Gemv(a);
+  // Batches of 2..255 rows against very wide weights (the LM heads: a round
+  // of 256-column tiles without a K split) take the big tiles, which stream
+  // the weights once (twice through L2 above 128 rows) with the batch in one
+  // M tile, where the GEMV re-reads the batch's rows from L2 for every 16
+  // weight rows and the 128 x 128 kernel is MFMA-bound on its small tiles
+  // (DeepSeek LM head, 4096 -> 129280: m = 2 186 -> 165 us, m = 16 194 ->
+  // 170 us, m = 64 177 us, m = 128 233 -> 186 us, m = 200 364 -> 285 us;
+  // m = 1 stays on the GEMV, 159 us).
+  const bool wide = a.m >= 2 && a.m < 256 && a.n % 128 == 0 && a.k % 64 == 0 && a.n / 256 >= 192;
+  if (a.m <= 64 && !wide) return LaunchBf16Gemv(a);
   if (a.n % 128 || a.k % 64) return Invalid("bf16_gemm_shape_invalid");
-  if ((BigTileWorthIt(a.m, a.n) || wide_decode) && (uint64_t)a.m * a.k * 2 <= 0xffffffffull &&
+  if ((BigTileWorthIt(a.m, a.n) || wide) && (uint64_t)a.m * a.k * 2 <= 0xffffffffull &&
       (uint64_t)a.n * a.k * 2 <= 0xffffffffull) {
     BigTileArgs b;
     b.a = a.a;

@@ -80,11 +80,11 @@ def _check_logits(got, x_bits, w_sub_bits, what):
     assert_close(got, ref, what)
 
 
-@pytest.mark.parametrize("rows", [1, 5, 64, 65, 300])
+@pytest.mark.parametrize("rows", [1, 2, 5, 64, 65, 200, 300])
 def test_deepseek_lm_head(ds_weight, rows):
-    """rows <= 16 run the weight-streaming GEMV; 17..64 (the vocabulary is
-    more than a round of 256-column tiles) and 256 or more the persistent
-    big tiles; 65..255 the 128 x 128 MFMA GEMM."""
+    """One row runs the weight-streaming GEMV; more (the vocabulary is more
+    than a round of 256-column tiles) the persistent big tiles, one M tile
+    up to 128 rows."""
     from pih_amd.linear import deepseek_lm_head
 
     w, words, w_sub = ds_weight
@@ -98,7 +98,7 @@ def test_deepseek_lm_head(ds_weight, rows):
     _check_logits(got, to_host(x), w_sub, f"deepseek lm_head rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [2, 40, 100])
+@pytest.mark.parametrize("rows", [1, 2, 40, 100])
 def test_deepseek_lm_head_error_bits(ds_weight, rows):
     import torch
 
