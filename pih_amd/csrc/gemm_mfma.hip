@@ -757,9 +757,32 @@ St LaunchFp8BlockGemm(const BlockGemmArgs& a) {
   // covers.)
   const bool contiguous1 = a.problems == 1 && a.a_row_stride == 1 && a.a_prob_row == 0 && a.out_prob_col == 0 &&
                            (a.out_row_stride == 0 || a.out_row_stride == a.n) && a.a_rows_total >= a.m;
-  const bool dense1 = !a.moe && !a.a_gather && (a.out_kind == kOutBf16 || a.out_kind == kOutF32) &&
-                      (contiguous1 || !a.check_codes) && BigTileWorthIt(a.m, a.n * a.problems) &&
-                      (uint64_t)a.a_rows_total * a.k <= 0xffffffffull && (uint64_t)a.n * a.k <= 0xffffffffull;
+  const bool dense_ok = !a.moe && !a.a_gather && (a.out_kind == kOutBf16 || a.out_kind == kOutF32) &&
+                        (contiguous1 || !a.check_codes) && (uint64_t)a.a_rows_total * a.k <= 0xffffffffull &&
+                        (uint64_t)a.n * a.k <= 0xffffffffull;
+  // Above 64 rows the big tiles also take what the 128 x 128 kernel took
+  // before (more than 256 rows, or too many 128 x 128 tiles for the small-M
+  // kernel) and the small-M kernel's 64-row chunks once together they would
+  // stream more than 20 MB of weights (each chunk streams all of W).
+  // DeepSeek launch_fp8_gemm, K -> N at M rows, us before -> after:
+  // 4096 -> 1024 M 384 63 -> 26; 8192 -> 4096 M 128 56 -> 50, M 256 111 ->
+  // 50, M 384 122 -> 51; 4096 -> 2048 M 192 30 -> 27, M 512 63 -> 28;
+  // 2048 -> 4096 M 256 26 -> 18; 1024 -> 32768 M 100 22 -> 17.  Below
+  // those sizes the small-M kernel stays faster (4096 -> 1024 at M 256: 16
+  // against 26 us: a big tile's 32 K steps take ~0.8 us each).
+  // At 33..64 rows the big tiles also win where the small-M kernel's one
+  // pass over W (~1.15 TB/s at 64 rows) takes longer than a round of big
+  // tiles (~0.8 us per 128-deep K step + ~5 us): 1024 -> 32768 at M 64,
+  // 25 -> 16 us.
+  bool big = BigTileWorthIt(a.m, a.n * a.problems);
+  const uint64_t w_bytes = (uint64_t)a.n * a.k * a.problems;
+  if (a.m > kSmallMChunkRows) {
+    const uint64_t chunks = (a.m + kSmallMChunkRows - 1) / kSmallMChunkRows;
+    big = big || a.m > kSmallMRows || !SmallMTakes(a.m, a.n, a.problems) || chunks * w_bytes > (20ull << 20);
+  } else if (a.m > 32) {
+    big = big || w_bytes / 1150 > (uint64_t)(a.k / 128) * 800 + 5000;  // ns
+  }
+  const bool dense1 = dense_ok && big;
   if (dense1) {
     BigTileArgs b;
     b.a = a.a;
