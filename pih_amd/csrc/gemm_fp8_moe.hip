@@ -1820,12 +1820,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 uint32_t DenseKSplits(uint32_t m, uint32_t n, uint32_t k_steps) {
   // a split is worth it below one 128 x 256 tile per CU (256 CUs); the
   // smallest split count that reaches a full round, with at least 8 K steps
-  // per split
+  // per split, else the largest such count (a GEMM of few tiles: M 128,
+  // 12288 -> 4096 has 16)
   const uint64_t tiles = (uint64_t)((m + BM - 1) / BM) * ((n + BN - 1) / BN);
   if (tiles == 0 || tiles >= 192) return 1;
-  for (uint32_t s = 2; s <= 8; ++s)
-    if (k_steps % s == 0 && k_steps / s >= 8 && tiles * s >= 192) return s;
-  return 1;
+  uint32_t best = 1;
+  for (uint32_t s = 2; s <= 8; ++s) {
+    if (k_steps % s || k_steps / s < 8) continue;
+    if (tiles * s >= 192) return s;
+    best = s;
+  }
+  return best;
 }
 
 St LaunchSplitKReduce(const float* ws, uint32_t splits, uint32_t m, uint32_t n, void* out, OutKind out_kind,

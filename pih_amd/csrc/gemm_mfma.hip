@@ -935,7 +935,7 @@ St LaunchBf16Gemm(const Bf16GemmArgs& a) {
   const bool wide = a.m >= 2 && a.m < 256 && a.n % 128 == 0 && a.k % 64 == 0 && a.n / 256 >= 192;
   if (a.m <= 64 && !wide) return LaunchBf16Gemv(a);
   if (a.n % 128 || a.k % 64) return Invalid("bf16_gemm_shape_invalid");
-  if ((BigTileWorthIt(a.m, a.n) || wide) && (uint64_t)a.m * a.k * 2 <= 0xffffffffull &&
+  if ((Bf16BigTiles(a.m, a.n, a.k) || wide) && (uint64_t)a.m * a.k * 2 <= 0xffffffffull &&
       (uint64_t)a.n * a.k * 2 <= 0xffffffffull) {
     BigTileArgs b;
     b.a = a.a;
@@ -1028,7 +1028,7 @@ uint64_t Bf16GemmWorkspaceBytes(uint32_t m, uint32_t n, uint32_t k) {
   if (m <= 64) return Bf16GemvWorkspaceBytes(m, n, k);
   // the big tiles' K split (fp32 partial sums); without this workspace the
   // call runs unsplit
-  if (n % 128 || k % 64 || !BigTileWorthIt(m, n)) return 0;
+  if (n % 128 || k % 64 || !Bf16BigTiles(m, n, k)) return 0;
   const uint32_t splits = DenseKSplits(m, n, k / 64);
   return splits > 1 ? (uint64_t)splits * m * n * 4 : 0;
 }

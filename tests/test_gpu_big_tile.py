@@ -279,12 +279,15 @@ def test_bf16_gemm_big_tile(eng, m, n, k, out_type):
     assert_close(got[rows], ref, f"big-tile bf16 {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 1024, 4096), (1000, 2048, 4096), (2048, 1280, 4608)])
+@pytest.mark.parametrize("m,n,k", [(2048, 1024, 4096), (1000, 2048, 4096), (2048, 1280, 4608), (128, 4096, 12288),
+                                   (96, 1024, 4096)])
 @pytest.mark.parametrize("out_type", [abi.OUTPUT_BF16, abi.OUTPUT_F32])
 def test_bf16_gemm_k_split(eng, m, n, k, out_type):
     """launch_bf16_gemm with the queried workspace at shapes with fewer big
     tiles than CUs (the Qwen3-8B k/v projections at M 2048: 4 K splits; M
-    1000: a partial M tile; 4608 -> 1280: 3 splits): the fp32 partial sums go to the
+    1000: a partial M tile; 4608 -> 1280: 3 splits; batches of 96 and 128
+    rows: 8 splits, one partial M tile; without the workspace they run
+    unsplit on 32-row M tiles): the fp32 partial sums go to the
     workspace (filled with NaN bytes first, so an element no split writes
     would show) and are summed in split order.  Sampled rows against the
     oracle, every row's sum against a float64 checksum, and the whole output
@@ -320,6 +323,7 @@ def test_bf16_gemm_k_split(eng, m, n, k, out_type):
     split, whole = run(True), run(False)
     assert np.all(np.isfinite(split))
     rows = np.unique(np.concatenate([np.linspace(0, m - 1, 24).astype(np.int64), [127, 128, m - 1]]))
+    rows = rows[rows < m]
     ref = oracle.bf16_gemm(np.ascontiguousarray(x[rows]), w)
     assert_close(split[rows], ref, f"k-split bf16 {m}x{n}x{k}")
     colsum = oracle.bf16_bits_to_f32(w).astype(np.float64).sum(axis=0)

@@ -201,10 +201,12 @@ def test_bf16_gemm_workspace_sizes():
     the big tiles when a GEMM has fewer 128 x 256 tiles than about a round on
     the 256 CUs -- 4 fp32 partial-sum slabs for M 2048, 4096 -> 1024 (64
     tiles, 64 K steps of 64) and M 1000, 4096 -> 2048; 3 for M 2048,
-    4608 -> 1280 (80 tiles, 72 K steps) -- and none for a full round
-    (4096 -> 4096: 256 tiles), decode shapes (m <= 64), shapes below the big
-    tiles (M 1000, 4096 -> 1024: 32 tiles) or K too short to split (at least
-    8 K steps per split)."""
+    4608 -> 1280 (80 tiles, 72 K steps); 8 for M 1000, 4096 -> 1024 (32
+    tiles) and, the largest count when no count reaches a round, for M 128,
+    12288 -> 4096 (16 tiles) -- and none for a full round (4096 -> 4096: 256
+    tiles), decode shapes (m <= 64), shapes below the big tiles (K under 512:
+    the 128 x 128 kernel) or K too short to split (at least 8 K steps per
+    split)."""
     ln = abi.linear_pack()
     out = (C.c_uint64 * 1)()
 
@@ -219,7 +221,9 @@ def test_bf16_gemm_workspace_sizes():
     assert q(2048, 1280, 4608) == 3 * 2048 * 1280 * 4
     assert q(2048, 4096, 4096) == 0
     assert q(64, 1024, 4096) == 0
-    assert q(1000, 1024, 4096) == 0
+    assert q(1000, 1024, 4096) == 8 * 1000 * 1024 * 4
+    assert q(128, 4096, 12288) == 8 * 128 * 4096 * 4
+    assert q(65, 128, 64) == 0
     assert q(2048, 1024, 512) == 0
 
 
