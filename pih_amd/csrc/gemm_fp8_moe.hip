@@ -1678,6 +1678,62 @@ St LaunchFp4MoeBigTile(const Fp4GemmArgs& a, uint32_t light_rows) {
   return AfterLaunch("fp4_moe_gemm_launch_failed");
 }
 
+// One dense FP4 problem (DeepSeek launch_fp4_gemm at batches the small-M
+// kernel does not take well) on the 128 x 256 tiles with the FP4 W operand:
+// the dense tile map of LaunchBigTileGemm (M tiles halved to 64 / 32 rows
+// while the tiles number fewer than 192), the MXFP4 error bits (1 code, 2
+// scale, 4 non-finite, non-finite results not stored), and every block
+// exiting at once when skip_if holds the code bit (the caller's NaN-code
+// scan of A runs first; W e2m1 has no NaN code).
+bool Fp4DenseBigTileTakes(const Fp4GemmArgs& a) {
+  return !a.moe && !a.a_gather && a.problems == 1 && a.act == kActE4m3 && a.k % 128 == 0 && a.k >= 512 &&
+         a.n % 128 == 0 && (a.out_kind == kOutBf16 || a.out_kind == kOutF32) && a.a_rows_total >= a.m &&
+         reinterpret_cast<uintptr_t>(a.w_scale) % 4 == 0 && reinterpret_cast<uintptr_t>(a.a) % 16 == 0 &&
+         (uint64_t)a.a_rows_total * a.k <= 0xffffffffull && (uint64_t)a.n * (a.k / 2) <= 0xffffffffull;
+}
+
+St LaunchFp4DenseBigTile(const Fp4GemmArgs& a, const uint32_t* skip_if, uint32_t skip_bit) {
+  if (!Fp4DenseBigTileTakes(a)) return Invalid("fp4_dense_big_tile_invalid");
+  MoeParams mp{};
+  mp.a = static_cast<const uint8_t*>(a.a);
+  mp.a_scale = a.a_scale;
+  mp.w = a.w;
+  mp.w_scale = a.w_scale;
+  mp.out = a.out;
+  mp.err = a.error_flag;
+  mp.m = a.m;
+  mp.n = a.n;
+  mp.k = a.k;
+  mp.experts = 1;
+  mp.a_rows_total = a.a_rows_total;
+  uint32_t tile_rows = BM;
+  const uint64_t nt = (a.n + BN - 1) / BN;
+  while (tile_rows > 32 && (uint64_t)((a.m + tile_rows - 1) / tile_rows) * nt < 192) tile_rows /= 2;
+  mp.dense_tile_rows = tile_rows;
+  mp.dense_m_tiles = (a.m + tile_rows - 1) / tile_rows;
+  mp.a_row_stride = 1;
+  mp.a_prob_row = 0;
+  mp.out_row_stride = a.n;
+  mp.out_prob_col = 0;
+  mp.n_tiles = (uint32_t)nt;
+  mp.stage_out = StageOut(a.out, mp.out_row_stride, 0, a.out_kind);
+  mp.err_code = 1u;
+  mp.err_scale = 2u;
+  mp.err_nonfinite = 4u;
+  mp.skip_if = skip_if;
+  mp.skip_bit = skip_bit;
+  const uint64_t total = (uint64_t)mp.dense_m_tiles * mp.n_tiles;
+  if (total > 0x7fffffffull - 8) return Invalid("fp4_dense_big_tile_grid_too_large");
+  const bool persist = Persistent(a.out_kind, false, true, 1, mp.out_row_stride, a.k / 128);
+  uint32_t grid = (uint32_t)((total + 7) / 8 * 8);
+  mp.vb_end = grid;
+  if (persist) grid = std::min(grid, PersistentBlocks());
+  St s = RequireCleanLastError();
+  if (!s.ok()) return s;
+  launch_out<kOpFp4, kScaleUe8m0>(mp, grid, a.stream, a.out_kind, persist);
+  return AfterLaunch("fp4_dense_big_tile_launch_failed");
+}
+
 St LaunchBigTileGemm(const BigTileArgs& a, bool* codes_in_tiles) {
   if (codes_in_tiles) *codes_in_tiles = false;
   const bool bf = a.bf16;

@@ -861,8 +861,36 @@ St LaunchFp4Gemm(const Fp4GemmArgs& a) {
   if (a.act != kActE4m3 && a.act != kActBf16) return Invalid("fp4_gemm_activation_type_invalid");
   if (a.moe && !a.offsets) return Invalid("fp4_gemm_offsets_missing");
   if (a.a_rows_total == 0) return Invalid("fp4_gemm_a_rows_invalid");
-  if (!a.moe && a.problems == 1 && a.act == kActE4m3 && a.m <= kSmallMRows &&
-      (a.out_kind == kOutBf16 || a.out_kind == kOutF32)) {
+  // Dense batches above 64 rows the small-M kernel does not take well (more
+  // than 256 rows, or 64-row chunks that together would stream more than
+  // 40 MB of weights and scales): the big tiles with the FP4 W operand,
+  // after a scan that raises the NaN-code bit if A holds a code; they then
+  // exit at once, and the checking 128 x 128 kernel enqueued after them
+  // (which otherwise exits at once) computes the result.  DeepSeek
+  // launch_fp4_gemm, K -> N, us before -> after: 7168 -> 4096 M 256 86 ->
+  // 55, M 512 98 -> 56, M 2048 111 -> 77; 4096 -> 2048 M 512 51 -> 30;
+  // 2048 -> 4096 M 512 29 -> 21 (M 128 at 7168 -> 4096, two chunks of
+  // 15.6 MB, stays on the small-M kernel: 45 against 55 us).
+  bool dense_big = false;
+  if (a.m > kSmallMChunkRows && Fp4DenseBigTileTakes(a)) {
+    const uint64_t w_bytes = (uint64_t)a.n * (a.k / 2) + (uint64_t)a.n * (a.k / 32);
+    const uint64_t chunks = (a.m + kSmallMChunkRows - 1) / kSmallMChunkRows;
+    dense_big = a.m > kSmallMRows || !SmallMTakes(a.m, a.n, 1) || chunks * w_bytes > (40ull << 20);
+  }
+  if (dense_big) {
+    NanCodeScanArgs sc;
+    sc.a = a.a;
+    sc.a_bytes = (uint64_t)a.m * a.k;
+    sc.w = a.a;  // e2m1 weights hold no NaN code
+    sc.w_bytes = 0;
+    sc.error_flag = a.error_flag;
+    sc.bit = 1u;
+    sc.stream = a.stream;
+    St s = LaunchNanCodeScan(sc);
+    if (!s.ok()) return s;
+    if (!(s = LaunchFp4DenseBigTile(a, a.error_flag, 1u)).ok()) return s;
+  } else if (!a.moe && a.problems == 1 && a.act == kActE4m3 && a.m <= kSmallMRows &&
+             (a.out_kind == kOutBf16 || a.out_kind == kOutF32)) {
     // a few activation rows (the per-expert decode call): weight streaming
     bool taken = false;
     St s = LaunchFp4SmallM(a, taken);
@@ -884,6 +912,10 @@ St LaunchFp4Gemm(const Fp4GemmArgs& a) {
   gp.err_code = 1u;
   gp.err_scale = 2u;
   gp.err_nonfinite = 4u;
+  if (dense_big) {  // the checking half
+    gp.run_if = a.error_flag;
+    gp.run_bit = 1u;
+  }
   // MoE: the light experts go to the weight-streaming kernel, the tiles
   // here cover the others
   uint32_t grid;

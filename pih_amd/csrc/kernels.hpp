@@ -134,6 +134,10 @@ St LaunchFp4MoeStream(const Fp4GemmArgs& a);
 // (Fp4MoeBigTileTakes), on the 128 x 128 tiles of gemm_mfma.hip otherwise.
 bool Fp4MoeBigTileTakes(const Fp4GemmArgs& a);
 St LaunchFp4MoeBigTile(const Fp4GemmArgs& a, uint32_t light_rows);
+// One dense FP4 problem with e4m3 activations on the 128 x 256 tiles (every
+// block exits at once when *skip_if holds skip_bit)
+bool Fp4DenseBigTileTakes(const Fp4GemmArgs& a);
+St LaunchFp4DenseBigTile(const Fp4GemmArgs& a, const uint32_t* skip_if, uint32_t skip_bit);
 
 // ------------------------------------------------------------- BF16 GEMM
 // C[m,n] = A[m,k] . W[n,k]^T, fp32 accumulate, bf16 or fp32 out.

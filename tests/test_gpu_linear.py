@@ -306,8 +306,12 @@ def _fp4_inputs(seed, m, n, k):
     return a, sa, packed, sw
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (33, 4096, 2048), (130, 2048, 4096)])
+@pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (33, 4096, 2048), (130, 2048, 4096), (300, 2048, 4096),
+                                   (256, 4096, 7168)])
 def test_fp4_gemm_deepseek_table(eng, m, n, k):
+    """M 1-130: the small-M kernel; M 300 (above 256 rows) and M 256 at
+    7168 -> 4096 (four 64-row chunks would stream 4 x 15.6 MB of weights):
+    the dense big tiles with the FP4 W operand."""
     import torch
 
     from pih_amd.device import ptr, stream_handle
@@ -325,6 +329,37 @@ def test_fp4_gemm_deepseek_table(eng, m, n, k):
     _sync()
     assert _flag(flag) == 0
     assert_close(oracle.bf16_bits_to_f32(to_host(out)), ref, f"fp4 gemm {m}x{n}x{k}")
+
+
+def test_fp4_gemm_big_tiles_nan_code(eng):
+    """The dense big-tile FP4 route (M 512) with an e4m3 NaN code in A: the
+    scan raises bit 1, the big tiles exit, and the checking 128 x 128 kernel
+    computes the result with the code as 0 (deepseek_fp4_gemm.cu decodes it
+    so)."""
+    import torch
+
+    from pih_amd.device import ptr, stream_handle
+
+    m, n, k = 512, 2048, 4096
+    a, sa, packed, sw = _fp4_inputs(synth.config_seed(5, 777), m, n, k)
+    a0 = a.copy()
+    a[200, 1000] = 0x7F
+    a0[200, 1000] = 0  # the code decodes as 0
+    out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ad, sad, pd, swd = to_dev(a), to_dev(sa), to_dev(packed), to_dev(sw)
+    r = abi.request(abi.DS["fp4_gemm"], activation_e4m3=ptr(ad), activation_scale_bits=ptr(sad),
+                    packed_weight=ptr(pd), weight_scale_bits=ptr(swd), output_bf16=ptr(out), error_flag=ptr(flag),
+                    stream=stream_handle(), m=m, n=n, k=k)
+    st = abi.deepseek_pack().call("launch_fp4_gemm", r)
+    assert st.code == abi.OK, st
+    _sync()
+    assert _flag(flag) == 1
+    rows = np.array([0, 199, 200, 201, m - 1])
+    ref = oracle.fp4_gemm(np.ascontiguousarray(a0[rows]), np.ascontiguousarray(sa[rows]), packed, sw)
+    got = oracle.bf16_bits_to_f32(to_host(out))
+    assert np.isfinite(got).all()
+    assert_close(got[rows], ref, "fp4 big tiles nan code")
 
 
 def _mx_moe_weights(experts, n, k, seed):
