@@ -220,22 +220,53 @@ class QwenMlpBlock:
     gate = x.Wg^T and up = x.Wu^T (GemmPlan, bf16 out;
     plugins/model-qwen3/qwen3_bf16_execution_schedule.cpp:34-37), then
     silu_mul (qwen3_cpu_oracle.cpp:114-126 semantics), then down = h.Wd^T.
-    Buffers are allocated at construction, so ``forward`` only enqueues."""
+    Buffers and the workspace are allocated at construction and the four
+    requests are built once per (input, stream), as a native host holds its
+    GemmPlans, so ``forward`` only enqueues."""
 
     def __init__(self, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, tokens: int):
         self.wg, self.wu, self.wd = w_gate, w_up, w_down
         inter, hidden = w_gate.shape
         dev = w_gate.device
+        self.tokens, self.inter, self.hidden = tokens, inter, hidden
         self.gate = torch.empty(tokens, inter, dtype=torch.bfloat16, device=dev)
         self.up = torch.empty(tokens, inter, dtype=torch.bfloat16, device=dev)
         self.h = torch.empty(tokens, inter, dtype=torch.bfloat16, device=dev)
         self.out = torch.empty(tokens, hidden, dtype=torch.bfloat16, device=dev)
+        self.ws_gu = bf16_gemm_workspace(tokens, inter, hidden)
+        self.ws_d = bf16_gemm_workspace(tokens, hidden, inter)
+        wsb = max(self.ws_gu, self.ws_d)
+        self.ws = torch.empty(wsb, dtype=torch.uint8, device=dev) if wsb else None
+        self._key = None
+        self._reqs = None
+
+    def _gemm(self, a, w, out, m, n, k, wsb, s):
+        return abi.request(abi.LN["bf16_gemm"], a_bf16=ptr(a), w_bf16=ptr(w), output=ptr(out),
+                           workspace=ptr(self.ws) if wsb else 0, workspace_bytes=wsb, stream=s, m=m, n=n, k=k,
+                           output_type=abi.OUTPUT_BF16)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        bf16_gemm(x, self.wg, out=self.gate)
-        bf16_gemm(x, self.wu, out=self.up)
-        silu_mul(self.gate, self.up, out=self.h)
-        return bf16_gemm(self.h, self.wd, out=self.out)
+        if x.shape != (self.tokens, self.hidden) or x.dtype != torch.bfloat16:
+            raise ValueError("Qwen MLP block input shape is invalid")
+        s = stream_handle()
+        key = (ptr(x), s)
+        if key != self._key:
+            t, i, h = self.tokens, self.inter, self.hidden
+            self._reqs = (
+                self._gemm(x, self.wg, self.gate, t, i, h, self.ws_gu, s),
+                self._gemm(x, self.wu, self.up, t, i, h, self.ws_gu, s),
+                abi.request(abi.LN["silu_mul"], gate_bf16=ptr(self.gate), up_bf16=ptr(self.up),
+                            output_bf16=ptr(self.h), stream=s, count=t * i),
+                self._gemm(self.h, self.wd, self.out, t, h, i, self.ws_d, s),
+            )
+            self._key = key
+        ln = _ln()
+        g, u, sm, d = self._reqs
+        _check(ln.call("launch_bf16_gemm", g), "bf16_gemm")
+        _check(ln.call("launch_bf16_gemm", u), "bf16_gemm")
+        _check(ln.call("launch_silu_mul", sm), "silu_mul")
+        _check(ln.call("launch_bf16_gemm", d), "bf16_gemm")
+        return self.out
 
 
 QWEN_VOCAB, QWEN_HIDDEN = 151936, 1024
