@@ -341,12 +341,13 @@ def bench_decode(torch, iters: int):
         out[f"w4a16_m{m}"] = _decode_line(ms, ms_graph, algo, nsets)
         out[f"w4a16_m{m}_grouped"] = _decode_line(ms_grp, ms_grp_graph, algo, nsets, launches=len(groups))
     del sets
-    # ---- BF16 decode, M = 1, 8, 64
+    # ---- BF16 decode, M = 1, 8, 64, and a 128-row batch (the big tiles with
+    # the K split into each projection's queried workspace)
     set_bytes = sum(n * k * 2 for _, n, k in QWEN8B)
     nsets = max(2, -(-600_000_000 // set_bytes))
     wsets = [[(torch.randn(n, k, device=dev, generator=gen) * 0.02).to(torch.bfloat16) for _, n, k in QWEN8B]
              for _ in range(nsets)]
-    for m in (1, 8, 64):
+    for m in (1, 8, 64, 128):
         xs = {k: torch.randn(m, k, device=dev, generator=gen).to(torch.bfloat16) for k in (4096, 12288)}
         ys = [torch.empty(m, n, dtype=torch.bfloat16, device=dev) for _, n, _ in QWEN8B]
         ws = [torch.zeros(max(1, query(abi.WORKSPACE_BF16_GEMM, m, n, k)), dtype=torch.uint8, device=dev)
@@ -556,7 +557,7 @@ def bench_dropin(torch, iters: int):
         wb, ws = n * k // 2, n * k // 32
         buf, stride, nsets = _rotation(torch, gen, wb + ws)
         buf.view(nsets, stride)[:, wb:wb + ws] = scales((nsets, ws), 118, 125)
-        for m in (8, 128):
+        for m in (8, 128, 512):
             a, sa = codes((m, k)), scales((m, k // 128), 118, 125)
             o = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
             reqs = [abi.request(abi.DS["fp4_gemm"], activation_e4m3=ptr(a), activation_scale_bits=ptr(sa),
@@ -573,7 +574,7 @@ def bench_dropin(torch, iters: int):
         buf, stride, nsets = _rotation(torch, gen, wb + ws)
         buf.view(nsets, stride)[:, wb:wb + ws] = scales((nsets, ws), 112, 118)
         buf.view(nsets, stride)[:, :wb] = codes((nsets, wb))
-        for m in (4, 2048):
+        for m in (4, 256, 2048):
             a, sa = codes((m, k)), scales((m, k // 128), 118, 124)
             o = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
             reqs = [abi.request(abi.DS["fp8_gemm"], activation_e4m3=ptr(a), activation_scale_bits=ptr(sa),
